@@ -1,0 +1,132 @@
+// tl_internal.h -- declarations shared by the HIP kernels (tl_kernels.hip) and
+// the C++ runtime (tl_runtime.hip).  Not part of the public C-ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tl {
+
+// Perfect pairwise-summation tree for a row width n: NumPy's float32 reduction
+// splits n in halves down to leaves of <= 128 elements, each leaf summed with
+// eight strided accumulators.  Widths supported on the device are those whose
+// halving chain stays on multiples of eight (2048 = 16 x 128, 5632 = 64 x 88).
+struct PwPlan {
+    int32_t leaf_len;   // elements per leaf, multiple of 8, <= 128
+    int32_t n_leaves;   // power of two
+};
+bool make_pw_plan(int32_t n, PwPlan* plan);
+
+// KV cache geometry.  One plane per (sequence, layer, kv head) holds max_pos
+// tokens of head_dim = 64 int8 values, laid out for coalesced reads:
+//   K plane: [max_pos/64 blocks][4 dim-groups of 16][64 tokens][16 bytes]
+//            so a wavefront whose lane t reads token t of a block issues four
+//            fully coalesced 1 KiB loads;
+//   V plane: [max_pos/16 groups][64 dims][16 tokens]
+//            so lane d reading dimension d of 16 consecutive tokens issues one
+//            fully coalesced 1 KiB load.
+constexpr int kHeadDim = 64;
+struct KvGeom {
+    int8_t* k;           // base of all K planes
+    int8_t* v;           // base of all V planes
+    int32_t n_layers;
+    int32_t n_kv_heads;
+    int32_t max_pos;
+    __host__ __device__ int64_t plane(int32_t seq, int32_t layer, int32_t g) const {
+        return (((int64_t)seq * n_layers + layer) * n_kv_heads + g) * (int64_t)max_pos * kHeadDim;
+    }
+    __host__ __device__ static int64_t k_off(int32_t t, int32_t d) {
+        return (int64_t)(t >> 6) * 4096 + (d >> 4) * 1024 + (t & 63) * 16 + (d & 15);
+    }
+    __host__ __device__ static int64_t v_off(int32_t t, int32_t d) {
+        return (int64_t)(t >> 4) * 1024 + d * 16 + (t & 15);
+    }
+};
+
+// Per-row description used by the row-parallel kernels (prefill rows of one
+// sequence, or one row per sequence in batched decode).
+struct RowMap {
+    const int32_t* seq;  // [rows] sequence (KV plane) of each row
+    const int32_t* pos;  // [rows] position of each row
+};
+
+enum GemvEpi : int {
+    EPI_DEQUANT = 0,      // y = f32(acc) * f32(sx * sw[n])
+    EPI_DEQUANT_RES = 1,  // y = residual + f32(acc) * f32(sx * sw[n])
+    EPI_REQUANT = 2,      // y8 = sat(rne(f32(acc) * m[n]))
+    EPI_GLU = 3,          // y = silu(gate) * up, both dequantized
+    EPI_ARGMAX = 4,       // argmax of dequantized logits into a 64-bit key
+    EPI_RAW = 5,          // acc only
+};
+
+struct GemvArgs {
+    const int8_t* w;         // [N][K]
+    const int8_t* w2;        // [N][K] up weights (EPI_GLU)
+    const float* ws;         // [N] weight scales or requant multipliers
+    const float* ws2;        // [N] up-weight scales (EPI_GLU)
+    const int8_t* x;         // [K] (row stride x_stride for multi-row)
+    const double* xs;        // [1] activation scale (per row)
+    const float* residual;   // [N]
+    float* y;                // [N]
+    int8_t* y8;              // [N] (EPI_REQUANT)
+    int32_t* acc;            // [N] optional raw accumulators
+    unsigned long long* key; // argmax slot (EPI_ARGMAX)
+    int32_t n, k;
+};
+
+struct GemmArgs {
+    const int8_t* a;          // [M][K]
+    const int8_t* w;          // [N][K]
+    const int8_t* w2;         // [N][K] up weights (GLU)
+    const double* as;         // [M] row scales
+    const float* ws;          // [N]
+    const float* ws2;         // [N]
+    const float* residual;    // [M][N]
+    float* y;                 // [M][N]
+    int32_t* acc;             // [M][N] raw (EPI_RAW) or [splits][M][N] partials
+    int32_t m, n, k;
+    int32_t k_split;          // K elements per split (multiple of 64)
+};
+
+// ---- launchers (tl_kernels.hip) ------------------------------------------
+hipError_t launch_rmsnorm_quant(hipStream_t s, const float* x, const float* g, int32_t rows,
+                                int32_t n, float eps, PwPlan plan, float* y, int8_t* q,
+                                double* scales);
+hipError_t launch_quantize_rows(hipStream_t s, const float* x, int32_t rows, int32_t n,
+                                int8_t* q, double* scales);
+hipError_t launch_quantize_tensor(hipStream_t s, const float* x, int64_t n, int8_t* q,
+                                  double* scale, float* scratch_max);
+hipError_t launch_quantize_weight_rows(hipStream_t s, const float* w, int32_t rows, int32_t n,
+                                       int8_t* q, float* scales);
+hipError_t launch_gemv(hipStream_t s, int epi, const GemvArgs& a);
+hipError_t launch_gemm(hipStream_t s, int epi, const GemmArgs& a, int32_t splits);
+hipError_t launch_gemm_reduce(hipStream_t s, int epi, const GemmArgs& a, int32_t splits);
+hipError_t launch_qkv_post(hipStream_t s, const float* qkv, int32_t rows, int32_t n_heads,
+                           int32_t n_kv_heads, RowMap rm, const float* cos, const float* sin,
+                           KvGeom kv, int32_t layer, const float* kv_sk, const float* kv_sv,
+                           int8_t* q8, double* q_scale, float* q_rot_out);
+hipError_t launch_attention(hipStream_t s, const int8_t* q8, const double* q_scale, int32_t rows,
+                            int32_t n_heads, int32_t n_kv_heads, RowMap rm, KvGeom kv,
+                            int32_t layer, const float* kv_sk, const float* kv_sv, float* out,
+                            int32_t max_t);
+hipError_t launch_rope(hipStream_t s, float* v, int32_t rows, int32_t n_heads, const int32_t* pos,
+                       const float* cos, const float* sin);
+hipError_t launch_softmax_rows(hipStream_t s, const float* x, int32_t rows, int32_t n, float* p);
+hipError_t launch_silu_mul(hipStream_t s, const float* g, const float* u, int64_t n, float* y);
+hipError_t launch_embed(hipStream_t s, const int32_t* tokens, int32_t rows, int32_t d, int32_t vocab,
+                        const int8_t* emb, const float* emb_s, float* x);
+hipError_t launch_reset_keys(hipStream_t s, unsigned long long* keys, int32_t n);
+hipError_t launch_finalize_tokens(hipStream_t s, unsigned long long* keys, int32_t rows,
+                                  int32_t* token_cur, int32_t* tokens_out, int32_t out_stride,
+                                  int32_t* n_gen, int32_t* cursor, float* best_logit, int32_t advance);
+hipError_t launch_argmax_rows(hipStream_t s, const float* logits, int32_t rows, int32_t n,
+                              unsigned long long* keys);
+hipError_t init_kernels();
+hipError_t launch_step_rows(hipStream_t s, const int32_t* seq_of_row, int32_t rows,
+                            const int32_t* cursor, int32_t* row_pos);
+hipError_t launch_kv_scatter(hipStream_t s, KvGeom kv, int32_t seq, int32_t layer, int32_t g,
+                             int32_t t0, int32_t n, const int8_t* k_rows, const int8_t* v_rows);
+hipError_t launch_kv_gather(hipStream_t s, KvGeom kv, int32_t seq, int32_t layer, int32_t g,
+                            int32_t t0, int32_t n, int8_t* k_rows, int8_t* v_rows);
+
+}  // namespace tl

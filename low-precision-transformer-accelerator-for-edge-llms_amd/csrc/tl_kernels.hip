@@ -1,0 +1,1108 @@
+// tl_kernels.hip -- hand-written HIP kernels for gfx950 (MI355X) implementing
+// the shared INT8 TinyLlama decoder path of the reference
+// (model/tinyllama_gemm_int8.py, rtl/compute/*.sv).
+//
+// Numerical contract (identical, operation by operation, to oracle/tl_oracle.c):
+//   * INT8 x INT8 -> INT32 contractions are exact (v_dot4 / v_mfma_i32_*_i8);
+//   * float32 arithmetic is never contracted into FMAs (built with
+//     -ffp-contract=off); divisions and square roots are correctly rounded;
+//   * every float reduction uses a fixed order: NumPy's pairwise tree for the
+//     RMSNorm sum of squares, a 64-wide xor butterfly per block of 64 keys
+//     followed by an in-order sum over blocks for the softmax denominator;
+//   * maxima, integer sums and the argmax key are order independent.
+// With these, results are bit-identical to the oracle.
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "tl_internal.h"
+
+namespace tl {
+
+#define TL_DEV __device__ __forceinline__
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// scalar helpers
+// ---------------------------------------------------------------------------
+
+// exp(x): Cody-Waite reduction x = k ln2 + r (ln2 = 355/512 + remainder),
+// degree-7 Taylor polynomial (1/n! in float32) in Horner form with explicit
+// fused multiply-adds, times 2^k from the exponent field.  x < -80 -> 0.
+TL_DEV float tl_expf(float x) {
+    if (!(x >= -80.0f)) return 0.0f;
+    if (x > 80.0f) x = 80.0f;
+    const float log2e = 0x1.715476p+0f;
+    const float c1 = 0x1.63p-1f;
+    const float c2 = -0x1.bd0106p-13f;
+    float kf = __builtin_rintf(x * log2e);
+    float r = __builtin_fmaf(-kf, c1, x);
+    r = __builtin_fmaf(-kf, c2, r);
+    float p = 0x1.a01a02p-13f;
+    p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+    p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    int k = (int)kf;
+    return p * __int_as_float((k + 127) << 23);
+}
+
+// SiLU, TL:159-161: x / (1 + exp(-clip(x, -60, 60)))
+TL_DEV float tl_silu(float x) {
+    float c = x < -60.0f ? -60.0f : (x > 60.0f ? 60.0f : x);
+    return __fdiv_rn(x, 1.0f + tl_expf(-c));
+}
+
+TL_DEV int8_t sat_i8(float v) {
+    v = v > 127.0f ? 127.0f : v;
+    v = v < -127.0f ? -127.0f : v;
+    return (int8_t)(int)v;
+}
+
+// GI:36-42 scale: max|x| / 127 in float64, 1.0 for an all-zero tensor
+TL_DEV double quant_scale(float mx) { return mx != 0.0f ? (double)mx / 127.0 : 1.0; }
+
+// GI:45-46 dequantization multiplier, formed in float64, rounded once
+TL_DEV float deq_mult(double sx, float sw) { return (float)(sx * (double)sw); }
+
+// 64-bit argmax key: order-preserving float bits above, (~index) below, so the
+// maximum key is the largest logit with the lowest index (B4 tie-break).
+TL_DEV unsigned long long argmax_key(float v, int32_t idx) {
+    if (v == 0.0f) v = 0.0f;  // -0 and +0 compare equal in np.argmax
+    unsigned u = __float_as_uint(v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - (unsigned)idx);
+}
+
+TL_DEV float key_logit(unsigned long long key) {
+    unsigned u = (unsigned)(key >> 32);
+    u = (u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u;
+    return __uint_as_float(u);
+}
+
+TL_DEV int32_t key_index(unsigned long long key) {
+    return (int32_t)(0xFFFFFFFFu - (unsigned)(key & 0xFFFFFFFFull));
+}
+
+TL_DEV int wave_sum_i32(int v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+TL_DEV float wave_max_f32(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    return v;
+}
+
+// the fixed 64-wide butterfly (same tree as or_block_sum64)
+TL_DEV float wave_butterfly_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off);
+    return v;
+}
+
+TL_DEV unsigned long long wave_max_u64(unsigned long long v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        unsigned lo = __shfl_xor((unsigned)(v & 0xFFFFFFFFull), off);
+        unsigned hi = __shfl_xor((unsigned)(v >> 32), off);
+        unsigned long long o = ((unsigned long long)hi << 32) | lo;
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+TL_DEV int sdot4x4(int4 a, int4 b, int acc) {
+    acc = __builtin_amdgcn_sdot4(a.x, b.x, acc, false);
+    acc = __builtin_amdgcn_sdot4(a.y, b.y, acc, false);
+    acc = __builtin_amdgcn_sdot4(a.z, b.z, acc, false);
+    acc = __builtin_amdgcn_sdot4(a.w, b.w, acc, false);
+    return acc;
+}
+
+// block-wide max of a non-negative float (all threads get the result)
+TL_DEV float block_max(float v, float* red /* >= 16 floats */) {
+    v = wave_max_f32(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float m = red[0];
+    for (int i = 1; i < nw; i++) m = fmaxf(m, red[i]);
+    return m;
+}
+
+// NumPy pairwise sum of sq[0 .. plan.leaf_len*plan.n_leaves) (a perfect
+// tree): 8 strided accumulators per leaf, ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7))
+// per leaf, then leaves combined pairwise level by level.  scr needs
+// 10 * n_leaves floats.  Returns the sum in every thread.
+TL_DEV float block_pairwise_sum(const float* sq, PwPlan plan, float* scr) {
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const int L = plan.n_leaves, len = plan.leaf_len;
+    float* part = scr;           // [8 L]
+    float* lv0 = scr + 8 * L;    // [L]
+    float* lv1 = lv0 + L;        // [L]
+    for (int idx = tid; idx < 8 * L; idx += nt) {
+        const float* a = sq + (idx >> 3) * len;
+        const int j = idx & 7;
+        float r = a[j];
+        for (int i = 8; i < len; i += 8) r = r + a[i + j];
+        part[idx] = r;
+    }
+    __syncthreads();
+    for (int leaf = tid; leaf < L; leaf += nt) {
+        const float* r = part + 8 * leaf;
+        lv0[leaf] = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+    }
+    __syncthreads();
+    float* cur = lv0;
+    float* nxt = lv1;
+    for (int w = L; w > 1; w >>= 1) {
+        for (int i = tid; i < (w >> 1); i += nt) nxt[i] = cur[2 * i] + cur[2 * i + 1];
+        __syncthreads();
+        float* t = cur; cur = nxt; nxt = t;
+    }
+    return cur[0];
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm + per-row INT8 quantization (TL:45-50, GI:36-42)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const float* __restrict__ x,
+                                                            const float* __restrict__ g, int32_t n,
+                                                            float eps, PwPlan plan,
+                                                            float* __restrict__ y,
+                                                            int8_t* __restrict__ q,
+                                                            double* __restrict__ scales) {
+    extern __shared__ float lds[];
+    float* xs = lds;
+    float* sq = lds + n;
+    float* scr = sq + n;
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const float* xr = x + (int64_t)row * n;
+    for (int i = tid; i < n; i += blockDim.x) {
+        float v = xr[i];
+        xs[i] = v;
+        sq[i] = v * v;
+    }
+    __syncthreads();
+    const float sum = block_pairwise_sum(sq, plan, scr);
+    const float var = __fdiv_rn(sum, (float)n);
+    const float inv = __fdiv_rn(1.0f, __builtin_sqrtf(var + eps));
+    float mx = 0.0f;
+    for (int i = tid; i < n; i += blockDim.x) {
+        float a = (xs[i] * inv) * g[i];
+        xs[i] = a;
+        mx = fmaxf(mx, fabsf(a));
+        if (y) y[(int64_t)row * n + i] = a;
+    }
+    mx = block_max(mx, scr);
+    const double s = quant_scale(mx);
+    const float sf = (float)s;
+    for (int i = tid; i < n; i += blockDim.x) q[(int64_t)row * n + i] = sat_i8(__builtin_rintf(__fdiv_rn(xs[i], sf)));
+    if (tid == 0) scales[row] = s;
+}
+
+// per-row quantize_int8 (GI:36-42); float scales variant is the offline
+// per-output-channel weight quantizer
+template <bool FLOAT_SCALE>
+__global__ __launch_bounds__(256) void quantize_rows_kernel(const float* __restrict__ x, int32_t n,
+                                                            int8_t* __restrict__ q, void* scales) {
+    __shared__ float red[16];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const float* xr = x + (int64_t)row * n;
+    float mx = 0.0f;
+    for (int i = tid; i < n; i += blockDim.x) mx = fmaxf(mx, fabsf(xr[i]));
+    mx = block_max(mx, red);
+    const double s = quant_scale(mx);
+    const float sf = (float)s;
+    for (int i = tid; i < n; i += blockDim.x) q[(int64_t)row * n + i] = sat_i8(__builtin_rintf(__fdiv_rn(xr[i], sf)));
+    if (tid == 0) {
+        if (FLOAT_SCALE) ((float*)scales)[row] = sf;
+        else ((double*)scales)[row] = s;
+    }
+}
+
+// per-tensor quantize_int8 over n elements (two passes: global max, then quantize)
+__global__ __launch_bounds__(256) void tensor_absmax_kernel(const float* __restrict__ x, int64_t n,
+                                                            unsigned* __restrict__ mx_bits) {
+    __shared__ float red[16];
+    float mx = 0.0f;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        mx = fmaxf(mx, fabsf(x[i]));
+    mx = block_max(mx, red);
+    if (threadIdx.x == 0) atomicMax(mx_bits, __float_as_uint(mx));  // |x| >= 0: bit order = value order
+}
+
+__global__ __launch_bounds__(256) void tensor_quant_kernel(const float* __restrict__ x, int64_t n,
+                                                           const unsigned* __restrict__ mx_bits,
+                                                           int8_t* __restrict__ q, double* __restrict__ scale) {
+    const double s = quant_scale(__uint_as_float(*mx_bits));
+    const float sf = (float)s;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        q[i] = sat_i8(__builtin_rintf(__fdiv_rn(x[i], sf)));
+    if (blockIdx.x == 0 && threadIdx.x == 0) *scale = s;
+}
+
+__global__ void fill_u32_kernel(unsigned* p, int32_t n, unsigned v) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+// ---------------------------------------------------------------------------
+// Decode GEMV (M = 1): y[n] = epilogue(sum_k x[k] * W[n][k])
+// Each wavefront owns R consecutive output rows; lane l streams bytes
+// [1024 c + 16 l, +16) of every row (128-bit loads, one coalesced KiB per
+// wavefront instruction) and all weight loads are issued before any math.
+// The dot products run on v_dot4_i32_i8 and each row sum is a wavefront
+// reduction (exact integer arithmetic).
+// ---------------------------------------------------------------------------
+template <int R, int KCH, int EPI>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+    constexpr int NM = (EPI == EPI_GLU) ? 2 : 1;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row0 = (blockIdx.x * 4 + wave) * R;
+    const int4 zero = make_int4(0, 0, 0, 0);
+
+    int4 wv[NM][R][KCH];
+#pragma unroll
+    for (int m = 0; m < NM; m++) {
+        const int8_t* wb = m ? a.w2 : a.w;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int n = min(row0 + r, a.n - 1);
+            const int8_t* wr = wb + (int64_t)n * a.k;
+#pragma unroll
+            for (int c = 0; c < KCH; c++) {
+                const int off = c * 1024 + lane * 16;
+                wv[m][r][c] = off < a.k ? *(const int4*)(wr + off) : zero;
+            }
+        }
+    }
+    int4 xv[KCH];
+#pragma unroll
+    for (int c = 0; c < KCH; c++) {
+        const int off = c * 1024 + lane * 16;
+        xv[c] = off < a.k ? *(const int4*)(a.x + off) : zero;
+    }
+    int acc[NM][R];
+#pragma unroll
+    for (int m = 0; m < NM; m++)
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            int s = 0;
+#pragma unroll
+            for (int c = 0; c < KCH; c++) s = sdot4x4(wv[m][r][c], xv[c], s);
+            acc[m][r] = wave_sum_i32(s);
+        }
+
+    if (EPI == EPI_ARGMAX) {
+        __shared__ unsigned long long wbest[4];
+        unsigned long long best = 0;
+        const double sx = a.xs[0];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int n = row0 + r;
+            if (n < a.n) {
+                const float logit = (float)acc[0][r] * deq_mult(sx, a.ws[n]);
+                if (a.y && lane == 0) a.y[n] = logit;
+                const unsigned long long k = argmax_key(logit, n);
+                best = k > best ? k : best;
+            }
+        }
+        if (lane == 0) wbest[wave] = best;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            unsigned long long b = wbest[0];
+            for (int i = 1; i < 4; i++) b = wbest[i] > b ? wbest[i] : b;
+            if (b) atomicMax(a.key, b);
+        }
+        return;
+    }
+
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int n = row0 + r;
+        if (lane != r || n >= a.n) continue;
+        if (a.acc) a.acc[n] = acc[0][r];
+        if (EPI == EPI_REQUANT) {
+            if (a.y8) a.y8[n] = sat_i8(__builtin_rintf((float)acc[0][r] * a.ws[n]));
+        } else if (EPI == EPI_DEQUANT || EPI == EPI_DEQUANT_RES) {
+            float v = (float)acc[0][r] * deq_mult(a.xs[0], a.ws[n]);
+            if (EPI == EPI_DEQUANT_RES) v = a.residual[n] + v;
+            a.y[n] = v;
+        } else if (EPI == EPI_GLU) {
+            const double sx = a.xs[0];
+            const float gt = (float)acc[0][r] * deq_mult(sx, a.ws[n]);
+            const float up = (float)acc[NM - 1][r] * deq_mult(sx, a.ws2[n]);
+            a.y[n] = tl_silu(gt) * up;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// INT8 MFMA GEMM (M > 1): C[M][N] = A[M][K] . W[N][K]^T with
+// v_mfma_i32_16x16x64_i8.  Workgroup of 4 wavefronts in a 2 x 2 grid; each
+// wavefront owns a (16 WTM) x (16 WTN) output tile; K advances 64 per step
+// through double-buffered LDS tiles (one 128-bit global load per thread per
+// operand tile, stored with an xor swizzle so the 128-bit fragment reads are
+// bank-conflict free).  Split-K writes exact int32 partials; otherwise the
+// dequantization (+ residual or SiLU-GLU) epilogue is fused.
+// ---------------------------------------------------------------------------
+TL_DEV int swz(int row, int kc) { return row * 4 + (kc ^ ((row >> 2) & 3)); }
+
+template <int WTM, int WTN, int EPI>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
+    constexpr int BM = 32 * WTM, BN = 32 * WTN;
+    constexpr int NB = (EPI == EPI_GLU) ? 2 : 1;
+    constexpr int ACH = BM * 4, BCH = BN * 4;   // 16-byte chunks per operand tile
+    __shared__ int4 sa[2][ACH];
+    __shared__ int4 sb[2][NB][BCH];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int kb = blockIdx.z * a.k_split;
+    const int ke = min(a.k, kb + a.k_split);
+    const int nsteps = (ke - kb) >> 6;
+
+    // global -> register staging assignment
+    const bool a_on = tid < ACH;
+    const int a_row = tid >> 2, a_kc = tid & 3;
+    const int8_t* a_src = a.a + (int64_t)min(m0 + a_row, a.m - 1) * a.k + a_kc * 16;
+    const bool b_on = tid < BCH;
+    const int b_row = tid >> 2, b_kc = tid & 3;
+    const int8_t* b_src[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+        b_src[b] = (b ? a.w2 : a.w) + (int64_t)min(n0 + b_row, a.n - 1) * a.k + b_kc * 16;
+
+    int4 ra = make_int4(0, 0, 0, 0), rb[NB];
+    auto gload = [&](int kk) {
+        if (a_on) ra = *(const int4*)(a_src + kk);
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+            if (b_on) rb[b] = *(const int4*)(b_src[b] + kk);
+    };
+    auto lstore = [&](int buf) {
+        if (a_on) sa[buf][swz(a_row, a_kc)] = ra;
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+            if (b_on) sb[buf][b][swz(b_row, b_kc)] = rb[b];
+    };
+
+    v4i acc[NB][WTM][WTN];
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int i = 0; i < WTM; i++)
+#pragma unroll
+            for (int j = 0; j < WTN; j++) acc[b][i][j] = (v4i){0, 0, 0, 0};
+
+    if (nsteps > 0) {
+        gload(kb);
+        lstore(0);
+        __syncthreads();
+    }
+    const int fr = lane & 15, fk = lane >> 4;
+    for (int s = 0; s < nsteps; s++) {
+        const int buf = s & 1;
+        if (s + 1 < nsteps) gload(kb + (s + 1) * 64);
+        v4i af[WTM], bf[NB][WTN];
+#pragma unroll
+        for (int i = 0; i < WTM; i++) {
+            const int row = wm * 16 * WTM + i * 16 + fr;
+            int4 t = sa[buf][swz(row, fk)];
+            af[i] = (v4i){t.x, t.y, t.z, t.w};
+        }
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int j = 0; j < WTN; j++) {
+                const int col = wn * 16 * WTN + j * 16 + fr;
+                int4 t = sb[buf][b][swz(col, fk)];
+                bf[b][j] = (v4i){t.x, t.y, t.z, t.w};
+            }
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int i = 0; i < WTM; i++)
+#pragma unroll
+                for (int j = 0; j < WTN; j++)
+                    acc[b][i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[b][j], acc[b][i][j], 0, 0, 0);
+        if (s + 1 < nsteps) {
+            lstore(buf ^ 1);
+            __syncthreads();
+        }
+    }
+
+    // epilogue: lane holds C[(lane/16)*4 + e][lane%16] of each 16x16 tile
+    const bool partial = gridDim.z > 1 || EPI == EPI_RAW;
+#pragma unroll
+    for (int i = 0; i < WTM; i++)
+#pragma unroll
+        for (int j = 0; j < WTN; j++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int m = m0 + wm * 16 * WTM + i * 16 + (lane >> 4) * 4 + e;
+                const int n = n0 + wn * 16 * WTN + j * 16 + (lane & 15);
+                if (m >= a.m || n >= a.n) continue;
+                const int64_t idx = (int64_t)m * a.n + n;
+                if (partial) {
+                    const int64_t plane = (int64_t)a.m * a.n;
+#pragma unroll
+                    for (int b = 0; b < NB; b++)
+                        a.acc[(int64_t)(blockIdx.z * NB + b) * plane + idx] = acc[b][i][j][e];
+                    continue;
+                }
+                const double sx = a.as[m];
+                const float v0 = (float)acc[0][i][j][e] * deq_mult(sx, a.ws[n]);
+                if (EPI == EPI_GLU) {
+                    const float up = (float)acc[NB - 1][i][j][e] * deq_mult(sx, a.ws2[n]);
+                    a.y[idx] = tl_silu(v0) * up;
+                } else if (EPI == EPI_DEQUANT_RES) {
+                    a.y[idx] = a.residual[idx] + v0;
+                } else {
+                    a.y[idx] = v0;
+                }
+            }
+}
+
+// sum split-K partials (exact) and apply the epilogue
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmArgs a, int32_t splits) {
+    constexpr int NB = (EPI == EPI_GLU) ? 2 : 1;
+    const int64_t total = (int64_t)a.m * a.n;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        int s[NB];
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            int v = 0;
+            for (int z = 0; z < splits; z++) v += a.acc[(int64_t)(z * NB + b) * total + idx];
+            s[b] = v;
+        }
+        const int m = (int)(idx / a.n), n = (int)(idx % a.n);
+        if (EPI == EPI_RAW) {
+            a.acc[idx] = s[0];
+            continue;
+        }
+        const double sx = a.as[m];
+        const float v0 = (float)s[0] * deq_mult(sx, a.ws[n]);
+        if (EPI == EPI_GLU) {
+            const float up = (float)s[NB - 1] * deq_mult(sx, a.ws2[n]);
+            a.y[idx] = tl_silu(v0) * up;
+        } else if (EPI == EPI_DEQUANT_RES) {
+            a.y[idx] = a.residual[idx] + v0;
+        } else {
+            a.y[idx] = v0;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Q/K/V post-processing per row (GI:150-156, design_decisions A7/B2):
+// RoPE on Q and K (TL:69-80), Q quantized at the row's own scale, K (post
+// RoPE) and V quantized at the static per-layer/per-KV-head scales and
+// appended to the KV cache at the row's position.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void qkv_post_kernel(const float* __restrict__ qkv, int32_t n_heads,
+                                                       int32_t n_kv, RowMap rm,
+                                                       const float* __restrict__ cosb,
+                                                       const float* __restrict__ sinb, KvGeom kv,
+                                                       int32_t layer, const float* __restrict__ kv_sk,
+                                                       const float* __restrict__ kv_sv,
+                                                       int8_t* __restrict__ q8,
+                                                       double* __restrict__ q_scale,
+                                                       float* __restrict__ q_rot_out) {
+    extern __shared__ float lds[];
+    __shared__ float red[16];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const int D = n_heads * kHeadDim, KVD = n_kv * kHeadDim, W = D + 2 * KVD;
+    float* v = lds;          // [W] inputs
+    float* o = lds + W;      // [D + KVD] rotated q, k
+    const float* src = qkv + (int64_t)row * W;
+    for (int i = tid; i < W; i += blockDim.x) v[i] = src[i];
+    __syncthreads();
+    const int pos = rm.pos[row], seq = rm.seq[row];
+    const float* cp = cosb + (int64_t)pos * kHeadDim;
+    const float* sp = sinb + (int64_t)pos * kHeadDim;
+    float mx = 0.0f;
+    for (int i = tid; i < D + KVD; i += blockDim.x) {
+        const int d = i & 63;
+        const float rot = d < 32 ? -v[i + 32] : v[i - 32];
+        const float r = (v[i] * cp[d]) + (rot * sp[d]);
+        o[i] = r;
+        if (i < D) mx = fmaxf(mx, fabsf(r));
+    }
+    mx = block_max(mx, red);  // includes the barrier that publishes o[]
+    const double s = quant_scale(mx);
+    const float sf = (float)s;
+    for (int i = tid; i < D; i += blockDim.x) {
+        q8[(int64_t)row * D + i] = sat_i8(__builtin_rintf(__fdiv_rn(o[i], sf)));
+        if (q_rot_out) q_rot_out[(int64_t)row * D + i] = o[i];
+    }
+    if (tid == 0) q_scale[row] = s;
+    for (int i = tid; i < KVD; i += blockDim.x) {
+        const int g = i >> 6, d = i & 63;
+        const int64_t pl = kv.plane(seq, layer, g);
+        kv.k[pl + KvGeom::k_off(pos, d)] = sat_i8(__builtin_rintf(__fdiv_rn(o[D + i], kv_sk[layer * n_kv + g])));
+        kv.v[pl + KvGeom::v_off(pos, d)] = sat_i8(__builtin_rintf(__fdiv_rn(v[D + KVD + i], kv_sv[layer * n_kv + g])));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// GQA attention over the INT8 KV cache, one workgroup per (row, KV head)
+// covering the G = n_heads / n_kv query heads that share the KV head
+// (gqa_router.sv:29).  For query position pos, keys 0..pos:
+//   S = q8 . k8 (INT32, v_dot4), s = f32(S) * f32((s_q s_k) attn_scale)
+//   softmax with the block-64 butterfly denominator, p8 = rne(127 p)
+//   O = p8 . v8 (INT32), out = f32(O) * f32((1/127) s_v)
+// ---------------------------------------------------------------------------
+constexpr int kMaxGroup = 8;
+
+__global__ __launch_bounds__(256) void attention_kernel(const int8_t* __restrict__ q8,
+                                                        const double* __restrict__ q_scale,
+                                                        int32_t n_heads, int32_t n_kv, RowMap rm,
+                                                        KvGeom kv, int32_t layer,
+                                                        const float* __restrict__ kv_sk,
+                                                        const float* __restrict__ kv_sv,
+                                                        double attn_scale, float* __restrict__ out) {
+    extern __shared__ float s_buf[];            // [G][tpad] scores then exps
+    __shared__ int4 qs[kMaxGroup][4];           // q8 of the group's heads
+    __shared__ float wmax[4][kMaxGroup];
+    __shared__ float mrow[kMaxGroup], tot[kMaxGroup], scl[kMaxGroup];
+    __shared__ int accs[4][kMaxGroup][64];
+
+    const int g = blockIdx.x, row = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int G = n_heads / n_kv;
+    const int pos = rm.pos[row], seq = rm.seq[row];
+    const int T = pos + 1;
+    const int tpad = (T + 63) & ~63;
+    const int nblk = tpad >> 6;
+    int8_t* p8 = (int8_t*)(s_buf + G * tpad);   // [G][tpad]
+    float* bsum = (float*)(p8 + G * tpad);       // [G][nblk]
+
+    const int D = n_heads * kHeadDim;
+    const int8_t* qrow = q8 + (int64_t)row * D + (int64_t)g * G * kHeadDim;
+    if (tid < G * 4) qs[tid >> 2][tid & 3] = ((const int4*)qrow)[tid];
+    if (tid < G) {
+        const float sk = kv_sk[layer * n_kv + g];
+        scl[tid] = (float)((q_scale[row] * (double)sk) * attn_scale);
+    }
+    __syncthreads();
+
+    const int64_t pl = kv.plane(seq, layer, g);
+    const int8_t* kp = kv.k + pl;
+    const int8_t* vp = kv.v + pl;
+
+    // scores: lane <-> key within a block of 64
+    float lmax[kMaxGroup];
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; h++) lmax[h] = -INFINITY;
+    for (int b = wave; b < nblk; b += 4) {
+        const int t = b * 64 + lane;
+        if (t < T) {
+            const int8_t* kb = kp + (int64_t)b * 4096 + lane * 16;
+            const int4 k0 = *(const int4*)(kb);
+            const int4 k1 = *(const int4*)(kb + 1024);
+            const int4 k2 = *(const int4*)(kb + 2048);
+            const int4 k3 = *(const int4*)(kb + 3072);
+#pragma unroll
+            for (int h = 0; h < kMaxGroup; h++) {
+                if (h < G) {
+                    int S = sdot4x4(k0, qs[h][0], 0);
+                    S = sdot4x4(k1, qs[h][1], S);
+                    S = sdot4x4(k2, qs[h][2], S);
+                    S = sdot4x4(k3, qs[h][3], S);
+                    const float sv = (float)S * scl[h];
+                    s_buf[h * tpad + t] = sv;
+                    lmax[h] = fmaxf(lmax[h], sv);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; h++) {
+        if (h < G) {
+            const float m = wave_max_f32(lmax[h]);
+            if (lane == 0) wmax[wave][h] = m;
+        }
+    }
+    __syncthreads();
+    if (tid < G) {
+        float m = wmax[0][tid];
+        for (int w = 1; w < 4; w++) m = fmaxf(m, wmax[w][tid]);
+        mrow[tid] = m;
+    }
+    __syncthreads();
+
+    // exponentials and per-block butterfly sums
+    for (int b = wave; b < nblk; b += 4) {
+        const int t = b * 64 + lane;
+#pragma unroll
+        for (int h = 0; h < kMaxGroup; h++) {
+            if (h < G) {
+                float e = 0.0f;
+                if (t < T) {
+                    e = tl_expf(s_buf[h * tpad + t] - mrow[h]);
+                    s_buf[h * tpad + t] = e;
+                }
+                const float bs = wave_butterfly_sum(e);
+                if (lane == 0) bsum[h * nblk + b] = bs;
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < G) {
+        float total = 0.0f;
+        for (int b = 0; b < nblk; b++) total = total + bsum[tid * nblk + b];
+        tot[tid] = total;
+    }
+    __syncthreads();
+
+    // INT8 probabilities (EX:870-873), zero beyond the last key
+    for (int t = tid; t < tpad; t += blockDim.x) {
+        for (int h = 0; h < G; h++) {
+            int8_t pq = 0;
+            if (t < T) {
+                float pr = __builtin_rintf(__fdiv_rn(s_buf[h * tpad + t], tot[h]) * 127.0f);
+                pr = pr < 0.0f ? 0.0f : (pr > 127.0f ? 127.0f : pr);
+                pq = (int8_t)(int)pr;
+            }
+            p8[h * tpad + t] = pq;
+        }
+    }
+    __syncthreads();
+
+    // O = P8 . V8: lane d reads dimension d of 16 consecutive keys (one
+    // coalesced 1 KiB load per wavefront) and dots it with each head's 16
+    // probabilities
+    int o[kMaxGroup];
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; h++) o[h] = 0;
+    const int ngrp = tpad >> 4;
+    for (int c = wave; c < ngrp; c += 4) {
+        const int4 vv = *(const int4*)(vp + (int64_t)c * 1024 + lane * 16);
+#pragma unroll
+        for (int h = 0; h < kMaxGroup; h++)
+            if (h < G) o[h] = sdot4x4(vv, *(const int4*)(p8 + h * tpad + c * 16), o[h]);
+    }
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; h++)
+        if (h < G) accs[wave][h][lane] = o[h];
+    __syncthreads();
+    const float pv_mult = deq_mult(1.0 / 127.0, kv_sv[layer * n_kv + g]);
+    for (int i = tid; i < G * 64; i += blockDim.x) {
+        const int h = i >> 6, d = i & 63;
+        const int O = accs[0][h][d] + accs[1][h][d] + accs[2][h][d] + accs[3][h][d];
+        out[(int64_t)row * D + (int64_t)(g * G + h) * kHeadDim + d] = (float)O * pv_mult;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// standalone element-wise ops (operator surface of TL)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ v, int32_t n_heads,
+                                                   const int32_t* __restrict__ pos,
+                                                   const float* __restrict__ cosb,
+                                                   const float* __restrict__ sinb) {
+    extern __shared__ float lds[];
+    const int row = blockIdx.x, n = n_heads * kHeadDim;
+    float* r = v + (int64_t)row * n;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) lds[i] = r[i];
+    __syncthreads();
+    const float* cp = cosb + (int64_t)pos[row] * kHeadDim;
+    const float* sp = sinb + (int64_t)pos[row] * kHeadDim;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const int d = i & 63;
+        const float rot = d < 32 ? -lds[i + 32] : lds[i - 32];
+        r[i] = (lds[i] * cp[d]) + (rot * sp[d]);
+    }
+}
+
+// softmax of each row with the block-64 butterfly denominator
+__global__ __launch_bounds__(256) void softmax_rows_kernel(const float* __restrict__ x, int32_t n,
+                                                           float* __restrict__ p) {
+    extern __shared__ float bs[];
+    __shared__ float red[16];
+    __shared__ float mtot[2];
+    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float* xr = x + (int64_t)row * n;
+    float* pr = p + (int64_t)row * n;
+    float mx = -INFINITY;
+    for (int i = tid; i < n; i += blockDim.x) mx = fmaxf(mx, xr[i]);
+    mx = wave_max_f32(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    if (tid == 0) {
+        float m = red[0];
+        for (int w = 1; w < (int)(blockDim.x >> 6); w++) m = fmaxf(m, red[w]);
+        mtot[0] = m;
+    }
+    __syncthreads();
+    const float m = mtot[0];
+    const int nblk = (n + 63) >> 6;
+    for (int b = wave; b < nblk; b += blockDim.x >> 6) {
+        const int t = b * 64 + lane;
+        float e = 0.0f;
+        if (t < n) {
+            e = tl_expf(xr[t] - m);
+            pr[t] = e;
+        }
+        const float s = wave_butterfly_sum(e);
+        if (lane == 0) bs[b] = s;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float total = 0.0f;
+        for (int b = 0; b < nblk; b++) total = total + bs[b];
+        mtot[1] = total;
+    }
+    __syncthreads();
+    const float total = mtot[1];
+    for (int i = tid; i < n; i += blockDim.x) pr[i] = __fdiv_rn(pr[i], total);
+}
+
+__global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__ g,
+                                                       const float* __restrict__ u, int64_t n,
+                                                       float* __restrict__ y) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        y[i] = u ? tl_silu(g[i]) * u[i] : tl_silu(g[i]);
+}
+
+// embedding row of the INT8 table: x = f32(e8[tok]) * s_e[tok]
+// (an id outside [0, vocab) yields a zero row instead of an out-of-bounds read)
+__global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ tokens, int32_t d,
+                                                    int32_t vocab, const int8_t* __restrict__ emb,
+                                                    const float* __restrict__ emb_s,
+                                                    float* __restrict__ x) {
+    const int row = blockIdx.x;
+    const int tok = tokens[row];
+    if (tok < 0 || tok >= vocab) {
+        for (int i = threadIdx.x; i < d; i += blockDim.x) x[(int64_t)row * d + i] = 0.0f;
+        return;
+    }
+    const int8_t* e = emb + (int64_t)tok * d;
+    const float s = emb_s[tok];
+    for (int i = threadIdx.x; i < d; i += blockDim.x) x[(int64_t)row * d + i] = (float)e[i] * s;
+}
+
+__global__ void reset_keys_kernel(unsigned long long* keys, int32_t n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) keys[i] = 0ull;
+}
+
+// after the LM head: decode each row's argmax key into the current token,
+// append it to the row's output list, advance the cursor, clear the key
+__global__ void finalize_tokens_kernel(unsigned long long* keys, int32_t rows, int32_t* token_cur,
+                                       int32_t* tokens_out, int32_t out_stride, int32_t* n_gen,
+                                       int32_t* cursor, float* best_logit, int32_t advance) {
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= rows) return;
+    const unsigned long long k = keys[r];
+    const int32_t tok = key_index(k);
+    token_cur[r] = tok;
+    const int32_t i = n_gen[r];
+    if (i >= 0 && i < out_stride) {
+        if (tokens_out) tokens_out[(int64_t)r * out_stride + i] = tok;
+        if (best_logit) best_logit[(int64_t)r * out_stride + i] = key_logit(k);
+    }
+    n_gen[r] = i + 1;
+    cursor[r] = cursor[r] + advance;
+    keys[r] = 0ull;
+}
+
+// argmax of each logits row (one workgroup per row) into its key slot
+__global__ __launch_bounds__(256) void argmax_rows_kernel(const float* __restrict__ logits, int32_t n,
+                                                          unsigned long long* __restrict__ keys) {
+    __shared__ unsigned long long wbest[4];
+    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float* lr = logits + (int64_t)row * n;
+    unsigned long long best = 0;
+    for (int i = tid; i < n; i += blockDim.x) {
+        const unsigned long long k = argmax_key(lr[i], i);
+        best = k > best ? k : best;
+    }
+    best = wave_max_u64(best);
+    if (lane == 0) wbest[wave] = best;
+    __syncthreads();
+    if (tid == 0) {
+        unsigned long long b = wbest[0];
+        for (int i = 1; i < 4; i++) b = wbest[i] > b ? wbest[i] : b;
+        keys[row] = b;
+    }
+}
+
+// batched decode: the position of each row is its sequence's cursor
+__global__ void step_rows_kernel(const int32_t* seq_of_row, int32_t rows, const int32_t* cursor,
+                                 int32_t* row_pos) {
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r < rows) row_pos[r] = cursor[seq_of_row[r]];
+}
+
+// logical [n][64] rows <-> cache plane layout
+__global__ void kv_scatter_kernel(KvGeom kv, int64_t pl, int32_t t0, int32_t n,
+                                  const int8_t* __restrict__ k_rows, const int8_t* __restrict__ v_rows) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)n * kHeadDim) return;
+    const int t = t0 + (int)(i >> 6), d = (int)(i & 63);
+    if (k_rows) kv.k[pl + KvGeom::k_off(t, d)] = k_rows[i];
+    if (v_rows) kv.v[pl + KvGeom::v_off(t, d)] = v_rows[i];
+}
+
+__global__ void kv_gather_kernel(KvGeom kv, int64_t pl, int32_t t0, int32_t n,
+                                 int8_t* __restrict__ k_rows, int8_t* __restrict__ v_rows) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)n * kHeadDim) return;
+    const int t = t0 + (int)(i >> 6), d = (int)(i & 63);
+    if (k_rows) k_rows[i] = kv.k[pl + KvGeom::k_off(t, d)];
+    if (v_rows) v_rows[i] = kv.v[pl + KvGeom::v_off(t, d)];
+}
+
+// ---------------------------------------------------------------------------
+// host launchers
+// ---------------------------------------------------------------------------
+bool make_pw_plan(int32_t n, PwPlan* plan) {
+    if (n < 8) return false;
+    int32_t len = n, leaves = 1;
+    while (len > 128) {
+        if (len % 2 != 0 || (len / 2) % 8 != 0) return false;
+        len /= 2;
+        leaves *= 2;
+    }
+    if (len % 8 != 0) return false;
+    plan->leaf_len = len;
+    plan->n_leaves = leaves;
+    return true;
+}
+
+static inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+
+hipError_t launch_rmsnorm_quant(hipStream_t s, const float* x, const float* g, int32_t rows,
+                                int32_t n, float eps, PwPlan plan, float* y, int8_t* q,
+                                double* scales) {
+    if (rows <= 0) return hipSuccess;
+    const size_t lds = sizeof(float) * ((size_t)2 * n + 10 * (size_t)plan.n_leaves + 16);
+    hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3(rows), dim3(256), lds, s, x, g, n, eps, plan, y, q, scales);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_rows(hipStream_t s, const float* x, int32_t rows, int32_t n, int8_t* q,
+                                double* scales) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(quantize_rows_kernel<false>, dim3(rows), dim3(256), 0, s, x, n, q, (void*)scales);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_weight_rows(hipStream_t s, const float* w, int32_t rows, int32_t n,
+                                       int8_t* q, float* scales) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(quantize_rows_kernel<true>, dim3(rows), dim3(256), 0, s, w, n, q, (void*)scales);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_tensor(hipStream_t s, const float* x, int64_t n, int8_t* q,
+                                  double* scale, float* scratch_max) {
+    unsigned* mx = (unsigned*)scratch_max;
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, s, mx, 1, 0u);
+    const int blocks = (int)std::min<int64_t>(1024, std::max<int64_t>(1, (n + 255) / 256));
+    if (n > 0) hipLaunchKernelGGL(tensor_absmax_kernel, dim3(blocks), dim3(256), 0, s, x, n, mx);
+    hipLaunchKernelGGL(tensor_quant_kernel, dim3(blocks), dim3(256), 0, s, x, n, mx, q, scale);
+    return hipGetLastError();
+}
+
+template <int R, int EPI>
+static hipError_t gemv_r(hipStream_t s, const GemvArgs& a) {
+    const int kch = ceil_div(a.k, 1024);
+    const dim3 grid(ceil_div(a.n, 4 * R)), block(256);
+    switch (kch) {
+        case 1: hipLaunchKernelGGL((gemv_kernel<R, 1, EPI>), grid, block, 0, s, a); break;
+        case 2: hipLaunchKernelGGL((gemv_kernel<R, 2, EPI>), grid, block, 0, s, a); break;
+        case 3: hipLaunchKernelGGL((gemv_kernel<R, 3, EPI>), grid, block, 0, s, a); break;
+        case 4: hipLaunchKernelGGL((gemv_kernel<R, 4, EPI>), grid, block, 0, s, a); break;
+        case 5: hipLaunchKernelGGL((gemv_kernel<R, 5, EPI>), grid, block, 0, s, a); break;
+        case 6: hipLaunchKernelGGL((gemv_kernel<R, 6, EPI>), grid, block, 0, s, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <int EPI>
+static hipError_t gemv_epi(hipStream_t s, const GemvArgs& a) {
+    // rows per wavefront: enough workgroups to cover the chip, enough bytes in
+    // flight per lane
+    const int kch = ceil_div(a.k, 1024);
+    if (EPI == EPI_GLU || kch > 3) return gemv_r<2, EPI>(s, a);
+    if (a.n >= 8192) return gemv_r<4, EPI>(s, a);
+    return gemv_r<2, EPI>(s, a);
+}
+
+hipError_t launch_gemv(hipStream_t s, int epi, const GemvArgs& a) {
+    if (a.n <= 0) return hipSuccess;
+    if (a.k <= 0 || a.k % 16 != 0 || a.k > 6 * 1024) return hipErrorInvalidValue;
+    switch (epi) {
+        case EPI_DEQUANT: return gemv_epi<EPI_DEQUANT>(s, a);
+        case EPI_DEQUANT_RES: return gemv_epi<EPI_DEQUANT_RES>(s, a);
+        case EPI_REQUANT: return gemv_epi<EPI_REQUANT>(s, a);
+        case EPI_GLU: return gemv_epi<EPI_GLU>(s, a);
+        case EPI_ARGMAX: return gemv_epi<EPI_ARGMAX>(s, a);
+        case EPI_RAW: return gemv_epi<EPI_REQUANT>(s, a);  // y8 unused when only acc wanted
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <int WTM, int WTN, int EPI>
+static void gemm_go(hipStream_t s, const GemmArgs& a, int32_t splits) {
+    constexpr int BM = 32 * WTM, BN = 32 * WTN;
+    const dim3 grid(ceil_div(a.n, BN), ceil_div(a.m, BM), splits);
+    hipLaunchKernelGGL((gemm_kernel<WTM, WTN, EPI>), grid, dim3(256), 0, s, a);
+}
+
+template <int EPI>
+static void gemm_shape(hipStream_t s, const GemmArgs& a, int32_t splits) {
+    if (a.m <= 32) gemm_go<1, 2, EPI>(s, a, splits);
+    else gemm_go<2, 2, EPI>(s, a, splits);
+}
+
+hipError_t launch_gemm(hipStream_t s, int epi, const GemmArgs& a, int32_t splits) {
+    if (a.m <= 0 || a.n <= 0) return hipSuccess;
+    if (a.k <= 0 || a.k % 64 != 0 || a.k_split % 64 != 0 || splits < 1) return hipErrorInvalidValue;
+    switch (epi) {
+        case EPI_DEQUANT: gemm_shape<EPI_DEQUANT>(s, a, splits); break;
+        case EPI_DEQUANT_RES: gemm_shape<EPI_DEQUANT_RES>(s, a, splits); break;
+        case EPI_GLU: gemm_shape<EPI_GLU>(s, a, splits); break;
+        case EPI_RAW: gemm_shape<EPI_RAW>(s, a, splits); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_reduce(hipStream_t s, int epi, const GemmArgs& a, int32_t splits) {
+    const int blocks = (int)std::min<int64_t>(2048, ((int64_t)a.m * a.n + 255) / 256);
+    switch (epi) {
+        case EPI_DEQUANT: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_DEQUANT>, dim3(blocks), dim3(256), 0, s, a, splits); break;
+        case EPI_DEQUANT_RES: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_DEQUANT_RES>, dim3(blocks), dim3(256), 0, s, a, splits); break;
+        case EPI_GLU: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_GLU>, dim3(blocks), dim3(256), 0, s, a, splits); break;
+        case EPI_RAW: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_RAW>, dim3(blocks), dim3(256), 0, s, a, splits); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_qkv_post(hipStream_t s, const float* qkv, int32_t rows, int32_t n_heads,
+                           int32_t n_kv_heads, RowMap rm, const float* cos, const float* sin,
+                           KvGeom kv, int32_t layer, const float* kv_sk, const float* kv_sv,
+                           int8_t* q8, double* q_scale, float* q_rot_out) {
+    if (rows <= 0) return hipSuccess;
+    const int D = n_heads * kHeadDim, KVD = n_kv_heads * kHeadDim;
+    const size_t lds = sizeof(float) * ((size_t)(D + 2 * KVD) + D + KVD);
+    hipLaunchKernelGGL(qkv_post_kernel, dim3(rows), dim3(256), lds, s, qkv, n_heads, n_kv_heads, rm,
+                       cos, sin, kv, layer, kv_sk, kv_sv, q8, q_scale, q_rot_out);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention(hipStream_t s, const int8_t* q8, const double* q_scale, int32_t rows,
+                            int32_t n_heads, int32_t n_kv_heads, RowMap rm, KvGeom kv,
+                            int32_t layer, const float* kv_sk, const float* kv_sv, float* out,
+                            int32_t max_t) {
+    if (rows <= 0) return hipSuccess;
+    const int G = n_heads / n_kv_heads;
+    if (G < 1 || G > kMaxGroup || n_heads % n_kv_heads) return hipErrorInvalidValue;
+    const int tpad = (max_t + 63) & ~63;
+    const size_t lds = (size_t)G * tpad * sizeof(float) + (size_t)G * tpad + (size_t)G * (tpad / 64) * sizeof(float) + 16;
+    const double attn_scale = 1.0 / sqrt((double)kHeadDim);
+    hipLaunchKernelGGL(attention_kernel, dim3(n_kv_heads, rows), dim3(256), lds, s, q8, q_scale, n_heads,
+                       n_kv_heads, rm, kv, layer, kv_sk, kv_sv, attn_scale, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope(hipStream_t s, float* v, int32_t rows, int32_t n_heads, const int32_t* pos,
+                       const float* cos, const float* sin) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(rope_kernel, dim3(rows), dim3(256), sizeof(float) * n_heads * kHeadDim, s, v,
+                       n_heads, pos, cos, sin);
+    return hipGetLastError();
+}
+
+hipError_t launch_softmax_rows(hipStream_t s, const float* x, int32_t rows, int32_t n, float* p) {
+    if (rows <= 0 || n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(softmax_rows_kernel, dim3(rows), dim3(256), sizeof(float) * ((n + 63) / 64), s, x, n, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_silu_mul(hipStream_t s, const float* g, const float* u, int64_t n, float* y) {
+    if (n <= 0) return hipSuccess;
+    const int blocks = (int)std::min<int64_t>(4096, (n + 255) / 256);
+    hipLaunchKernelGGL(silu_mul_kernel, dim3(blocks), dim3(256), 0, s, g, u, n, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed(hipStream_t s, const int32_t* tokens, int32_t rows, int32_t d, int32_t vocab,
+                        const int8_t* emb, const float* emb_s, float* x) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(embed_kernel, dim3(rows), dim3(256), 0, s, tokens, d, vocab, emb, emb_s, x);
+    return hipGetLastError();
+}
+
+hipError_t launch_reset_keys(hipStream_t s, unsigned long long* keys, int32_t n) {
+    hipLaunchKernelGGL(reset_keys_kernel, dim3(ceil_div(n, 64)), dim3(64), 0, s, keys, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_finalize_tokens(hipStream_t s, unsigned long long* keys, int32_t rows,
+                                  int32_t* token_cur, int32_t* tokens_out, int32_t out_stride,
+                                  int32_t* n_gen, int32_t* cursor, float* best_logit, int32_t advance) {
+    hipLaunchKernelGGL(finalize_tokens_kernel, dim3(ceil_div(rows, 64)), dim3(64), 0, s, keys, rows,
+                       token_cur, tokens_out, out_stride, n_gen, cursor, best_logit, advance);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax_rows(hipStream_t s, const float* logits, int32_t rows, int32_t n,
+                              unsigned long long* keys) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(argmax_rows_kernel, dim3(rows), dim3(256), 0, s, logits, n, keys);
+    return hipGetLastError();
+}
+
+hipError_t init_kernels() {
+    // the attention kernel keeps scores and INT8 probabilities of up to 2048
+    // keys x 8 heads in LDS (gfx950: 160 KiB per workgroup)
+    return hipFuncSetAttribute((const void*)attention_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               150 * 1024);
+}
+
+hipError_t launch_step_rows(hipStream_t s, const int32_t* seq_of_row, int32_t rows,
+                            const int32_t* cursor, int32_t* row_pos) {
+    hipLaunchKernelGGL(step_rows_kernel, dim3(ceil_div(rows, 64)), dim3(64), 0, s, seq_of_row, rows,
+                       cursor, row_pos);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_scatter(hipStream_t s, KvGeom kv, int32_t seq, int32_t layer, int32_t g,
+                             int32_t t0, int32_t n, const int8_t* k_rows, const int8_t* v_rows) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(kv_scatter_kernel, dim3(ceil_div((int64_t)n * kHeadDim, 256)), dim3(256), 0, s,
+                       kv, kv.plane(seq, layer, g), t0, n, k_rows, v_rows);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_gather(hipStream_t s, KvGeom kv, int32_t seq, int32_t layer, int32_t g,
+                            int32_t t0, int32_t n, int8_t* k_rows, int8_t* v_rows) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(kv_gather_kernel, dim3(ceil_div((int64_t)n * kHeadDim, 256)), dim3(256), 0, s,
+                       kv, kv.plane(seq, layer, g), t0, n, k_rows, v_rows);
+    return hipGetLastError();
+}
+
+}  // namespace tl

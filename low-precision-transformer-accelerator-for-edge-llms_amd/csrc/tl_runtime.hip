@@ -1,0 +1,988 @@
+// tl_runtime.hip -- C++ runtime behind the C-ABI of include/tl_int8.h.
+//
+// Owns the device copy of the quantized model, the INT8 KV cache, the
+// workspaces and one HIP stream per handle, and sequences the kernels of
+// tl_kernels.hip into the reference's decoder-layer / generation schedule
+// (model/tinyllama_gemm_int8.py:256-281, 437-467, 629-685;
+// rtl/control/layer_controller.sv block order).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "tl_int8.h"
+#include "tl_internal.h"
+
+using namespace tl;
+
+namespace {
+
+struct LayerDev {
+    int8_t* wqkv = nullptr;  // [D + 2 KVD][D]  q rows, then k rows, then v rows
+    float* sqkv = nullptr;
+    int8_t* wo = nullptr;
+    float* so = nullptr;
+    int8_t* wg = nullptr;
+    float* sg = nullptr;
+    int8_t* wu = nullptr;
+    float* su = nullptr;
+    int8_t* wd = nullptr;
+    float* sd = nullptr;
+    float* g_in = nullptr;
+    float* g_post = nullptr;
+};
+
+struct ProfEvent {
+    int kclass;
+    hipEvent_t start, stop;
+    double bytes;
+};
+
+thread_local std::string g_create_error;
+
+}  // namespace
+
+struct tl_handle {
+    tl_config cfg{};
+    int32_t max_seqs = 0;
+    int32_t max_rows = 0;
+    int device = 0;
+    hipStream_t stream = nullptr;
+    PwPlan plan{};
+    int32_t D = 0, F = 0, KVD = 0, QKV = 0;
+
+    std::vector<LayerDev> layers;
+    int8_t* lm_w = nullptr;
+    float* lm_s = nullptr;
+    float* g_final = nullptr;
+    int8_t* emb = nullptr;
+    float* emb_s = nullptr;
+    float* rope_cos = nullptr;
+    float* rope_sin = nullptr;
+    int32_t rope_n = 0;
+    float* kv_sk = nullptr;
+    float* kv_sv = nullptr;
+    KvGeom kv{};
+
+    // workspaces, [max_rows] rows each
+    float* x = nullptr;
+    float* qkv = nullptr;
+    int8_t* a8 = nullptr;
+    double* as = nullptr;
+    int8_t* q8 = nullptr;
+    double* qs = nullptr;
+    float* att = nullptr;
+    float* hid = nullptr;
+    float* logits = nullptr;      // [max_seqs][V]
+    int32_t* row_seq = nullptr;
+    int32_t* row_pos = nullptr;
+    int32_t* tokens = nullptr;    // [max_rows]
+    float* fscratch = nullptr;    // small scratch
+    unsigned long long* op_key = nullptr;  // argmax slot of the standalone LM-head operator
+    int32_t* partials = nullptr;
+    size_t partial_cap = 0;       // int32 elements
+
+    // per-sequence generation state
+    unsigned long long* keys = nullptr;
+    int32_t* token_cur = nullptr;
+    int32_t* cursor = nullptr;
+    int32_t* n_gen = nullptr;
+    int32_t* tokens_out = nullptr;   // [max_seqs][max_pos]
+    float* logit_out = nullptr;      // [max_seqs][max_pos]
+    std::vector<int32_t> host_cursor;
+    std::vector<int32_t> host_ngen;
+
+    std::vector<void*> allocs;
+    std::string err;
+
+    bool profiling = false;
+    std::vector<ProfEvent> prof_pending;
+    std::vector<hipEvent_t> event_pool;
+    int64_t prof_count[TL_K_COUNT] = {};
+    double prof_ms[TL_K_COUNT] = {};
+    double prof_bytes[TL_K_COUNT] = {};
+};
+
+namespace {
+
+int fail(tl_handle* h, int32_t code, const std::string& msg) {
+    if (h) h->err = msg;
+    else g_create_error = msg;
+    return code;
+}
+
+#define TL_HIP(h, expr)                                                                     \
+    do {                                                                                    \
+        hipError_t e_ = (expr);                                                             \
+        if (e_ != hipSuccess)                                                               \
+            return fail((h), TL_ERR_INTERNAL, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+#define TL_REQ(h, cond, msg)                                               \
+    do {                                                                   \
+        if (!(cond)) return fail((h), TL_ERR_BAD_DESCRIPTOR, (msg));       \
+    } while (0)
+
+template <typename T>
+hipError_t dalloc(tl_handle* h, T** p, size_t count) {
+    void* q = nullptr;
+    hipError_t e = hipMalloc(&q, std::max<size_t>(count, 1) * sizeof(T));
+    if (e == hipSuccess) {
+        h->allocs.push_back(q);
+        *p = (T*)q;
+    }
+    return e;
+}
+
+hipEvent_t take_event(tl_handle* h) {
+    if (!h->event_pool.empty()) {
+        hipEvent_t e = h->event_pool.back();
+        h->event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+// optional per-kernel-class timing with events on the handle's stream
+struct Prof {
+    tl_handle* h;
+    int kc;
+    double bytes;
+    hipEvent_t a = nullptr;
+    Prof(tl_handle* hh, int k, double b) : h(hh), kc(k), bytes(b) {
+        if (h->profiling) {
+            a = take_event(h);
+            if (a) hipEventRecord(a, h->stream);
+        }
+    }
+    ~Prof() {
+        if (h->profiling && a) {
+            hipEvent_t b = take_event(h);
+            if (b) {
+                hipEventRecord(b, h->stream);
+                h->prof_pending.push_back({kc, a, b, bytes});
+            }
+        }
+    }
+};
+
+void harvest_profile(tl_handle* h) {
+    if (h->prof_pending.empty()) return;
+    hipStreamSynchronize(h->stream);
+    for (auto& p : h->prof_pending) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, p.start, p.stop) == hipSuccess) {
+            h->prof_count[p.kclass] += 1;
+            h->prof_ms[p.kclass] += ms;
+            h->prof_bytes[p.kclass] += p.bytes;
+        }
+        h->event_pool.push_back(p.start);
+        h->event_pool.push_back(p.stop);
+    }
+    h->prof_pending.clear();
+}
+
+hipError_t copy_in(tl_handle* h, void* dst, const void* src, size_t bytes, int32_t src_mem) {
+    return hipMemcpyAsync(dst, src, bytes, src_mem == TL_MEM_DEVICE ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                          h->stream);
+}
+
+// default RoPE table following TL:59-66 step by step in float32
+void default_rope(int32_t n_pos, float theta, std::vector<float>& c, std::vector<float>& s) {
+    float inv[kHeadDim / 2];
+    for (int i = 0; i < kHeadDim / 2; i++) {
+        const float e = (float)(2 * i) / (float)kHeadDim;
+        inv[i] = 1.0f / powf(theta, e);
+    }
+    c.resize((size_t)n_pos * kHeadDim);
+    s.resize((size_t)n_pos * kHeadDim);
+    for (int p = 0; p < n_pos; p++)
+        for (int d = 0; d < kHeadDim; d++) {
+            const float a = (float)p * inv[d % (kHeadDim / 2)];
+            c[(size_t)p * kHeadDim + d] = (float)cos((double)a);
+            s[(size_t)p * kHeadDim + d] = (float)sin((double)a);
+        }
+}
+
+int32_t check_launch(tl_handle* h, hipError_t e, const char* what) {
+    if (e != hipSuccess) return fail(h, TL_ERR_INTERNAL, std::string(what) + ": " + hipGetErrorString(e));
+    return TL_OK;
+}
+
+#define TL_LAUNCH(h, expr)                                   \
+    do {                                                     \
+        int32_t r_ = check_launch((h), (expr), #expr);       \
+        if (r_) return r_;                                   \
+    } while (0)
+
+int32_t finish(tl_handle* h) {
+    hipError_t e = hipStreamSynchronize(h->stream);
+    if (e != hipSuccess) return fail(h, TL_ERR_INTERNAL, std::string("stream: ") + hipGetErrorString(e));
+    if (h->profiling) harvest_profile(h);
+    return TL_OK;
+}
+
+// ---- GEMM dispatch: M == 1 uses the GEMV kernels, M > 1 the MFMA kernels ----
+int32_t ensure_partials(tl_handle* h, size_t need) {
+    if (need <= h->partial_cap) return TL_OK;
+    if (h->partials) {
+        hipFree(h->partials);
+        h->allocs.erase(std::remove(h->allocs.begin(), h->allocs.end(), (void*)h->partials), h->allocs.end());
+        h->partials = nullptr;
+    }
+    TL_HIP(h, dalloc(h, &h->partials, need));
+    h->partial_cap = need;
+    return TL_OK;
+}
+
+int32_t run_gemm(tl_handle* h, int epi, GemmArgs a, int kclass) {
+    const int nb = epi == EPI_GLU ? 2 : 1;
+    // split K when the output tiles alone cannot fill the 256 CUs
+    const int bm = a.m <= 32 ? 32 : 64;
+    const int64_t tiles = (int64_t)((a.m + bm - 1) / bm) * ((a.n + 63) / 64);
+    int splits = 1;
+    while (tiles * splits < 512 && a.k / (64 * splits * 2) >= 4 && splits < 16) splits *= 2;
+    if (epi == EPI_RAW) splits = 1;
+    a.k_split = ((a.k / 64 + splits - 1) / splits) * 64;
+    splits = (a.k + a.k_split - 1) / a.k_split;
+    if (splits > 1) {
+        int32_t r = ensure_partials(h, (size_t)splits * nb * a.m * a.n);
+        if (r) return r;
+        a.acc = h->partials;
+    }
+    const double bytes = (double)a.m * a.k + (double)nb * a.n * a.k + (double)a.m * a.n * 4.0;
+    Prof p(h, kclass, bytes);
+    TL_LAUNCH(h, launch_gemm(h->stream, epi, a, splits));
+    if (splits > 1) TL_LAUNCH(h, launch_gemm_reduce(h->stream, epi, a, splits));
+    return TL_OK;
+}
+
+int32_t linear(tl_handle* h, int epi, int rows, const int8_t* x8, const double* xs, const int8_t* w,
+               const float* ws, const int8_t* w2, const float* ws2, int32_t n, int32_t k,
+               const float* residual, float* y, int kclass) {
+    if (rows == 1) {
+        GemvArgs g{};
+        g.w = w; g.w2 = w2; g.ws = ws; g.ws2 = ws2; g.x = x8; g.xs = xs;
+        g.residual = residual; g.y = y; g.n = n; g.k = k;
+        const double bytes = (double)(w2 ? 2 : 1) * ((double)n * k + n * 4.0) + k + n * 4.0 + (residual ? n * 4.0 : 0.0);
+        Prof p(h, kclass, bytes);
+        TL_LAUNCH(h, launch_gemv(h->stream, epi, g));
+        return TL_OK;
+    }
+    GemmArgs a{};
+    a.a = x8; a.w = w; a.w2 = w2; a.as = xs; a.ws = ws; a.ws2 = ws2;
+    a.residual = residual; a.y = y; a.m = rows; a.n = n; a.k = k;
+    return run_gemm(h, epi, a, kclass == TL_K_LMHEAD ? TL_K_LMHEAD : TL_K_GEMM_PREFILL);
+}
+
+RowMap rowmap(tl_handle* h) { return RowMap{h->row_seq, h->row_pos}; }
+
+// one decoder layer (GI:256-281) for `rows` rows of h->x whose sequence and
+// position are in h->row_seq / h->row_pos; max_t bounds pos + 1 over the rows
+int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t) {
+    const tl_config& c = h->cfg;
+    const LayerDev& L = h->layers[layer];
+    const int D = h->D, F = h->F, KVD = h->KVD, QKV = h->QKV;
+    int32_t r;
+    {
+        Prof p(h, TL_K_NORM, (double)rows * D * 9.0);
+        TL_LAUNCH(h, launch_rmsnorm_quant(h->stream, h->x, L.g_in, rows, D, c.rms_eps, h->plan, nullptr, h->a8, h->as));
+    }
+    if ((r = linear(h, EPI_DEQUANT, rows, h->a8, h->as, L.wqkv, L.sqkv, nullptr, nullptr, QKV, D, nullptr, h->qkv, TL_K_QKV)))
+        return r;
+    {
+        Prof p(h, TL_K_ATTN, (double)rows * (QKV * 4.0 + D) + (double)rows * KVD * 2.0);
+        TL_LAUNCH(h, launch_qkv_post(h->stream, h->qkv, rows, c.n_heads, c.n_kv_heads, rowmap(h), h->rope_cos,
+                                     h->rope_sin, h->kv, layer, h->kv_sk, h->kv_sv, h->q8, h->qs, nullptr));
+    }
+    {
+        Prof p(h, TL_K_ATTN, (double)rows * c.n_kv_heads * (double)max_t * 128.0 + rows * D * 5.0);
+        TL_LAUNCH(h, launch_attention(h->stream, h->q8, h->qs, rows, c.n_heads, c.n_kv_heads, rowmap(h), h->kv,
+                                      layer, h->kv_sk, h->kv_sv, h->att, max_t));
+    }
+    {
+        Prof p(h, TL_K_NORM, (double)rows * D * 5.0);
+        TL_LAUNCH(h, launch_quantize_rows(h->stream, h->att, rows, D, h->a8, h->as));
+    }
+    if ((r = linear(h, EPI_DEQUANT_RES, rows, h->a8, h->as, L.wo, L.so, nullptr, nullptr, D, D, h->x, h->x, TL_K_O)))
+        return r;
+    {
+        Prof p(h, TL_K_NORM, (double)rows * D * 9.0);
+        TL_LAUNCH(h, launch_rmsnorm_quant(h->stream, h->x, L.g_post, rows, D, c.rms_eps, h->plan, nullptr, h->a8, h->as));
+    }
+    if ((r = linear(h, EPI_GLU, rows, h->a8, h->as, L.wg, L.sg, L.wu, L.su, F, D, nullptr, h->hid, TL_K_GLU)))
+        return r;
+    {
+        Prof p(h, TL_K_NORM, (double)rows * F * 5.0);
+        TL_LAUNCH(h, launch_quantize_rows(h->stream, h->hid, rows, F, h->a8, h->as));
+    }
+    if ((r = linear(h, EPI_DEQUANT_RES, rows, h->a8, h->as, L.wd, L.sd, nullptr, nullptr, D, F, h->x, h->x, TL_K_DOWN)))
+        return r;
+    return TL_OK;
+}
+
+// final RMSNorm + LM head + argmax for `rows` rows of h->x (row r predicts for
+// sequence r when rows > 1, for `seq` when rows == 1), then record tokens
+int32_t lm_head_rows(tl_handle* h, const float* xrow, int32_t rows, int32_t seq, int32_t advance) {
+    const tl_config& c = h->cfg;
+    const int D = h->D, V = c.vocab;
+    {
+        Prof p(h, TL_K_NORM, (double)rows * D * 9.0);
+        TL_LAUNCH(h, launch_rmsnorm_quant(h->stream, xrow, h->g_final, rows, D, c.rms_eps, h->plan, nullptr, h->a8, h->as));
+    }
+    unsigned long long* keys = h->keys + (rows == 1 ? seq : 0);
+    if (rows == 1) {
+        GemvArgs g{};
+        g.w = h->lm_w; g.ws = h->lm_s; g.x = h->a8; g.xs = h->as; g.key = keys; g.n = V; g.k = D;
+        Prof p(h, TL_K_LMHEAD, (double)V * D + V * 4.0 + D);
+        TL_LAUNCH(h, launch_gemv(h->stream, EPI_ARGMAX, g));
+    } else {
+        // M > 1: MFMA GEMM writes logits, a row argmax folds them into keys
+        GemmArgs a{};
+        a.a = h->a8; a.w = h->lm_w; a.as = h->as; a.ws = h->lm_s; a.y = h->logits; a.m = rows; a.n = V; a.k = D;
+        int32_t r = run_gemm(h, EPI_DEQUANT, a, TL_K_LMHEAD);
+        if (r) return r;
+        TL_LAUNCH(h, launch_argmax_rows(h->stream, h->logits, rows, V, keys));
+    }
+    TL_LAUNCH(h, launch_finalize_tokens(h->stream, keys, rows, h->token_cur + (rows == 1 ? seq : 0),
+                                        h->tokens_out + (int64_t)(rows == 1 ? seq : 0) * c.max_pos, c.max_pos,
+                                        h->n_gen + (rows == 1 ? seq : 0), h->cursor + (rows == 1 ? seq : 0),
+                                        h->logit_out + (int64_t)(rows == 1 ? seq : 0) * c.max_pos, advance));
+    return TL_OK;
+}
+
+int32_t upload_rows(tl_handle* h, int32_t rows, int32_t seq_first, bool seq_per_row, int32_t pos0) {
+    std::vector<int32_t> s(rows), p(rows);
+    for (int i = 0; i < rows; i++) {
+        s[i] = seq_per_row ? seq_first + i : seq_first;
+        p[i] = pos0 + i;
+    }
+    TL_HIP(h, hipMemcpyAsync(h->row_seq, s.data(), rows * sizeof(int32_t), hipMemcpyHostToDevice, h->stream));
+    TL_HIP(h, hipMemcpyAsync(h->row_pos, p.data(), rows * sizeof(int32_t), hipMemcpyHostToDevice, h->stream));
+    // the host vectors must outlive the async copies
+    TL_HIP(h, hipStreamSynchronize(h->stream));
+    return TL_OK;
+}
+
+int32_t check_model_loaded(tl_handle* h) {
+    for (size_t l = 0; l < h->layers.size(); l++)
+        if (!h->layers[l].wqkv) return fail(h, TL_ERR_BAD_DESCRIPTOR, "layer " + std::to_string(l) + " not loaded");
+    return TL_OK;
+}
+
+}  // namespace
+
+// ===========================================================================
+// C-ABI
+// ===========================================================================
+extern "C" {
+
+const char* tl_status_string(int32_t s) {
+    switch (s) {
+        case TL_OK: return "ok";
+        case TL_ERR_BAD_DESCRIPTOR: return "bad descriptor";
+        case TL_ERR_UNSUPPORTED: return "unsupported";
+        case TL_ERR_INTERNAL: return "internal error";
+        default: return "unknown status";
+    }
+}
+
+const char* tl_last_error(const tl_handle* h) { return h ? h->err.c_str() : g_create_error.c_str(); }
+
+int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
+    if (!cfg || !out) return fail(nullptr, TL_ERR_BAD_DESCRIPTOR, "null argument");
+    *out = nullptr;
+    const tl_config c = *cfg;
+    if (c.head_dim != kHeadDim) return fail(nullptr, TL_ERR_UNSUPPORTED, "head_dim must be 64");
+    if (c.hidden != c.n_heads * c.head_dim) return fail(nullptr, TL_ERR_BAD_DESCRIPTOR, "hidden != n_heads * head_dim");
+    if (c.n_kv_heads < 1 || c.n_heads % c.n_kv_heads) return fail(nullptr, TL_ERR_BAD_DESCRIPTOR, "n_heads % n_kv_heads");
+    if (c.n_heads / c.n_kv_heads > 8) return fail(nullptr, TL_ERR_UNSUPPORTED, "more than 8 query heads per KV head");
+    if (c.hidden % 64 || c.intermediate % 64 || c.vocab % 64)
+        return fail(nullptr, TL_ERR_UNSUPPORTED, "hidden, intermediate and vocab must be multiples of 64");
+    if (c.hidden > 6144 || c.intermediate > 6144) return fail(nullptr, TL_ERR_UNSUPPORTED, "K above 6144");
+    if (c.max_pos < 64 || c.max_pos % 64) return fail(nullptr, TL_ERR_UNSUPPORTED, "max_pos must be a multiple of 64");
+    if (c.n_layers < 1 || max_seqs < 1) return fail(nullptr, TL_ERR_BAD_DESCRIPTOR, "n_layers and max_seqs must be >= 1");
+    PwPlan plan;
+    if (!make_pw_plan(c.hidden, &plan)) return fail(nullptr, TL_ERR_UNSUPPORTED, "hidden size has no perfect pairwise-sum tree");
+
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev < 1) return fail(nullptr, TL_ERR_INTERNAL, "no HIP device");
+    int dev = 0;
+    hipGetDevice(&dev);
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return fail(nullptr, TL_ERR_INTERNAL, "hipGetDeviceProperties failed");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(nullptr, TL_ERR_UNSUPPORTED, std::string("kernels are built for gfx950, device is ") + prop.gcnArchName);
+
+    tl_handle* h = new tl_handle();
+    h->cfg = c;
+    h->max_seqs = max_seqs;
+    h->max_rows = std::max(c.max_pos, max_seqs);
+    h->device = dev;
+    h->plan = plan;
+    h->D = c.hidden;
+    h->F = c.intermediate;
+    h->KVD = c.n_kv_heads * kHeadDim;
+    h->QKV = h->D + 2 * h->KVD;
+    h->layers.resize(c.n_layers);
+    h->host_cursor.assign(max_seqs, 0);
+    h->host_ngen.assign(max_seqs, 0);
+    auto bad = [&](hipError_t e) {
+        std::string m = std::string("allocation failed: ") + hipGetErrorString(e);
+        tl_destroy(h);
+        return fail(nullptr, TL_ERR_INTERNAL, m);
+    };
+    hipError_t e;
+    if ((e = hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking)) != hipSuccess) return bad(e);
+    const int R = h->max_rows, D = h->D, F = h->F;
+    const int KF = std::max(D, F);
+    if ((e = dalloc(h, &h->x, (size_t)R * D)) || (e = dalloc(h, &h->qkv, (size_t)R * h->QKV)) ||
+        (e = dalloc(h, &h->a8, (size_t)R * KF)) || (e = dalloc(h, &h->as, (size_t)R)) ||
+        (e = dalloc(h, &h->q8, (size_t)R * D)) || (e = dalloc(h, &h->qs, (size_t)R)) ||
+        (e = dalloc(h, &h->att, (size_t)R * D)) || (e = dalloc(h, &h->hid, (size_t)R * F)) ||
+        (e = dalloc(h, &h->logits, (size_t)max_seqs * c.vocab)) || (e = dalloc(h, &h->row_seq, (size_t)R)) ||
+        (e = dalloc(h, &h->row_pos, (size_t)R)) || (e = dalloc(h, &h->tokens, (size_t)R)) ||
+        (e = dalloc(h, &h->fscratch, 64)) || (e = dalloc(h, &h->op_key, 1)) || (e = dalloc(h, &h->keys, (size_t)max_seqs)) ||
+        (e = dalloc(h, &h->token_cur, (size_t)max_seqs)) || (e = dalloc(h, &h->cursor, (size_t)max_seqs)) ||
+        (e = dalloc(h, &h->n_gen, (size_t)max_seqs)) ||
+        (e = dalloc(h, &h->tokens_out, (size_t)max_seqs * c.max_pos)) ||
+        (e = dalloc(h, &h->logit_out, (size_t)max_seqs * c.max_pos)) ||
+        (e = dalloc(h, &h->rope_cos, (size_t)c.max_pos * kHeadDim)) ||
+        (e = dalloc(h, &h->rope_sin, (size_t)c.max_pos * kHeadDim)) ||
+        (e = dalloc(h, &h->kv_sk, (size_t)c.n_layers * c.n_kv_heads)) ||
+        (e = dalloc(h, &h->kv_sv, (size_t)c.n_layers * c.n_kv_heads)) ||
+        (e = dalloc(h, &h->g_final, (size_t)D)) || (e = dalloc(h, &h->lm_w, (size_t)c.vocab * D)) ||
+        (e = dalloc(h, &h->lm_s, (size_t)c.vocab)) || (e = dalloc(h, &h->emb, (size_t)c.vocab * D)) ||
+        (e = dalloc(h, &h->emb_s, (size_t)c.vocab)))
+        return bad(e);
+    const size_t plane = (size_t)c.max_pos * kHeadDim;
+    const size_t kv_bytes = (size_t)max_seqs * c.n_layers * c.n_kv_heads * plane;
+    if ((e = dalloc(h, &h->kv.k, kv_bytes)) || (e = dalloc(h, &h->kv.v, kv_bytes))) return bad(e);
+    h->kv.n_layers = c.n_layers;
+    h->kv.n_kv_heads = c.n_kv_heads;
+    h->kv.max_pos = c.max_pos;
+    if ((e = hipMemsetAsync(h->kv.k, 0, kv_bytes, h->stream)) || (e = hipMemsetAsync(h->kv.v, 0, kv_bytes, h->stream)) ||
+        (e = hipMemsetAsync(h->keys, 0, sizeof(unsigned long long) * max_seqs, h->stream)) ||
+        (e = hipMemsetAsync(h->cursor, 0, sizeof(int32_t) * max_seqs, h->stream)) ||
+        (e = hipMemsetAsync(h->n_gen, 0, sizeof(int32_t) * max_seqs, h->stream)))
+        return bad(e);
+    std::vector<float> cs, sn;
+    default_rope(c.max_pos, c.rope_theta, cs, sn);
+    if ((e = hipMemcpy(h->rope_cos, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice)) ||
+        (e = hipMemcpy(h->rope_sin, sn.data(), sn.size() * sizeof(float), hipMemcpyHostToDevice)))
+        return bad(e);
+    h->rope_n = c.max_pos;
+    if ((e = init_kernels())) return bad(e);
+    if ((e = hipStreamSynchronize(h->stream))) return bad(e);
+    *out = h;
+    return TL_OK;
+}
+
+void tl_destroy(tl_handle* h) {
+    if (!h) return;
+    if (h->stream) hipStreamSynchronize(h->stream);
+    for (auto& p : h->prof_pending) {
+        hipEventDestroy(p.start);
+        hipEventDestroy(p.stop);
+    }
+    for (auto e : h->event_pool) hipEventDestroy(e);
+    for (void* p : h->allocs) hipFree(p);
+    if (h->stream) hipStreamDestroy(h->stream);
+    delete h;
+}
+
+int32_t tl_get_config(const tl_handle* h, tl_config* cfg) {
+    if (!h || !cfg) return TL_ERR_BAD_DESCRIPTOR;
+    *cfg = h->cfg;
+    return TL_OK;
+}
+
+int32_t tl_sync(tl_handle* h) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    return finish(h);
+}
+
+int32_t tl_load_layer(tl_handle* h, int32_t layer, const int8_t* const w[7], const float* const s[7],
+                      const float* g_in, const float* g_post, int32_t src) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, layer >= 0 && layer < h->cfg.n_layers, "layer out of range");
+    TL_REQ(h, w && s && g_in && g_post, "null weight pointer");
+    for (int i = 0; i < 7; i++) TL_REQ(h, w[i] && s[i], "null weight pointer");
+    LayerDev& L = h->layers[layer];
+    const int D = h->D, F = h->F, KVD = h->KVD;
+    if (!L.wqkv) {
+        TL_HIP(h, dalloc(h, &L.wqkv, (size_t)h->QKV * D));
+        TL_HIP(h, dalloc(h, &L.sqkv, (size_t)h->QKV));
+        TL_HIP(h, dalloc(h, &L.wo, (size_t)D * D));
+        TL_HIP(h, dalloc(h, &L.so, (size_t)D));
+        TL_HIP(h, dalloc(h, &L.wg, (size_t)F * D));
+        TL_HIP(h, dalloc(h, &L.sg, (size_t)F));
+        TL_HIP(h, dalloc(h, &L.wu, (size_t)F * D));
+        TL_HIP(h, dalloc(h, &L.su, (size_t)F));
+        TL_HIP(h, dalloc(h, &L.wd, (size_t)D * F));
+        TL_HIP(h, dalloc(h, &L.sd, (size_t)D));
+        TL_HIP(h, dalloc(h, &L.g_in, (size_t)D));
+        TL_HIP(h, dalloc(h, &L.g_post, (size_t)D));
+    }
+    TL_HIP(h, copy_in(h, L.wqkv, w[0], (size_t)D * D, src));
+    TL_HIP(h, copy_in(h, L.wqkv + (size_t)D * D, w[1], (size_t)KVD * D, src));
+    TL_HIP(h, copy_in(h, L.wqkv + (size_t)(D + KVD) * D, w[2], (size_t)KVD * D, src));
+    TL_HIP(h, copy_in(h, L.sqkv, s[0], sizeof(float) * D, src));
+    TL_HIP(h, copy_in(h, L.sqkv + D, s[1], sizeof(float) * KVD, src));
+    TL_HIP(h, copy_in(h, L.sqkv + D + KVD, s[2], sizeof(float) * KVD, src));
+    TL_HIP(h, copy_in(h, L.wo, w[3], (size_t)D * D, src));
+    TL_HIP(h, copy_in(h, L.so, s[3], sizeof(float) * D, src));
+    TL_HIP(h, copy_in(h, L.wg, w[4], (size_t)F * D, src));
+    TL_HIP(h, copy_in(h, L.sg, s[4], sizeof(float) * F, src));
+    TL_HIP(h, copy_in(h, L.wu, w[5], (size_t)F * D, src));
+    TL_HIP(h, copy_in(h, L.su, s[5], sizeof(float) * F, src));
+    TL_HIP(h, copy_in(h, L.wd, w[6], (size_t)D * F, src));
+    TL_HIP(h, copy_in(h, L.sd, s[6], sizeof(float) * D, src));
+    TL_HIP(h, copy_in(h, L.g_in, g_in, sizeof(float) * D, src));
+    TL_HIP(h, copy_in(h, L.g_post, g_post, sizeof(float) * D, src));
+    return finish(h);
+}
+
+int32_t tl_load_lm_head(tl_handle* h, const int8_t* w, const float* s, const float* g_final, int32_t src) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, w && s && g_final, "null pointer");
+    TL_HIP(h, copy_in(h, h->lm_w, w, (size_t)h->cfg.vocab * h->D, src));
+    TL_HIP(h, copy_in(h, h->lm_s, s, sizeof(float) * h->cfg.vocab, src));
+    TL_HIP(h, copy_in(h, h->g_final, g_final, sizeof(float) * h->D, src));
+    return finish(h);
+}
+
+int32_t tl_load_embedding(tl_handle* h, const int8_t* e, const float* s, int32_t src) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, e && s, "null pointer");
+    TL_HIP(h, copy_in(h, h->emb, e, (size_t)h->cfg.vocab * h->D, src));
+    TL_HIP(h, copy_in(h, h->emb_s, s, sizeof(float) * h->cfg.vocab, src));
+    return finish(h);
+}
+
+int32_t tl_set_kv_scales(tl_handle* h, const float* k_scales, const float* v_scales) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, k_scales && v_scales, "null pointer");
+    const size_t n = (size_t)h->cfg.n_layers * h->cfg.n_kv_heads;
+    for (size_t i = 0; i < n; i++)
+        TL_REQ(h, k_scales[i] > 0.0f && v_scales[i] > 0.0f && std::isfinite(k_scales[i]) && std::isfinite(v_scales[i]),
+               "KV scales must be positive and finite");
+    TL_HIP(h, hipMemcpyAsync(h->kv_sk, k_scales, n * sizeof(float), hipMemcpyHostToDevice, h->stream));
+    TL_HIP(h, hipMemcpyAsync(h->kv_sv, v_scales, n * sizeof(float), hipMemcpyHostToDevice, h->stream));
+    return finish(h);
+}
+
+int32_t tl_set_rope_table(tl_handle* h, const float* cos, const float* sin, int32_t n_pos) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, cos && sin, "null pointer");
+    TL_REQ(h, n_pos >= h->cfg.max_pos, "RoPE table shorter than max_pos");
+    const size_t n = (size_t)h->cfg.max_pos * kHeadDim * sizeof(float);
+    TL_HIP(h, hipMemcpyAsync(h->rope_cos, cos, n, hipMemcpyHostToDevice, h->stream));
+    TL_HIP(h, hipMemcpyAsync(h->rope_sin, sin, n, hipMemcpyHostToDevice, h->stream));
+    return finish(h);
+}
+
+int32_t tl_kv_write(tl_handle* h, int32_t seq, int32_t layer, int32_t g, int32_t t0, int32_t n,
+                    const int8_t* k_rows, const int8_t* v_rows) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    const tl_config& c = h->cfg;
+    TL_REQ(h, seq >= 0 && seq < h->max_seqs && layer >= 0 && layer < c.n_layers && g >= 0 && g < c.n_kv_heads,
+           "KV index out of range");
+    TL_REQ(h, t0 >= 0 && n >= 0 && t0 + n <= c.max_pos, "KV token range out of bounds");
+    if (n == 0) return TL_OK;
+    const size_t bytes = (size_t)n * kHeadDim;
+    int8_t* kd = nullptr;
+    int8_t* vd = nullptr;
+    TL_HIP(h, hipMalloc(&kd, bytes));
+    hipError_t e = hipMalloc(&vd, bytes);
+    if (e != hipSuccess) {
+        hipFree(kd);
+        return fail(h, TL_ERR_INTERNAL, "hipMalloc");
+    }
+    int32_t rc = TL_OK;
+    if (k_rows && hipMemcpy(kd, k_rows, bytes, hipMemcpyHostToDevice) != hipSuccess) rc = TL_ERR_INTERNAL;
+    if (v_rows && hipMemcpy(vd, v_rows, bytes, hipMemcpyHostToDevice) != hipSuccess) rc = TL_ERR_INTERNAL;
+    if (!rc && launch_kv_scatter(h->stream, h->kv, seq, layer, g, t0, n, k_rows ? kd : nullptr, v_rows ? vd : nullptr) != hipSuccess)
+        rc = TL_ERR_INTERNAL;
+    if (!rc) rc = finish(h);
+    hipFree(kd);
+    hipFree(vd);
+    return rc ? fail(h, rc, h->err.empty() ? "kv write failed" : h->err) : TL_OK;
+}
+
+int32_t tl_kv_read(tl_handle* h, int32_t seq, int32_t layer, int32_t g, int32_t t0, int32_t n,
+                   int8_t* k_rows, int8_t* v_rows) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    const tl_config& c = h->cfg;
+    TL_REQ(h, seq >= 0 && seq < h->max_seqs && layer >= 0 && layer < c.n_layers && g >= 0 && g < c.n_kv_heads,
+           "KV index out of range");
+    TL_REQ(h, t0 >= 0 && n >= 0 && t0 + n <= c.max_pos, "KV token range out of bounds");
+    if (n == 0) return TL_OK;
+    const size_t bytes = (size_t)n * kHeadDim;
+    int8_t* kd = nullptr;
+    int8_t* vd = nullptr;
+    TL_HIP(h, hipMalloc(&kd, bytes));
+    hipError_t e = hipMalloc(&vd, bytes);
+    if (e != hipSuccess) {
+        hipFree(kd);
+        return fail(h, TL_ERR_INTERNAL, "hipMalloc");
+    }
+    int32_t rc = TL_OK;
+    if (launch_kv_gather(h->stream, h->kv, seq, layer, g, t0, n, kd, vd) != hipSuccess) rc = TL_ERR_INTERNAL;
+    if (!rc) rc = finish(h);
+    if (!rc && k_rows && hipMemcpy(k_rows, kd, bytes, hipMemcpyDeviceToHost) != hipSuccess) rc = TL_ERR_INTERNAL;
+    if (!rc && v_rows && hipMemcpy(v_rows, vd, bytes, hipMemcpyDeviceToHost) != hipSuccess) rc = TL_ERR_INTERNAL;
+    hipFree(kd);
+    hipFree(vd);
+    return rc ? fail(h, rc, h->err.empty() ? "kv read failed" : h->err) : TL_OK;
+}
+
+// ---- operators ----------------------------------------------------------------
+
+int32_t tl_quantize_rows(tl_handle* h, const float* x, int32_t rows, int32_t n, int8_t* q, double* scales) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, rows >= 0 && n > 0 && x && q && scales, "bad quantize_rows arguments");
+    TL_LAUNCH(h, launch_quantize_rows(h->stream, x, rows, n, q, scales));
+    return finish(h);
+}
+
+int32_t tl_quantize_tensor(tl_handle* h, const float* x, int64_t n, int8_t* q, double* scale) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, n >= 0 && x && q && scale, "bad quantize_tensor arguments");
+    TL_LAUNCH(h, launch_quantize_tensor(h->stream, x, n, q, scale, h->fscratch));
+    return finish(h);
+}
+
+int32_t tl_quantize_weight_rows(tl_handle* h, const float* w, int32_t rows, int32_t n, int8_t* q, float* scales) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, rows >= 0 && n > 0 && w && q && scales, "bad quantize_weight_rows arguments");
+    TL_LAUNCH(h, launch_quantize_weight_rows(h->stream, w, rows, n, q, scales));
+    return finish(h);
+}
+
+int32_t tl_rmsnorm_quant(tl_handle* h, const float* x, const float* gamma, int32_t rows, int32_t n, float* y,
+                         int8_t* q, double* scales) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, rows >= 0 && x && gamma && q && scales, "bad rmsnorm arguments");
+    PwPlan plan;
+    if (!make_pw_plan(n, &plan)) return fail(h, TL_ERR_UNSUPPORTED, "width has no perfect pairwise-sum tree");
+    TL_LAUNCH(h, launch_rmsnorm_quant(h->stream, x, gamma, rows, n, h->cfg.rms_eps, plan, y, q, scales));
+    return finish(h);
+}
+
+int32_t tl_gemv_i8_requant(tl_handle* h, const int8_t* x, const int8_t* w, const float* m, int32_t n, int32_t k,
+                           int8_t* y, int32_t* acc) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, x && w && m && y && n > 0, "bad gemv arguments");
+    TL_REQ(h, k > 0 && k % 16 == 0 && k <= 6144, "K must be a positive multiple of 16, at most 6144");
+    GemvArgs g{};
+    g.w = w; g.ws = m; g.x = x; g.y8 = y; g.acc = acc; g.n = n; g.k = k;
+    {
+        Prof p(h, TL_K_QKV, (double)n * k + n * 4.0 + k + n);
+        TL_LAUNCH(h, launch_gemv(h->stream, EPI_REQUANT, g));
+    }
+    return finish(h);
+}
+
+int32_t tl_gemm_i8(tl_handle* h, const int8_t* a, const int8_t* w, int32_t m, int32_t n, int32_t k, int32_t* c) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, a && w && c && m > 0 && n > 0, "bad gemm arguments");
+    TL_REQ(h, k > 0 && k % 64 == 0, "K must be a positive multiple of 64");
+    GemmArgs g{};
+    g.a = a; g.w = w; g.acc = c; g.m = m; g.n = n; g.k = k;
+    int32_t r = run_gemm(h, EPI_RAW, g, TL_K_GEMM_PREFILL);
+    if (r) return r;
+    return finish(h);
+}
+
+int32_t tl_gemm_i8_dequant(tl_handle* h, const int8_t* a, const double* a_scales, const int8_t* w,
+                           const float* w_scales, int32_t m, int32_t n, int32_t k, const float* residual, float* y) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, a && a_scales && w && w_scales && y && m > 0 && n > 0, "bad gemm arguments");
+    if (m == 1) TL_REQ(h, k > 0 && k % 16 == 0 && k <= 6144, "K must be a multiple of 16, at most 6144");
+    else TL_REQ(h, k > 0 && k % 64 == 0, "K must be a positive multiple of 64");
+    int32_t r = linear(h, residual ? EPI_DEQUANT_RES : EPI_DEQUANT, m, a, a_scales, w, w_scales, nullptr, nullptr, n, k,
+                       residual, y, TL_K_OTHER);
+    if (r) return r;
+    return finish(h);
+}
+
+int32_t tl_rope(tl_handle* h, float* v, int32_t rows, int32_t n_heads, const int32_t* pos) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, v && pos && rows >= 0 && n_heads > 0, "bad rope arguments");
+    TL_LAUNCH(h, launch_rope(h->stream, v, rows, n_heads, pos, h->rope_cos, h->rope_sin));
+    return finish(h);
+}
+
+int32_t tl_softmax_rows(tl_handle* h, const float* x, int32_t rows, int32_t n, float* p) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, x && p && rows >= 0 && n > 0, "bad softmax arguments");
+    TL_LAUNCH(h, launch_softmax_rows(h->stream, x, rows, n, p));
+    return finish(h);
+}
+
+int32_t tl_silu_mul(tl_handle* h, const float* g, const float* u, int64_t n, float* y) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, g && y && n >= 0, "bad silu arguments");
+    TL_LAUNCH(h, launch_silu_mul(h->stream, g, u, n, y));
+    return finish(h);
+}
+
+int32_t tl_qkv_append(tl_handle* h, int32_t seq, int32_t layer, int32_t pos0, int32_t rows, const float* qkv,
+                      int8_t* q8, double* q_scale, float* q_rot) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    const tl_config& c = h->cfg;
+    TL_REQ(h, seq >= 0 && seq < h->max_seqs && layer >= 0 && layer < c.n_layers, "index out of range");
+    TL_REQ(h, rows >= 1 && rows <= h->max_rows && pos0 >= 0 && pos0 + rows <= c.max_pos, "position range out of bounds");
+    TL_REQ(h, qkv && q8 && q_scale, "null pointer");
+    int32_t r = upload_rows(h, rows, seq, false, pos0);
+    if (r) return r;
+    TL_LAUNCH(h, launch_qkv_post(h->stream, qkv, rows, c.n_heads, c.n_kv_heads, rowmap(h), h->rope_cos, h->rope_sin,
+                                 h->kv, layer, h->kv_sk, h->kv_sv, q8, q_scale, q_rot));
+    return finish(h);
+}
+
+int32_t tl_attention(tl_handle* h, int32_t seq, int32_t layer, int32_t pos0, int32_t rows, const int8_t* q8,
+                     const double* q_scale, float* out) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    const tl_config& c = h->cfg;
+    TL_REQ(h, seq >= 0 && seq < h->max_seqs && layer >= 0 && layer < c.n_layers, "index out of range");
+    TL_REQ(h, rows >= 1 && rows <= h->max_rows && pos0 >= 0 && pos0 + rows <= c.max_pos, "position range out of bounds");
+    TL_REQ(h, q8 && q_scale && out, "null pointer");
+    int32_t r = upload_rows(h, rows, seq, false, pos0);
+    if (r) return r;
+    {
+        Prof p(h, TL_K_ATTN, 0.0);
+        TL_LAUNCH(h, launch_attention(h->stream, q8, q_scale, rows, c.n_heads, c.n_kv_heads, rowmap(h), h->kv, layer,
+                                      h->kv_sk, h->kv_sv, out, pos0 + rows));
+    }
+    return finish(h);
+}
+
+int32_t tl_lm_head_argmax(tl_handle* h, const float* x, int32_t* token, float* logit, float* logits) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, x && token, "null pointer");
+    const int D = h->D, V = h->cfg.vocab;
+    TL_LAUNCH(h, launch_reset_keys(h->stream, h->op_key, 1));
+    {
+        Prof p(h, TL_K_NORM, D * 9.0);
+        TL_LAUNCH(h, launch_rmsnorm_quant(h->stream, x, h->g_final, 1, D, h->cfg.rms_eps, h->plan, nullptr, h->a8, h->as));
+    }
+    GemvArgs g{};
+    g.w = h->lm_w; g.ws = h->lm_s; g.x = h->a8; g.xs = h->as; g.key = h->op_key; g.y = logits; g.n = V; g.k = D;
+    {
+        Prof p(h, TL_K_LMHEAD, (double)V * D + V * 4.0 + D);
+        TL_LAUNCH(h, launch_gemv(h->stream, EPI_ARGMAX, g));
+    }
+    unsigned long long key = 0;
+    TL_HIP(h, hipMemcpyAsync(&key, h->op_key, sizeof key, hipMemcpyDeviceToHost, h->stream));
+    int32_t r = finish(h);
+    if (r) return r;
+    *token = (int32_t)(0xFFFFFFFFu - (unsigned)(key & 0xFFFFFFFFull));
+    if (logit) {
+        unsigned u = (unsigned)(key >> 32);
+        u = (u & 0x80000000u) ? (u & 0x7FFFFFFFu) : ~u;
+        std::memcpy(logit, &u, sizeof u);
+    }
+    return TL_OK;
+}
+
+// ---- composed path ----------------------------------------------------------------
+
+int32_t tl_embed(tl_handle* h, const int32_t* tokens, int32_t rows, float* x) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, tokens && x && rows >= 0, "bad embed arguments");
+    TL_LAUNCH(h, launch_embed(h->stream, tokens, rows, h->D, h->cfg.vocab, h->emb, h->emb_s, x));
+    return finish(h);
+}
+
+int32_t tl_decode_layer(tl_handle* h, int32_t seq, int32_t layer, int32_t pos, float* x) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    const tl_config& c = h->cfg;
+    TL_REQ(h, seq >= 0 && seq < h->max_seqs && layer >= 0 && layer < c.n_layers, "index out of range");
+    TL_REQ(h, pos >= 0 && pos < c.max_pos, "position out of range");
+    TL_REQ(h, x, "null pointer");
+    if (!h->layers[layer].wqkv) return fail(h, TL_ERR_BAD_DESCRIPTOR, "layer not loaded");
+    int32_t r = upload_rows(h, 1, seq, false, pos);
+    if (r) return r;
+    TL_HIP(h, hipMemcpyAsync(h->x, x, sizeof(float) * h->D, hipMemcpyDeviceToDevice, h->stream));
+    if ((r = layer_rows(h, layer, 1, pos + 1))) return r;
+    TL_HIP(h, hipMemcpyAsync(x, h->x, sizeof(float) * h->D, hipMemcpyDeviceToDevice, h->stream));
+    return finish(h);
+}
+
+int32_t tl_prefill(tl_handle* h, int32_t seq, const int32_t* tokens, int32_t n, int32_t* next_token, float* next_logit) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    const tl_config& c = h->cfg;
+    TL_REQ(h, seq >= 0 && seq < h->max_seqs, "sequence out of range");
+    TL_REQ(h, tokens && n >= 1, "Input token sequence is empty");
+    TL_REQ(h, n <= c.max_pos, "Sequence length exceeds max_position_embeddings");
+    for (int i = 0; i < n; i++) TL_REQ(h, tokens[i] >= 0 && tokens[i] < c.vocab, "token id out of range");
+    int32_t r = check_model_loaded(h);
+    if (r) return r;
+    if ((r = upload_rows(h, n, seq, false, 0))) return r;
+    TL_HIP(h, hipMemcpyAsync(h->tokens, tokens, sizeof(int32_t) * n, hipMemcpyHostToDevice, h->stream));
+    const int32_t zero = 0;
+    TL_HIP(h, hipMemcpyAsync(h->n_gen + seq, &zero, sizeof zero, hipMemcpyHostToDevice, h->stream));
+    TL_HIP(h, hipMemcpyAsync(h->cursor + seq, &n, sizeof n, hipMemcpyHostToDevice, h->stream));
+    TL_LAUNCH(h, launch_reset_keys(h->stream, h->keys + seq, 1));
+    TL_LAUNCH(h, launch_embed(h->stream, h->tokens, n, h->D, h->cfg.vocab, h->emb, h->emb_s, h->x));
+    for (int l = 0; l < c.n_layers; l++)
+        if ((r = layer_rows(h, l, n, n))) return r;
+    if ((r = lm_head_rows(h, h->x + (size_t)(n - 1) * h->D, 1, seq, 0))) return r;
+    if ((r = finish(h))) return r;
+    h->host_cursor[seq] = n;
+    h->host_ngen[seq] = 1;
+    if (next_token) TL_HIP(h, hipMemcpy(next_token, h->tokens_out + (size_t)seq * c.max_pos, sizeof(int32_t), hipMemcpyDeviceToHost));
+    if (next_logit) TL_HIP(h, hipMemcpy(next_logit, h->logit_out + (size_t)seq * c.max_pos, sizeof(float), hipMemcpyDeviceToHost));
+    return TL_OK;
+}
+
+int32_t tl_decode(tl_handle* h, int32_t seq, int32_t max_new, int32_t eos_id, const volatile int32_t* abort_flag,
+                  int32_t* tokens_out, int32_t* n_out, int32_t* stop_reason) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    const tl_config& c = h->cfg;
+    TL_REQ(h, seq >= 0 && seq < h->max_seqs, "sequence out of range");
+    TL_REQ(h, max_new >= 1, "--max-tokens must be at least 1");
+    TL_REQ(h, tokens_out && n_out, "null pointer");
+    TL_REQ(h, h->host_ngen[seq] >= 1, "tl_decode needs a prefilled sequence");
+    TL_REQ(h, h->host_cursor[seq] + max_new <= c.max_pos, "Sequence length exceeds max_position_embeddings");
+    *n_out = 0;
+    if (stop_reason) *stop_reason = TL_STOP_NONE;
+    const bool per_step = eos_id >= 0 || abort_flag;
+    const int32_t first = h->host_ngen[seq];
+    int32_t r;
+    if ((r = upload_rows(h, 1, seq, false, h->host_cursor[seq]))) return r;
+    for (int step = 0; step < max_new; step++) {
+        if (abort_flag && *abort_flag) {
+            if (stop_reason) *stop_reason = TL_STOP_HOST_ABORT;
+            break;
+        }
+        TL_LAUNCH(h, launch_step_rows(h->stream, h->row_seq, 1, h->cursor, h->row_pos));
+        TL_LAUNCH(h, launch_embed(h->stream, h->token_cur + seq, 1, h->D, h->cfg.vocab, h->emb, h->emb_s, h->x));
+        const int32_t max_t = h->host_cursor[seq] + 1;
+        for (int l = 0; l < c.n_layers; l++)
+            if ((r = layer_rows(h, l, 1, max_t))) return r;
+        if ((r = lm_head_rows(h, h->x, 1, seq, 1))) return r;
+        h->host_cursor[seq] += 1;
+        h->host_ngen[seq] += 1;
+        *n_out = step + 1;
+        if (per_step) {
+            int32_t tok = -1;
+            TL_HIP(h, hipMemcpyAsync(&tok, h->tokens_out + (size_t)seq * c.max_pos + first + step, sizeof tok,
+                                     hipMemcpyDeviceToHost, h->stream));
+            if ((r = finish(h))) return r;
+            tokens_out[step] = tok;
+            if (eos_id >= 0 && tok == eos_id) {
+                if (stop_reason) *stop_reason = TL_STOP_EOS;
+                return TL_OK;
+            }
+        }
+    }
+    if ((r = finish(h))) return r;
+    if (!per_step && *n_out > 0)
+        TL_HIP(h, hipMemcpy(tokens_out, h->tokens_out + (size_t)seq * c.max_pos + first, sizeof(int32_t) * *n_out,
+                            hipMemcpyDeviceToHost));
+    if (stop_reason && *stop_reason == TL_STOP_NONE) *stop_reason = TL_STOP_MAX_TOKENS;
+    return TL_OK;
+}
+
+int32_t tl_generate(tl_handle* h, int32_t seq, const int32_t* prompt, int32_t n_prompt, int32_t max_new, int32_t eos_id,
+                    const volatile int32_t* abort_flag, int32_t* tokens_out, int32_t* n_out, int32_t* stop_reason) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, max_new >= 1, "--max-tokens must be at least 1");
+    TL_REQ(h, tokens_out && n_out, "null pointer");
+    TL_REQ(h, prompt && n_prompt >= 1, "Input token sequence is empty");
+    TL_REQ(h, n_prompt + max_new - 1 <= h->cfg.max_pos, "Sequence length exceeds max_position_embeddings");
+    *n_out = 0;
+    if (stop_reason) *stop_reason = TL_STOP_NONE;
+    if (abort_flag && *abort_flag) {
+        if (stop_reason) *stop_reason = TL_STOP_HOST_ABORT;
+        return TL_OK;
+    }
+    int32_t first = 0;
+    int32_t r = tl_prefill(h, seq, prompt, n_prompt, &first, nullptr);
+    if (r) return r;
+    tokens_out[0] = first;
+    *n_out = 1;
+    if (eos_id >= 0 && first == eos_id) {
+        if (stop_reason) *stop_reason = TL_STOP_EOS;
+        return TL_OK;
+    }
+    if (max_new == 1) {
+        if (stop_reason) *stop_reason = TL_STOP_MAX_TOKENS;
+        return TL_OK;
+    }
+    int32_t more = 0;
+    r = tl_decode(h, seq, max_new - 1, eos_id, abort_flag, tokens_out + 1, &more, stop_reason);
+    *n_out = 1 + more;
+    return r;
+}
+
+int32_t tl_decode_batch(tl_handle* h, int32_t n_seqs, const int32_t* tokens, const int32_t* start_pos, int32_t n_steps,
+                        int32_t* tokens_out) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    const tl_config& c = h->cfg;
+    TL_REQ(h, n_seqs >= 1 && n_seqs <= h->max_seqs, "batch larger than max_seqs");
+    TL_REQ(h, tokens && start_pos && tokens_out && n_steps >= 1, "bad decode_batch arguments");
+    int32_t max_t = 0;
+    for (int b = 0; b < n_seqs; b++) {
+        TL_REQ(h, tokens[b] >= 0 && tokens[b] < c.vocab, "token id out of range");
+        TL_REQ(h, start_pos[b] >= 0 && start_pos[b] + n_steps <= c.max_pos, "Sequence length exceeds max_position_embeddings");
+        max_t = std::max(max_t, start_pos[b] + n_steps);
+    }
+    int32_t r = check_model_loaded(h);
+    if (r) return r;
+    if ((r = upload_rows(h, n_seqs, 0, true, 0))) return r;
+    std::vector<int32_t> zeros(n_seqs, 0);
+    TL_HIP(h, hipMemcpyAsync(h->token_cur, tokens, sizeof(int32_t) * n_seqs, hipMemcpyHostToDevice, h->stream));
+    TL_HIP(h, hipMemcpyAsync(h->cursor, start_pos, sizeof(int32_t) * n_seqs, hipMemcpyHostToDevice, h->stream));
+    TL_HIP(h, hipMemcpyAsync(h->n_gen, zeros.data(), sizeof(int32_t) * n_seqs, hipMemcpyHostToDevice, h->stream));
+    TL_LAUNCH(h, launch_reset_keys(h->stream, h->keys, n_seqs));
+    for (int step = 0; step < n_steps; step++) {
+        TL_LAUNCH(h, launch_step_rows(h->stream, h->row_seq, n_seqs, h->cursor, h->row_pos));
+        TL_LAUNCH(h, launch_embed(h->stream, h->token_cur, n_seqs, h->D, h->cfg.vocab, h->emb, h->emb_s, h->x));
+        for (int l = 0; l < c.n_layers; l++)
+            if ((r = layer_rows(h, l, n_seqs, max_t))) return r;
+        if ((r = lm_head_rows(h, h->x, n_seqs, 0, 1))) return r;
+    }
+    if ((r = finish(h))) return r;
+    for (int b = 0; b < n_seqs; b++) {
+        TL_HIP(h, hipMemcpy(tokens_out + (size_t)b * n_steps, h->tokens_out + (size_t)b * c.max_pos,
+                            sizeof(int32_t) * n_steps, hipMemcpyDeviceToHost));
+        h->host_cursor[b] = start_pos[b] + n_steps;
+        h->host_ngen[b] = n_steps;
+    }
+    return TL_OK;
+}
+
+// ---- profiling -----------------------------------------------------------------------
+
+int32_t tl_set_profiling(tl_handle* h, int32_t on) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    harvest_profile(h);
+    h->profiling = on != 0;
+    for (int i = 0; i < TL_K_COUNT; i++) {
+        h->prof_count[i] = 0;
+        h->prof_ms[i] = 0.0;
+        h->prof_bytes[i] = 0.0;
+    }
+    return TL_OK;
+}
+
+int32_t tl_get_profile(tl_handle* h, int32_t kclass, int64_t* count, double* total_ms, double* bytes) {
+    if (!h || kclass < 0 || kclass >= TL_K_COUNT) return TL_ERR_BAD_DESCRIPTOR;
+    harvest_profile(h);
+    if (count) *count = h->prof_count[kclass];
+    if (total_ms) *total_ms = h->prof_ms[kclass];
+    if (bytes) *bytes = h->prof_bytes[kclass];
+    return TL_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,78 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function
+include/tl_int8.h declares, and refuses to run without a gfx950 device
+instead of falling back to the CPU."""
+import ctypes
+import os
+
+import pytest
+
+import lpta
+from lpta import _native
+
+
+def test_library_exports_every_header_symbol():
+    lib = lpta.load_library()
+    declared = lpta.header_symbols()
+    assert len(declared) >= 30
+    missing = [s for s in declared if not hasattr(lib, s)]
+    assert not missing, f"declared in tl_int8.h but not exported: {missing}"
+    # and the Python binding declares a signature for each of them
+    assert sorted(_native.SIGNATURES) == declared
+
+
+def test_status_strings():
+    lib = lpta.load_library()
+    assert lib.tl_status_string(0) == b"ok"
+    assert lib.tl_status_string(1) == b"bad descriptor"
+    assert lib.tl_status_string(7) == b"internal error"
+
+
+def test_config_layout_matches_header():
+    # ten 4-byte fields, as tl_config in include/tl_int8.h and or_config in the oracle
+    assert ctypes.sizeof(_native.TlConfig) == 40
+    import oracle
+    assert ctypes.sizeof(oracle.OrConfig) == 40
+
+
+def _has_gpu():
+    try:
+        import torch
+        return torch.cuda.is_available()
+    except Exception:
+        return False
+
+
+@pytest.mark.skipif(_has_gpu(), reason="checks the no-device path")
+def test_no_cpu_fallback_without_gpu():
+    with pytest.raises(_native.TlError) as e:
+        _native.Runtime(dict(hidden=512, intermediate=1408, n_layers=1, n_heads=8, n_kv_heads=2,
+                             head_dim=64, vocab=64, max_pos=128, rms_eps=1e-5, rope_theta=1e4))
+    assert e.value.status == _native.TL_ERR_INTERNAL
+
+
+def test_bad_geometry_rejected_before_device_use():
+    lib = lpta.load_library()
+    h = ctypes.c_void_p()
+    bad = _native.TlConfig(512, 1408, 1, 8, 2, 128, 64, 128, 1e-5, 1e4)   # head_dim 128
+    assert lib.tl_create(ctypes.byref(bad), 1, ctypes.byref(h)) == _native.TL_ERR_UNSUPPORTED
+    assert b"head_dim" in lib.tl_last_error(None)
+    bad = _native.TlConfig(520, 1408, 1, 8, 2, 64, 64, 128, 1e-5, 1e4)    # hidden != heads * 64
+    assert lib.tl_create(ctypes.byref(bad), 1, ctypes.byref(h)) == _native.TL_ERR_BAD_DESCRIPTOR
+    bad = _native.TlConfig(1536, 1408, 1, 24, 2, 64, 64, 128, 1e-5, 1e4)  # 24 heads per kv head
+    assert lib.tl_create(ctypes.byref(bad), 1, ctypes.byref(h)) == _native.TL_ERR_UNSUPPORTED
+    assert not h.value
+
+
+def test_missing_library_fails_loudly(tmp_path, monkeypatch):
+    monkeypatch.setattr(_native, "_lib", None)
+    monkeypatch.setattr(_native, "LIB_PATH", os.path.join(tmp_path, "nope.so"))
+    with pytest.raises(RuntimeError, match="missing"):
+        _native.load_library()
+
+
+def test_pairwise_plan_widths():
+    # widths the device RMSNorm accepts: halving chain on multiples of 8
+    lib = lpta.load_library()
+    h = ctypes.c_void_p()
+    bad = _native.TlConfig(64 * 3 * 7, 1408, 1, 21, 3, 64, 64, 128, 1e-5, 1e4)  # 1344 -> 672 -> 336 -> 168 -> 84
+    assert lib.tl_create(ctypes.byref(bad), 1, ctypes.byref(h)) == _native.TL_ERR_UNSUPPORTED

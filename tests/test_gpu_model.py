@@ -1,0 +1,166 @@
+"""Decoder-layer and model-level parity through the C-ABI against the CPU
+oracle: the TinyLlama-shape decode layer over a prefilled INT8 KV cache,
+prefill vs token-by-token decode, greedy generation and batched decode.
+Token ids, KV rows, INT8 values and float outputs must be bit-identical."""
+import numpy as np
+import pytest
+
+import oracle
+from gpu_util import assert_bits_equal, dev, host
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+
+
+def engine_for(model, max_seqs=1):
+    from lpta.engine import Engine
+    return Engine(model.cfg, max_seqs=max_seqs).load_model(model)
+
+
+def fill_cache_random(eng, model, seq, n_tokens, seed, kc=None, vc=None):
+    """Seeded uniform INT8 K/V rows at positions 0..n_tokens-1 (written to the
+    engine and, when given, to the oracle's logical cache)."""
+    rng = np.random.default_rng(seed)
+    c = model.cfg
+    for layer in range(c["n_layers"]):
+        for g in range(c["n_kv_heads"]):
+            k = rng.integers(-127, 128, (n_tokens, 64)).astype(np.int8)
+            v = rng.integers(-127, 128, (n_tokens, 64)).astype(np.int8)
+            eng.kv_write(seq, layer, g, 0, k, v)
+            if kc is not None:
+                kc[layer, g, :n_tokens] = k
+                vc[layer, g, :n_tokens] = v
+
+
+# ---- one TinyLlama-shape decoder layer, one decode step over a 512-token cache ----
+
+@pytest.fixture(scope="module")
+def layer_model():
+    cfg = dict(oracle.TINYLLAMA_CFG, n_layers=1, vocab=64)
+    return oracle.synthetic_model(cfg, seed=2024, kv_range=(0.01, 0.1))
+
+
+def test_decode_layer_tinyllama_shape(layer_model):
+    m = layer_model
+    eng = engine_for(m)
+    orc = oracle.Oracle(m)
+    kc, vc = m.new_cache()
+    fill_cache_random(eng, m, 0, 512, seed=77, kc=kc, vc=vc)
+    x = np.random.default_rng(5).standard_normal(2048).astype(F32)
+    xd = dev(x)
+    eng.decode_layer(xd, layer=0, pos=512)
+    want = orc.decode_row(0, 512, x, kc, vc)
+    assert_bits_equal(host(xd), want, "layer output")
+    for g in range(4):
+        k, v = eng.kv_read(0, 0, g, 0, 513)
+        assert_bits_equal(k, kc[0, g, :513], f"K cache head {g}")
+        assert_bits_equal(v, vc[0, g, :513], f"V cache head {g}")
+    eng.close()
+
+
+# ---- small models: generation, prefill == decode, batched decode -------------------
+
+@pytest.fixture(scope="module")
+def small_model():
+    return oracle.synthetic_model(dict(oracle.SMALL_CFG), seed=11)
+
+
+def test_generate_matches_oracle(small_model):
+    eng = engine_for(small_model)
+    prompt = np.array([5, 17, 1000, 3, 3, 2047, 64], np.int32)
+    got, stop = eng.generate(prompt, 24)
+    want, _ = oracle.Oracle(small_model).generate(prompt, 24)
+    assert stop == "max_tokens"
+    assert_bits_equal(got, want, "token ids")
+    eng.close()
+
+
+def test_prefill_cache_equals_sequential_decode(small_model):
+    """Rows of a prefill are the same rows sequential decode would produce."""
+    m = small_model
+    eng = engine_for(m)
+    prompt = np.random.default_rng(3).integers(0, m.cfg["vocab"], 70).astype(np.int32)
+    tok, _ = eng.prefill(prompt)
+    kc, vc = m.new_cache()
+    orc = oracle.Oracle(m)
+    x = None
+    for i, t in enumerate(prompt):
+        x = orc.embed(int(t))
+        for layer in range(m.cfg["n_layers"]):
+            x = orc.decode_row(layer, i, x, kc, vc)
+    want_tok, _ = orc.lm_head(x)
+    assert tok == want_tok
+    for layer in range(m.cfg["n_layers"]):
+        for g in range(m.cfg["n_kv_heads"]):
+            k, v = eng.kv_read(0, layer, g, 0, prompt.size)
+            assert_bits_equal(k, kc[layer, g, :prompt.size], "K")
+            assert_bits_equal(v, vc[layer, g, :prompt.size], "V")
+    eng.close()
+
+
+def test_generate_eos_and_abort(small_model):
+    import ctypes
+    eng = engine_for(small_model)
+    prompt = np.array([1, 2, 3], np.int32)
+    free, _ = eng.generate(prompt, 12)
+    eos = int(free[4])
+    first = int(np.argmax(free == eos))
+    got, stop = eng.generate(prompt, 12, eos_id=eos)
+    assert stop == "eos" and got.tolist() == free[:first + 1].tolist()
+    flag = ctypes.c_int32(1)
+    got, stop = eng.generate(prompt, 12, abort_flag=flag)
+    assert stop == "host_abort" and got.size == 0
+    eng.close()
+
+
+def test_decode_batch_matches_oracle(small_model):
+    m = small_model
+    B, steps = 4, 6
+    eng = engine_for(m, max_seqs=B)
+    start = np.array([40, 100, 7, 180], np.int32)
+    toks = np.array([9, 999, 2000, 0], np.int32)
+    caches = []
+    for b in range(B):
+        kc, vc = m.new_cache()
+        fill_cache_random(eng, m, b, int(start[b]), seed=100 + b, kc=kc, vc=vc)
+        caches.append((kc, vc))
+    got = eng.decode_batch(toks, start, steps)
+    orc = oracle.Oracle(m)
+    for b in range(B):
+        kc, vc = caches[b]
+        tok = int(toks[b])
+        for s in range(steps):
+            x = orc.embed(tok)
+            for layer in range(m.cfg["n_layers"]):
+                x = orc.decode_row(layer, int(start[b]) + s, x, kc, vc)
+            tok, _ = orc.lm_head(x)
+            assert got[b, s] == tok, f"seq {b} step {s}"
+    eng.close()
+
+
+def test_lm_head_argmax_operator(small_model):
+    m = small_model
+    eng = engine_for(m)
+    x = np.random.default_rng(1).standard_normal(m.cfg["hidden"]).astype(F32)
+    import ctypes
+    tok, lg = ctypes.c_int32(), ctypes.c_float()
+    logits = dev(np.zeros(m.cfg["vocab"], F32))
+    eng.rt.call("tl_lm_head_argmax", dev(x), ctypes.byref(tok), ctypes.byref(lg), logits)
+    want_tok, want_lg, want_logits = oracle.Oracle(m).lm_head(x, want_logits=True)
+    assert_bits_equal(host(logits), want_logits, "logits")
+    assert tok.value == want_tok and lg.value == want_lg
+    eng.close()
+
+
+def test_bad_arguments_raise_value_error(small_model):
+    from lpta import TlValueError
+    eng = engine_for(small_model)
+    with pytest.raises(TlValueError):
+        eng.prefill(np.array([], np.int32))
+    with pytest.raises(TlValueError):
+        eng.prefill(np.array([small_model.cfg["vocab"]], np.int32))
+    with pytest.raises(TlValueError):
+        eng.generate(np.arange(10, dtype=np.int32), small_model.cfg["max_pos"])
+    with pytest.raises(TlValueError):
+        eng.decode(1, seq=0)  # nothing prefilled
+    eng.close()
