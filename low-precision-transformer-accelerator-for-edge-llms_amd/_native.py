@@ -101,6 +101,19 @@ def header_symbols(path: str = HEADER) -> list[str]:
 _lib = None
 
 
+def _bind_torch_runtime() -> None:
+    """PyTorch-ROCm ships its own HIP runtime (SONAME libamdhip64.so.7) and
+    loads it under another file name.  Importing torch before this library
+    makes the dynamic linker resolve our libamdhip64.so.7 dependency to that
+    already-loaded copy, so the process has a single HIP runtime and torch
+    device pointers are valid here.  Without torch the library binds to the
+    system ROCm runtime."""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 def library_path() -> str:
     return LIB_PATH
 
@@ -112,6 +125,7 @@ def load_library() -> C.CDLL:
         return _lib
     if not os.path.exists(LIB_PATH):
         raise RuntimeError(f"{LIB_PATH} is missing: build the HIP library first (__graft_entry__.build())")
+    _bind_torch_runtime()
     L = C.CDLL(LIB_PATH)
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(L, name)
@@ -166,9 +180,10 @@ class Runtime:
             raise cls(status, f"{what}: {msg}" if what else msg)
 
     def call(self, name: str, *args) -> None:
+        """Call tl_<name>(h, *args): tensors and arrays become their addresses,
+        everything else (ints, floats, ctypes objects, None) passes through."""
         fn = getattr(self.lib, name)
-        conv = [_addr(a) if not isinstance(a, (C._SimpleCData, C.Array, C._Pointer)) and not isinstance(a, float) else a
-                for a in args]
+        conv = [_addr(a) if hasattr(a, "data_ptr") or hasattr(a, "__array_interface__") else a for a in args]
         self.check(fn(self.h, *conv), name)
 
     # ---- model state -------------------------------------------------------

@@ -24,7 +24,7 @@ HEADERS = ["tl_internal.h", os.path.join(ROOT, "include", "tl_int8.h")]
 # oracle) rounds.  The packed-fp32 target feature is switched off for the
 # device code so that no v_pk_*_f32 instructions are generated.
 HIPCC_FLAGS = [
-    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
+    "--offload-arch=gfx950", "-mcode-object-version=5", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function", "-Wno-unused-result",
 ]
