@@ -1,0 +1,574 @@
+// tl_decode.hip -- fused kernels of the batch-1 decode step (five kernels per
+// decoder layer, each ending at one of the global reductions the reference's
+// per-tensor activation quantization requires):
+//
+//   gemv_fused<RMSNORM, DEQUANT>   x -> RMSNorm -> INT8 -> Q|K|V projections
+//   attention_decode               RoPE, Q to INT8, K/V to the cache, GQA attention
+//   gemv_fused<QUANT, DEQUANT_RES> attended -> INT8 -> O projection + residual
+//   gemv_fused<RMSNORM, GLU>       x -> RMSNorm -> INT8 -> gate/up -> SiLU(gate)*up
+//   gemv_fused<QUANT, DEQUANT_RES> hidden -> INT8 -> down projection + residual
+//
+// Every workgroup of a fused GEMV first issues the global loads of its
+// activation row, then all of its weight rows (one 128-bit load per lane per
+// KiB of row), and only then runs the prologue (RMSNorm / quantization of the
+// activation into LDS), so the weight stream is in flight while the prologue
+// computes.  The prologue is the same arithmetic as the standalone kernels
+// (NumPy pairwise tree for the sum of squares, float64 scale), so results are
+// bit-identical to them and to the CPU oracle.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "tl_device.h"
+#include "tl_internal.h"
+
+namespace tl {
+
+constexpr int kNT = 256;   // threads per workgroup of the fused GEMV
+constexpr int kNW = kNT / 64;
+
+// ---------------------------------------------------------------------------
+// activation prologues: f32 row (K elements, 4 per float4 chunk) -> INT8 row
+// in LDS (natural byte order) + its float64 scale
+// ---------------------------------------------------------------------------
+template <int KCH>
+TL_DEV void prologue_quant(const float4 (&xv)[KCH], int K, int8_t* xs8, float* red, double* xscale) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float mx = 0.0f;
+#pragma unroll
+    for (int c = 0; c < KCH; c++) {
+        if ((c * kNT + tid) * 4 < K) {
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(xv[c].x), fabsf(xv[c].y)), fmaxf(fabsf(xv[c].z), fabsf(xv[c].w))));
+        }
+    }
+    mx = wave_max_f32(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const double s = quant_scale(mx);
+    const float sf = (float)s;
+#pragma unroll
+    for (int c = 0; c < KCH; c++) {
+        const int idx = c * kNT + tid;
+        if (idx * 4 < K) {
+            const unsigned b0 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(xv[c].x, sf)));
+            const unsigned b1 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(xv[c].y, sf)));
+            const unsigned b2 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(xv[c].z, sf)));
+            const unsigned b3 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(xv[c].w, sf)));
+            ((unsigned*)xs8)[idx] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+        }
+    }
+    if (tid == 0) *xscale = s;
+    __syncthreads();
+}
+
+template <int KCH>
+TL_DEV void prologue_rmsnorm(const float4 (&xv)[KCH], const float4 (&gv)[KCH], int K, float eps, PwPlan plan,
+                             float* sq, float* part, int8_t* xs8, float* red, double* xscale) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+    for (int c = 0; c < KCH; c++) {
+        const int idx = c * kNT + tid;
+        if (idx * 4 < K) {
+            float4 q;
+            q.x = xv[c].x * xv[c].x;
+            q.y = xv[c].y * xv[c].y;
+            q.z = xv[c].z * xv[c].z;
+            q.w = xv[c].w * xv[c].w;
+            ((float4*)sq)[idx] = q;
+        }
+    }
+    __syncthreads();
+    // NumPy pairwise tree: eight strided accumulators per leaf ...
+    const int L = plan.n_leaves, len = plan.leaf_len;
+    for (int p = tid; p < 8 * L; p += kNT) {
+        const float* a = sq + (p >> 3) * len;
+        const int j = p & 7;
+        float r = a[j];
+        for (int i = 8; i < len; i += 8) r = r + a[i + j];
+        part[p] = r;
+    }
+    __syncthreads();
+    // ... combined per leaf, then leaves pairwise across lanes of wave 0
+    if (wave == 0) {
+        float v = 0.0f;
+        if (lane < L) {
+            const float* r = part + 8 * lane;
+            v = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+        }
+        for (int off = 1; off < L; off <<= 1) v = v + __shfl_xor(v, off);
+        if (lane == 0) red[8] = v;
+    }
+    __syncthreads();
+    const float var = __fdiv_rn(red[8], (float)K);
+    const float inv = __fdiv_rn(1.0f, __builtin_sqrtf(var + eps));
+    float4 av[KCH];
+    float mx = 0.0f;
+#pragma unroll
+    for (int c = 0; c < KCH; c++) {
+        if ((c * kNT + tid) * 4 < K) {
+            av[c].x = (xv[c].x * inv) * gv[c].x;
+            av[c].y = (xv[c].y * inv) * gv[c].y;
+            av[c].z = (xv[c].z * inv) * gv[c].z;
+            av[c].w = (xv[c].w * inv) * gv[c].w;
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(av[c].x), fabsf(av[c].y)), fmaxf(fabsf(av[c].z), fabsf(av[c].w))));
+        }
+    }
+    mx = wave_max_f32(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const double s = quant_scale(mx);
+    const float sf = (float)s;
+#pragma unroll
+    for (int c = 0; c < KCH; c++) {
+        const int idx = c * kNT + tid;
+        if (idx * 4 < K) {
+            const unsigned b0 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(av[c].x, sf)));
+            const unsigned b1 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(av[c].y, sf)));
+            const unsigned b2 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(av[c].z, sf)));
+            const unsigned b3 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(av[c].w, sf)));
+            ((unsigned*)xs8)[idx] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+        }
+    }
+    if (tid == 0) *xscale = s;
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// fused decode GEMV: y = epilogue(W . prologue(x)); 4 wavefronts x R rows
+// ---------------------------------------------------------------------------
+template <int PRO, int EPI, int R, int KCH>
+__global__ __launch_bounds__(kNT) void gemv_fused_kernel(GemvArgs a) {
+    constexpr int NM = (EPI == EPI_GLU) ? 2 : 1;
+    __shared__ __align__(16) int8_t xs8[KCH * 1024];
+    __shared__ __align__(16) float sq[PRO == PRO_RMSNORM ? KCH * 1024 : 4];
+    __shared__ float part[PRO == PRO_RMSNORM ? 8 * 64 : 4];
+    __shared__ float red[16];
+    __shared__ double xscale;
+    __shared__ unsigned long long wbest[kNW];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int K = a.k;
+    const int row0 = (blockIdx.x * kNW + wave) * R;
+    const int4 zero = make_int4(0, 0, 0, 0);
+
+    // 1) activation row first ...
+    float4 xv[KCH], gv[KCH];
+    int4 xr[KCH];
+    if (PRO == PRO_X8) {
+#pragma unroll
+        for (int c = 0; c < KCH; c++) {
+            const int off = c * 1024 + lane * 16;
+            xr[c] = off < K ? *(const int4*)(a.x + off) : zero;
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < KCH; c++) {
+            const int idx = c * kNT + tid;
+            xv[c] = idx * 4 < K ? ((const float4*)a.xf)[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+            if (PRO == PRO_RMSNORM) gv[c] = idx * 4 < K ? ((const float4*)a.gamma)[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    // 2) ... then every weight row of this wavefront
+    int4 wv[NM][R][KCH];
+#pragma unroll
+    for (int m = 0; m < NM; m++) {
+        const int8_t* wb = m ? a.w2 : a.w;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int8_t* wr = wb + (int64_t)min(row0 + r, a.n - 1) * K;
+#pragma unroll
+            for (int c = 0; c < KCH; c++) {
+                const int off = c * 1024 + lane * 16;
+                wv[m][r][c] = off < K ? *(const int4*)(wr + off) : zero;
+            }
+        }
+    }
+    // 3) prologue while the weights stream in
+    double sx;
+    if (PRO == PRO_X8) {
+        sx = a.xs[0];
+    } else {
+        if (PRO == PRO_QUANT) prologue_quant<KCH>(xv, K, xs8, red, &xscale);
+        else prologue_rmsnorm<KCH>(xv, gv, K, a.eps, a.plan, sq, part, xs8, red, &xscale);
+        sx = xscale;
+#pragma unroll
+        for (int c = 0; c < KCH; c++) {
+            const int off = c * 1024 + lane * 16;
+            xr[c] = off < K ? *(const int4*)(xs8 + off) : zero;
+        }
+    }
+    // 4) dot products and wavefront reductions (exact integers)
+    int acc[NM][R];
+#pragma unroll
+    for (int m = 0; m < NM; m++)
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            int s = 0;
+#pragma unroll
+            for (int c = 0; c < KCH; c++) s = sdot4x4(wv[m][r][c], xr[c], s);
+            acc[m][r] = wave_sum_i32(s);
+        }
+    // 5) epilogue
+    if (EPI == EPI_ARGMAX) {
+        unsigned long long best = 0;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int n = row0 + r;
+            if (n < a.n) {
+                const float logit = (float)acc[0][r] * deq_mult(sx, a.ws[n]);
+                if (a.y && lane == 0) a.y[n] = logit;
+                const unsigned long long k = argmax_key(logit, n);
+                best = k > best ? k : best;
+            }
+        }
+        if (lane == 0) wbest[wave] = best;
+        __syncthreads();
+        if (tid == 0) {
+            unsigned long long b = wbest[0];
+            for (int i = 1; i < kNW; i++) b = wbest[i] > b ? wbest[i] : b;
+            if (b) atomicMax(a.key, b);
+        }
+        return;
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int n = row0 + r;
+        if (lane != r || n >= a.n) continue;
+        if (EPI == EPI_DEQUANT || EPI == EPI_DEQUANT_RES) {
+            float v = (float)acc[0][r] * deq_mult(sx, a.ws[n]);
+            if (EPI == EPI_DEQUANT_RES) v = a.residual[n] + v;
+            a.y[n] = v;
+        } else if (EPI == EPI_GLU) {
+            const float gt = (float)acc[0][r] * deq_mult(sx, a.ws[n]);
+            const float up = (float)acc[NM - 1][r] * deq_mult(sx, a.ws2[n]);
+            a.y[n] = tl_silu(gt) * up;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// decode attention with the Q/K/V post-processing fused in.  One workgroup
+// per (row, HPW query heads); for query position pos the keys are 0..pos, of
+// which 0..pos-1 are read from the cache and pos is this step's own row,
+// computed here: RoPE (TL:69-80) on Q and K, Q quantized at the row's scale
+// (max over all heads), K and V at the static per-layer/per-KV-head scales.
+// The first workgroup of each KV head writes that row to the cache.
+// ---------------------------------------------------------------------------
+struct AttnDecodeArgs {
+    const float* qkv;     // [rows][D + 2 KVD]
+    int32_t n_heads, n_kv;
+    RowMap rm;
+    const float* cosb;
+    const float* sinb;
+    KvGeom kv;
+    int32_t layer;
+    const float* kv_sk;
+    const float* kv_sv;
+    double attn_scale;
+    float* out;           // [rows][D]
+};
+
+template <int HPW>
+__global__ __launch_bounds__(256) void attention_decode_kernel(AttnDecodeArgs p) {
+    extern __shared__ __align__(16) float dyn[];
+    __shared__ __align__(16) int8_t qs[HPW][64];
+    __shared__ __align__(16) int8_t knew[64];
+    __shared__ __align__(16) int8_t vnew[64];
+    __shared__ float red[16];
+    __shared__ float scl[HPW], mrow[HPW], tot[HPW];
+    __shared__ float wmax[4][HPW];
+    __shared__ int accs[4][HPW][64];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int G = p.n_heads / p.n_kv;
+    int hb = blockIdx.x;
+    if (HPW == 1 && p.n_heads == 32 && p.n_kv == 4) {
+        // keep the 8 query heads of a KV head on two XCDs (workgroups are
+        // dispatched round-robin over the 8 XCDs) so its K/V rows are shared
+        // through their L2 caches
+        const int xcd = hb & 7, slot = hb >> 3;
+        hb = (xcd >> 1) * 8 + (xcd & 1) * 4 + slot;
+    }
+    const int h0 = hb * HPW;
+    const int g = h0 / G;
+    const int row = blockIdx.y;
+    const int D = p.n_heads * kHeadDim, KVD = p.n_kv * kHeadDim, W = D + 2 * KVD;
+    const int pos = p.rm.pos[row], seq = p.rm.seq[row];
+    const int T = pos + 1;
+    const int tpad = (T + 63) & ~63;
+    const int nblk = tpad >> 6;
+
+    float* v = dyn;                          // [W] this row's q|k|v
+    float* s_buf = dyn + W;                  // [HPW][tpad] scores, then exps
+    int8_t* p8 = (int8_t*)(s_buf + HPW * tpad);
+    float* bsum = (float*)(p8 + HPW * tpad); // [HPW][nblk]
+
+    const float* src = p.qkv + (int64_t)row * W;
+    for (int i = tid; i < W / 4; i += blockDim.x) ((float4*)v)[i] = ((const float4*)src)[i];
+    __syncthreads();
+
+    const float* cp = p.cosb + (int64_t)pos * kHeadDim;
+    const float* sp = p.sinb + (int64_t)pos * kHeadDim;
+    // RoPE of every Q element (the row's scale is the max over all heads)
+    float mx = 0.0f;
+    float qr[(32 * 64 + 255) / 256];
+#pragma unroll
+    for (int k = 0; k < (32 * 64 + 255) / 256; k++) {
+        const int i = tid + k * 256;
+        qr[k] = 0.0f;
+        if (i < D) {
+            const int d = i & 63;
+            const float rot = d < 32 ? -v[i + 32] : v[i - 32];
+            qr[k] = (v[i] * cp[d]) + (rot * sp[d]);
+            mx = fmaxf(mx, fabsf(qr[k]));
+        }
+    }
+    for (int i = tid + 8 * 256; i < D; i += 256) {   // heads beyond 32 (not TinyLlama)
+        const int d = i & 63;
+        const float rot = d < 32 ? -v[i + 32] : v[i - 32];
+        mx = fmaxf(mx, fabsf((v[i] * cp[d]) + (rot * sp[d])));
+    }
+    mx = wave_max_f32(mx);
+    if (lane == 0) red[wave] = mx;
+    // this row's K (after RoPE) and V of KV head g, quantized at the static scales
+    const float sk = p.kv_sk[p.layer * p.n_kv + g], sv = p.kv_sv[p.layer * p.n_kv + g];
+    if (tid < 64) {
+        const int i = D + g * 64 + tid, d = tid;
+        const float rot = d < 32 ? -v[i + 32] : v[i - 32];
+        const float kr = (v[i] * cp[d]) + (rot * sp[d]);
+        knew[d] = sat_i8(__builtin_rintf(__fdiv_rn(kr, sk)));
+    } else if (tid < 128) {
+        const int d = tid - 64;
+        vnew[d] = sat_i8(__builtin_rintf(__fdiv_rn(v[D + KVD + g * 64 + d], sv)));
+    }
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const double s_q = quant_scale(mx);
+    const float sfq = (float)s_q;
+#pragma unroll
+    for (int k = 0; k < (32 * 64 + 255) / 256; k++) {
+        const int i = tid + k * 256;
+        if (i >= h0 * 64 && i < (h0 + HPW) * 64) qs[(i >> 6) - h0][i & 63] = sat_i8(__builtin_rintf(__fdiv_rn(qr[k], sfq)));
+    }
+    for (int i = tid + 8 * 256; i < D; i += 256) {
+        if (i >= h0 * 64 && i < (h0 + HPW) * 64) {
+            const int d = i & 63;
+            const float rot = d < 32 ? -v[i + 32] : v[i - 32];
+            qs[(i >> 6) - h0][d] = sat_i8(__builtin_rintf(__fdiv_rn((v[i] * cp[d]) + (rot * sp[d]), sfq)));
+        }
+    }
+    if (tid < HPW) scl[tid] = (float)((s_q * (double)sk) * p.attn_scale);
+    const int64_t pl = p.kv.plane(seq, p.layer, g);
+    if (h0 % G == 0 && tid < 64) {
+        p.kv.k[pl + KvGeom::k_off(pos, tid)] = knew[tid];
+        p.kv.v[pl + KvGeom::v_off(pos, tid)] = vnew[tid];
+    }
+    __syncthreads();
+
+    const int8_t* kp = p.kv.k + pl;
+    const int8_t* vp = p.kv.v + pl;
+    // scores: lane <-> key inside a block of 64
+    float lmax[HPW];
+#pragma unroll
+    for (int h = 0; h < HPW; h++) lmax[h] = -INFINITY;
+    for (int b = wave; b < nblk; b += 4) {
+        const int t = b * 64 + lane;
+        if (t < T) {
+            int4 k0, k1, k2, k3;
+            if (t < pos) {
+                const int8_t* kb = kp + (int64_t)b * 4096 + lane * 16;
+                k0 = *(const int4*)(kb);
+                k1 = *(const int4*)(kb + 1024);
+                k2 = *(const int4*)(kb + 2048);
+                k3 = *(const int4*)(kb + 3072);
+            } else {
+                k0 = ((const int4*)knew)[0];
+                k1 = ((const int4*)knew)[1];
+                k2 = ((const int4*)knew)[2];
+                k3 = ((const int4*)knew)[3];
+            }
+#pragma unroll
+            for (int h = 0; h < HPW; h++) {
+                const int4* q4 = (const int4*)qs[h];
+                int S = sdot4x4(k0, q4[0], 0);
+                S = sdot4x4(k1, q4[1], S);
+                S = sdot4x4(k2, q4[2], S);
+                S = sdot4x4(k3, q4[3], S);
+                const float sv2 = (float)S * scl[h];
+                s_buf[h * tpad + t] = sv2;
+                lmax[h] = fmaxf(lmax[h], sv2);
+            }
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < HPW; h++) {
+        const float m = wave_max_f32(lmax[h]);
+        if (lane == 0) wmax[wave][h] = m;
+    }
+    __syncthreads();
+    if (tid < HPW) mrow[tid] = fmaxf(fmaxf(wmax[0][tid], wmax[1][tid]), fmaxf(wmax[2][tid], wmax[3][tid]));
+    __syncthreads();
+    // exponentials and the block-64 butterfly sums
+    for (int b = wave; b < nblk; b += 4) {
+        const int t = b * 64 + lane;
+#pragma unroll
+        for (int h = 0; h < HPW; h++) {
+            float e = 0.0f;
+            if (t < T) {
+                e = tl_expf(s_buf[h * tpad + t] - mrow[h]);
+                s_buf[h * tpad + t] = e;
+            }
+            const float bs = wave_butterfly_sum(e);
+            if (lane == 0) bsum[h * nblk + b] = bs;
+        }
+    }
+    __syncthreads();
+    if (tid < HPW) {
+        float total = 0.0f;
+        for (int b = 0; b < nblk; b++) total = total + bsum[tid * nblk + b];
+        tot[tid] = total;
+    }
+    __syncthreads();
+    for (int t = tid; t < tpad; t += blockDim.x) {
+#pragma unroll
+        for (int h = 0; h < HPW; h++) {
+            int8_t pq = 0;
+            if (t < T) {
+                float pr = __builtin_rintf(__fdiv_rn(s_buf[h * tpad + t], tot[h]) * 127.0f);
+                pr = pr < 0.0f ? 0.0f : (pr > 127.0f ? 127.0f : pr);
+                pq = (int8_t)(int)pr;
+            }
+            p8[h * tpad + t] = pq;
+        }
+    }
+    __syncthreads();
+    // O = P8 . V8, lane <-> dimension; this row's V comes from vnew
+    int o[HPW];
+#pragma unroll
+    for (int h = 0; h < HPW; h++) o[h] = 0;
+    const int ngrp = tpad >> 4;
+    const int cpos = pos >> 4, bpos = pos & 15;
+    for (int c = wave; c < ngrp; c += 4) {
+        int4 vv = *(const int4*)(vp + (int64_t)c * 1024 + lane * 16);
+        if (c == cpos) {
+            const unsigned nb = (uint8_t)vnew[lane];
+            const int sh = (bpos & 3) * 8;
+            const unsigned keep = ~(0xFFu << sh);
+            int* comp = (bpos >> 2) == 0 ? &vv.x : (bpos >> 2) == 1 ? &vv.y : (bpos >> 2) == 2 ? &vv.z : &vv.w;
+            *comp = (int)(((unsigned)*comp & keep) | (nb << sh));
+        }
+#pragma unroll
+        for (int h = 0; h < HPW; h++) o[h] = sdot4x4(vv, *(const int4*)(p8 + h * tpad + c * 16), o[h]);
+    }
+#pragma unroll
+    for (int h = 0; h < HPW; h++) accs[wave][h][lane] = o[h];
+    __syncthreads();
+    const float pv_mult = deq_mult(1.0 / 127.0, sv);
+    for (int i = tid; i < HPW * 64; i += blockDim.x) {
+        const int h = i >> 6, d = i & 63;
+        const int O = accs[0][h][d] + accs[1][h][d] + accs[2][h][d] + accs[3][h][d];
+        p.out[(int64_t)row * D + (int64_t)(h0 + h) * kHeadDim + d] = (float)O * pv_mult;
+    }
+}
+
+// embedding of each row's current token and the row's position (= its
+// sequence's cursor) for this step
+__global__ __launch_bounds__(256) void embed_step_kernel(const int32_t* __restrict__ tok_by_seq,
+                                                         const int32_t* __restrict__ seq_of_row,
+                                                         const int32_t* __restrict__ cursor,
+                                                         int32_t* __restrict__ row_pos, int32_t d, int32_t vocab,
+                                                         const int8_t* __restrict__ emb,
+                                                         const float* __restrict__ emb_s, float* __restrict__ x) {
+    const int row = blockIdx.x;
+    const int seq = seq_of_row[row];
+    const int tok = tok_by_seq[seq];
+    if (threadIdx.x == 0) row_pos[row] = cursor[seq];
+    if (tok < 0 || tok >= vocab) {
+        for (int i = threadIdx.x; i < d; i += blockDim.x) x[(int64_t)row * d + i] = 0.0f;
+        return;
+    }
+    const int8_t* e = emb + (int64_t)tok * d;
+    const float s = emb_s[tok];
+    for (int i = threadIdx.x; i < d; i += blockDim.x) x[(int64_t)row * d + i] = (float)e[i] * s;
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+static inline int cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+
+template <int PRO, int EPI, int R>
+static hipError_t gemv_fused_r(hipStream_t s, const GemvArgs& a) {
+    const int kch = cdiv(a.k, 1024);
+    const dim3 grid(cdiv(a.n, kNW * R)), block(kNT);
+    switch (kch) {
+        case 1: hipLaunchKernelGGL((gemv_fused_kernel<PRO, EPI, R, 1>), grid, block, 0, s, a); break;
+        case 2: hipLaunchKernelGGL((gemv_fused_kernel<PRO, EPI, R, 2>), grid, block, 0, s, a); break;
+        case 3: hipLaunchKernelGGL((gemv_fused_kernel<PRO, EPI, R, 3>), grid, block, 0, s, a); break;
+        case 4: hipLaunchKernelGGL((gemv_fused_kernel<PRO, EPI, R, 4>), grid, block, 0, s, a); break;
+        case 5: hipLaunchKernelGGL((gemv_fused_kernel<PRO, EPI, R, 5>), grid, block, 0, s, a); break;
+        case 6: hipLaunchKernelGGL((gemv_fused_kernel<PRO, EPI, R, 6>), grid, block, 0, s, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_fused(hipStream_t s, int pro, int epi, const GemvArgs& a) {
+    if (a.n <= 0) return hipSuccess;
+    if (a.k <= 0 || a.k % 64 != 0 || a.k > 6 * 1024) return hipErrorInvalidValue;
+    if (pro == PRO_RMSNORM && (a.plan.n_leaves > 64 || a.plan.leaf_len * a.plan.n_leaves != a.k)) return hipErrorInvalidValue;
+    const int kch = cdiv(a.k, 1024);
+#define TL_GO(P, E, R) return gemv_fused_r<P, E, R>(s, a)
+    if (pro == PRO_RMSNORM) {
+        if (epi == EPI_DEQUANT) { if (kch <= 2) TL_GO(PRO_RMSNORM, EPI_DEQUANT, 2); TL_GO(PRO_RMSNORM, EPI_DEQUANT, 1); }
+        if (epi == EPI_GLU) { if (kch <= 2) TL_GO(PRO_RMSNORM, EPI_GLU, 3); TL_GO(PRO_RMSNORM, EPI_GLU, 1); }
+        if (epi == EPI_ARGMAX) { if (kch <= 2) TL_GO(PRO_RMSNORM, EPI_ARGMAX, 8); TL_GO(PRO_RMSNORM, EPI_ARGMAX, 2); }
+    } else if (pro == PRO_QUANT) {
+        if (epi == EPI_DEQUANT_RES) { if (kch <= 2) TL_GO(PRO_QUANT, EPI_DEQUANT_RES, 2); TL_GO(PRO_QUANT, EPI_DEQUANT_RES, 1); }
+        if (epi == EPI_DEQUANT) { if (kch <= 2) TL_GO(PRO_QUANT, EPI_DEQUANT, 2); TL_GO(PRO_QUANT, EPI_DEQUANT, 1); }
+    }
+#undef TL_GO
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_attention_decode(hipStream_t s, const float* qkv, int32_t rows, int32_t n_heads, int32_t n_kv,
+                                   RowMap rm, const float* cos, const float* sin, KvGeom kv, int32_t layer,
+                                   const float* kv_sk, const float* kv_sv, float* out, int32_t max_t, int32_t hpw) {
+    if (rows <= 0) return hipSuccess;
+    const int G = n_heads / n_kv;
+    if (n_heads % n_kv || G > kMaxGroupHeads || n_heads > 32 * 4) return hipErrorInvalidValue;
+    const int D = n_heads * kHeadDim, W = D + 2 * n_kv * kHeadDim;
+    const int tpad = (max_t + 63) & ~63;
+    AttnDecodeArgs p{qkv, n_heads, n_kv, rm, cos, sin, kv, layer, kv_sk, kv_sv, 1.0 / sqrt((double)kHeadDim), out};
+    if (hpw == 1) {
+        const size_t lds = sizeof(float) * W + (size_t)tpad * 4 + tpad + (tpad / 64) * 4 + 64;
+        hipLaunchKernelGGL(attention_decode_kernel<1>, dim3(n_heads, rows), dim3(256), lds, s, p);
+    } else if (hpw == 8 && G == 8) {
+        const size_t lds = sizeof(float) * W + (size_t)8 * tpad * 4 + 8 * tpad + 8 * (tpad / 64) * 4 + 64;
+        hipLaunchKernelGGL(attention_decode_kernel<8>, dim3(n_heads / 8, rows), dim3(256), lds, s, p);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_step(hipStream_t s, const int32_t* tok_by_seq, const int32_t* seq_of_row, int32_t rows,
+                             const int32_t* cursor, int32_t* row_pos, int32_t d, int32_t vocab, const int8_t* emb,
+                             const float* emb_s, float* x) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(embed_step_kernel, dim3(rows), dim3(256), 0, s, tok_by_seq, seq_of_row, cursor, row_pos, d,
+                       vocab, emb, emb_s, x);
+    return hipGetLastError();
+}
+
+hipError_t init_decode_kernels() {
+    hipError_t e = hipFuncSetAttribute((const void*)attention_decode_kernel<8>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 120 * 1024);
+    if (e != hipSuccess) return e;
+    return hipFuncSetAttribute((const void*)attention_decode_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               64 * 1024);
+}
+
+}  // namespace tl

@@ -59,7 +59,20 @@ enum GemvEpi : int {
     EPI_RAW = 5,          // acc only
 };
 
+// activation prologue of the fused decode GEMV
+enum GemvPro : int {
+    PRO_X8 = 0,       // x is already INT8 with its scale
+    PRO_QUANT = 1,    // x float32 -> per-tensor INT8 (GI:36-42)
+    PRO_RMSNORM = 2,  // x float32 -> RMSNorm (TL:45-50) -> INT8
+};
+
+constexpr int kMaxGroupHeads = 8;
+
 struct GemvArgs {
+    const float* xf;         // [K] float32 activation (fused prologues)
+    const float* gamma;      // [K] RMSNorm gain (PRO_RMSNORM)
+    float eps;
+    PwPlan plan;
     const int8_t* w;         // [N][K]
     const int8_t* w2;        // [N][K] up weights (EPI_GLU)
     const float* ws;         // [N] weight scales or requant multipliers
@@ -122,6 +135,14 @@ hipError_t launch_finalize_tokens(hipStream_t s, unsigned long long* keys, int32
 hipError_t launch_argmax_rows(hipStream_t s, const float* logits, int32_t rows, int32_t n,
                               unsigned long long* keys);
 hipError_t init_kernels();
+hipError_t init_decode_kernels();
+hipError_t launch_gemv_fused(hipStream_t s, int pro, int epi, const GemvArgs& a);
+hipError_t launch_attention_decode(hipStream_t s, const float* qkv, int32_t rows, int32_t n_heads, int32_t n_kv,
+                                   RowMap rm, const float* cos, const float* sin, KvGeom kv, int32_t layer,
+                                   const float* kv_sk, const float* kv_sv, float* out, int32_t max_t, int32_t hpw);
+hipError_t launch_embed_step(hipStream_t s, const int32_t* tok_by_seq, const int32_t* seq_of_row, int32_t rows,
+                             const int32_t* cursor, int32_t* row_pos, int32_t d, int32_t vocab, const int8_t* emb,
+                             const float* emb_s, float* x);
 hipError_t launch_step_rows(hipStream_t s, const int32_t* seq_of_row, int32_t rows,
                             const int32_t* cursor, int32_t* row_pos);
 hipError_t launch_kv_scatter(hipStream_t s, KvGeom kv, int32_t seq, int32_t layer, int32_t g,

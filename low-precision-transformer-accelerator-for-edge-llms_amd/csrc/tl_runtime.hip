@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -98,6 +99,9 @@ struct tl_handle {
 
     std::vector<void*> allocs;
     std::string err;
+
+    bool use_graphs = true;
+    std::vector<hipGraphExec_t> graphs;   // captured batch-1 decode step per sequence
 
     bool profiling = false;
     std::vector<ProfEvent> prof_pending;
@@ -283,9 +287,60 @@ int32_t linear(tl_handle* h, int epi, int rows, const int8_t* x8, const double* 
 
 RowMap rowmap(tl_handle* h) { return RowMap{h->row_seq, h->row_pos}; }
 
+GemvArgs gemv_args(const tl_handle* h) {
+    GemvArgs g{};
+    g.eps = h->cfg.rms_eps;
+    g.plan = h->plan;
+    return g;
+}
+
+// one decoder layer (GI:256-281) for a single row (batch-1 decode or a
+// one-token prefill) as five fused kernels; the row's sequence and position
+// are in h->row_seq[0] / h->row_pos[0]; max_t bounds pos + 1
+int32_t layer_row1(tl_handle* h, int32_t layer, int32_t max_t) {
+    const tl_config& c = h->cfg;
+    const LayerDev& L = h->layers[layer];
+    const int D = h->D, F = h->F, QKV = h->QKV;
+    {
+        GemvArgs g = gemv_args(h);
+        g.xf = h->x; g.gamma = L.g_in; g.w = L.wqkv; g.ws = L.sqkv; g.y = h->qkv; g.n = QKV; g.k = D;
+        Prof p(h, TL_K_QKV, (double)QKV * D + QKV * 8.0 + D * 8.0);
+        TL_LAUNCH(h, launch_gemv_fused(h->stream, PRO_RMSNORM, EPI_DEQUANT, g));
+    }
+    {
+        Prof p(h, TL_K_ATTN, (double)c.n_heads * max_t * 128.0 + QKV * 4.0 + D * 4.0);
+        TL_LAUNCH(h, launch_attention_decode(h->stream, h->qkv, 1, c.n_heads, c.n_kv_heads, rowmap(h), h->rope_cos,
+                                             h->rope_sin, h->kv, layer, h->kv_sk, h->kv_sv, h->att, max_t, 1));
+    }
+    {
+        GemvArgs g = gemv_args(h);
+        g.xf = h->att; g.w = L.wo; g.ws = L.so; g.residual = h->x; g.y = h->x; g.n = D; g.k = D;
+        Prof p(h, TL_K_O, (double)D * D + D * 4.0 + D * 12.0);
+        TL_LAUNCH(h, launch_gemv_fused(h->stream, PRO_QUANT, EPI_DEQUANT_RES, g));
+    }
+    {
+        GemvArgs g = gemv_args(h);
+        g.xf = h->x; g.gamma = L.g_post; g.w = L.wg; g.w2 = L.wu; g.ws = L.sg; g.ws2 = L.su; g.y = h->hid;
+        g.n = F; g.k = D;
+        Prof p(h, TL_K_GLU, 2.0 * F * D + F * 8.0 + D * 8.0 + F * 4.0);
+        TL_LAUNCH(h, launch_gemv_fused(h->stream, PRO_RMSNORM, EPI_GLU, g));
+    }
+    {
+        GemvArgs g = gemv_args(h);
+        g.xf = h->hid; g.w = L.wd; g.ws = L.sd; g.residual = h->x; g.y = h->x; g.n = D; g.k = F;
+        Prof p(h, TL_K_DOWN, (double)D * F + D * 4.0 + F * 4.0 + D * 8.0);
+        TL_LAUNCH(h, launch_gemv_fused(h->stream, PRO_QUANT, EPI_DEQUANT_RES, g));
+    }
+    return TL_OK;
+}
+
 // one decoder layer (GI:256-281) for `rows` rows of h->x whose sequence and
-// position are in h->row_seq / h->row_pos; max_t bounds pos + 1 over the rows
-int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t) {
+// position are in h->row_seq / h->row_pos; max_t bounds pos + 1 over the rows.
+// decode: every row is a different sequence (its own K/V row is appended by
+// the attention kernel); otherwise the rows are consecutive prompt positions
+// of one sequence (all appended before attention reads them).
+int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, bool decode) {
+    if (rows == 1) return layer_row1(h, layer, max_t);
     const tl_config& c = h->cfg;
     const LayerDev& L = h->layers[layer];
     const int D = h->D, F = h->F, KVD = h->KVD, QKV = h->QKV;
@@ -296,12 +351,18 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t) {
     }
     if ((r = linear(h, EPI_DEQUANT, rows, h->a8, h->as, L.wqkv, L.sqkv, nullptr, nullptr, QKV, D, nullptr, h->qkv, TL_K_QKV)))
         return r;
-    {
-        Prof p(h, TL_K_ATTN, (double)rows * (QKV * 4.0 + D) + (double)rows * KVD * 2.0);
-        TL_LAUNCH(h, launch_qkv_post(h->stream, h->qkv, rows, c.n_heads, c.n_kv_heads, rowmap(h), h->rope_cos,
-                                     h->rope_sin, h->kv, layer, h->kv_sk, h->kv_sv, h->q8, h->qs, nullptr));
-    }
-    {
+    if (decode) {
+        const int G = c.n_heads / c.n_kv_heads;
+        Prof p(h, TL_K_ATTN, (double)rows * c.n_kv_heads * (double)max_t * 128.0 + rows * QKV * 4.0);
+        TL_LAUNCH(h, launch_attention_decode(h->stream, h->qkv, rows, c.n_heads, c.n_kv_heads, rowmap(h), h->rope_cos,
+                                             h->rope_sin, h->kv, layer, h->kv_sk, h->kv_sv, h->att, max_t,
+                                             G == 8 ? 8 : 1));
+    } else {
+        {
+            Prof p(h, TL_K_ATTN, (double)rows * (QKV * 4.0 + D) + (double)rows * KVD * 2.0);
+            TL_LAUNCH(h, launch_qkv_post(h->stream, h->qkv, rows, c.n_heads, c.n_kv_heads, rowmap(h), h->rope_cos,
+                                         h->rope_sin, h->kv, layer, h->kv_sk, h->kv_sv, h->q8, h->qs, nullptr));
+        }
         Prof p(h, TL_K_ATTN, (double)rows * c.n_kv_heads * (double)max_t * 128.0 + rows * D * 5.0);
         TL_LAUNCH(h, launch_attention(h->stream, h->q8, h->qs, rows, c.n_heads, c.n_kv_heads, rowmap(h), h->kv,
                                       layer, h->kv_sk, h->kv_sv, h->att, max_t));
@@ -332,17 +393,17 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t) {
 int32_t lm_head_rows(tl_handle* h, const float* xrow, int32_t rows, int32_t seq, int32_t advance) {
     const tl_config& c = h->cfg;
     const int D = h->D, V = c.vocab;
-    {
-        Prof p(h, TL_K_NORM, (double)rows * D * 9.0);
-        TL_LAUNCH(h, launch_rmsnorm_quant(h->stream, xrow, h->g_final, rows, D, c.rms_eps, h->plan, nullptr, h->a8, h->as));
-    }
     unsigned long long* keys = h->keys + (rows == 1 ? seq : 0);
     if (rows == 1) {
-        GemvArgs g{};
-        g.w = h->lm_w; g.ws = h->lm_s; g.x = h->a8; g.xs = h->as; g.key = keys; g.n = V; g.k = D;
-        Prof p(h, TL_K_LMHEAD, (double)V * D + V * 4.0 + D);
-        TL_LAUNCH(h, launch_gemv(h->stream, EPI_ARGMAX, g));
+        GemvArgs g = gemv_args(h);
+        g.xf = xrow; g.gamma = h->g_final; g.w = h->lm_w; g.ws = h->lm_s; g.key = keys; g.n = V; g.k = D;
+        Prof p(h, TL_K_LMHEAD, (double)V * D + V * 4.0 + D * 8.0);
+        TL_LAUNCH(h, launch_gemv_fused(h->stream, PRO_RMSNORM, EPI_ARGMAX, g));
     } else {
+        {
+            Prof p(h, TL_K_NORM, (double)rows * D * 9.0);
+            TL_LAUNCH(h, launch_rmsnorm_quant(h->stream, xrow, h->g_final, rows, D, c.rms_eps, h->plan, nullptr, h->a8, h->as));
+        }
         // M > 1: MFMA GEMM writes logits, a row argmax folds them into keys
         GemmArgs a{};
         a.a = h->a8; a.w = h->lm_w; a.as = h->as; a.ws = h->lm_s; a.y = h->logits; a.m = rows; a.n = V; a.k = D;
@@ -373,6 +434,44 @@ int32_t upload_rows(tl_handle* h, int32_t rows, int32_t seq_first, bool seq_per_
 int32_t check_model_loaded(tl_handle* h) {
     for (size_t l = 0; l < h->layers.size(); l++)
         if (!h->layers[l].wqkv) return fail(h, TL_ERR_BAD_DESCRIPTOR, "layer " + std::to_string(l) + " not loaded");
+    return TL_OK;
+}
+
+// one batch-1 decode step of sequence seq (row 0 of the workspaces): embed
+// the sequence's current token at its cursor, 22 fused layers, fused LM head +
+// argmax, then record the token and advance the cursor.  Every argument is a
+// fixed device pointer, so the step can be captured once and replayed.
+int32_t decode_step1(tl_handle* h, int32_t seq, int32_t max_t) {
+    const tl_config& c = h->cfg;
+    TL_LAUNCH(h, launch_embed_step(h->stream, h->token_cur, h->row_seq, 1, h->cursor, h->row_pos, h->D, c.vocab,
+                                   h->emb, h->emb_s, h->x));
+    int32_t r;
+    for (int l = 0; l < c.n_layers; l++)
+        if ((r = layer_row1(h, l, max_t))) return r;
+    return lm_head_rows(h, h->x, 1, seq, 1);
+}
+
+int32_t decode_graph_launch(tl_handle* h, int32_t seq) {
+    if ((int)h->graphs.size() < h->max_seqs) h->graphs.assign(h->max_seqs, nullptr);
+    if (!h->graphs[seq]) {
+        hipGraph_t g = nullptr;
+        TL_HIP(h, hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal));
+        int32_t r = decode_step1(h, seq, h->cfg.max_pos);
+        hipGraph_t cap = nullptr;
+        hipError_t e = hipStreamEndCapture(h->stream, &cap);
+        if (r) {
+            if (cap) hipGraphDestroy(cap);
+            return r;
+        }
+        TL_HIP(h, e);
+        g = cap;
+        hipGraphExec_t ex = nullptr;
+        e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+        hipGraphDestroy(g);
+        TL_HIP(h, e);
+        h->graphs[seq] = ex;
+    }
+    TL_HIP(h, hipGraphLaunch(h->graphs[seq], h->stream));
     return TL_OK;
 }
 
@@ -479,6 +578,8 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
         return bad(e);
     h->rope_n = c.max_pos;
     if ((e = init_kernels())) return bad(e);
+    if ((e = init_decode_kernels())) return bad(e);
+    if (const char* env = std::getenv("TL_NO_GRAPHS")) h->use_graphs = env[0] == '0';
     if ((e = hipStreamSynchronize(h->stream))) return bad(e);
     *out = h;
     return TL_OK;
@@ -492,6 +593,8 @@ void tl_destroy(tl_handle* h) {
         hipEventDestroy(p.stop);
     }
     for (auto e : h->event_pool) hipEventDestroy(e);
+    for (auto g : h->graphs)
+        if (g) hipGraphExecDestroy(g);
     for (void* p : h->allocs) hipFree(p);
     if (h->stream) hipStreamDestroy(h->stream);
     delete h;
@@ -812,7 +915,7 @@ int32_t tl_decode_layer(tl_handle* h, int32_t seq, int32_t layer, int32_t pos, f
     int32_t r = upload_rows(h, 1, seq, false, pos);
     if (r) return r;
     TL_HIP(h, hipMemcpyAsync(h->x, x, sizeof(float) * h->D, hipMemcpyDeviceToDevice, h->stream));
-    if ((r = layer_rows(h, layer, 1, pos + 1))) return r;
+    if ((r = layer_rows(h, layer, 1, pos + 1, true))) return r;
     TL_HIP(h, hipMemcpyAsync(x, h->x, sizeof(float) * h->D, hipMemcpyDeviceToDevice, h->stream));
     return finish(h);
 }
@@ -834,7 +937,7 @@ int32_t tl_prefill(tl_handle* h, int32_t seq, const int32_t* tokens, int32_t n, 
     TL_LAUNCH(h, launch_reset_keys(h->stream, h->keys + seq, 1));
     TL_LAUNCH(h, launch_embed(h->stream, h->tokens, n, h->D, h->cfg.vocab, h->emb, h->emb_s, h->x));
     for (int l = 0; l < c.n_layers; l++)
-        if ((r = layer_rows(h, l, n, n))) return r;
+        if ((r = layer_rows(h, l, n, n, false))) return r;
     if ((r = lm_head_rows(h, h->x + (size_t)(n - 1) * h->D, 1, seq, 0))) return r;
     if ((r = finish(h))) return r;
     h->host_cursor[seq] = n;
@@ -864,12 +967,11 @@ int32_t tl_decode(tl_handle* h, int32_t seq, int32_t max_new, int32_t eos_id, co
             if (stop_reason) *stop_reason = TL_STOP_HOST_ABORT;
             break;
         }
-        TL_LAUNCH(h, launch_step_rows(h->stream, h->row_seq, 1, h->cursor, h->row_pos));
-        TL_LAUNCH(h, launch_embed(h->stream, h->token_cur + seq, 1, h->D, h->cfg.vocab, h->emb, h->emb_s, h->x));
-        const int32_t max_t = h->host_cursor[seq] + 1;
-        for (int l = 0; l < c.n_layers; l++)
-            if ((r = layer_rows(h, l, 1, max_t))) return r;
-        if ((r = lm_head_rows(h, h->x, 1, seq, 1))) return r;
+        if (h->use_graphs && !h->profiling) {
+            if ((r = decode_graph_launch(h, seq))) return r;
+        } else if ((r = decode_step1(h, seq, h->host_cursor[seq] + 1))) {
+            return r;
+        }
         h->host_cursor[seq] += 1;
         h->host_ngen[seq] += 1;
         *n_out = step + 1;
@@ -946,10 +1048,10 @@ int32_t tl_decode_batch(tl_handle* h, int32_t n_seqs, const int32_t* tokens, con
     TL_HIP(h, hipMemcpyAsync(h->n_gen, zeros.data(), sizeof(int32_t) * n_seqs, hipMemcpyHostToDevice, h->stream));
     TL_LAUNCH(h, launch_reset_keys(h->stream, h->keys, n_seqs));
     for (int step = 0; step < n_steps; step++) {
-        TL_LAUNCH(h, launch_step_rows(h->stream, h->row_seq, n_seqs, h->cursor, h->row_pos));
-        TL_LAUNCH(h, launch_embed(h->stream, h->token_cur, n_seqs, h->D, h->cfg.vocab, h->emb, h->emb_s, h->x));
+        TL_LAUNCH(h, launch_embed_step(h->stream, h->token_cur, h->row_seq, n_seqs, h->cursor, h->row_pos, h->D,
+                                       c.vocab, h->emb, h->emb_s, h->x));
         for (int l = 0; l < c.n_layers; l++)
-            if ((r = layer_rows(h, l, n_seqs, max_t))) return r;
+            if ((r = layer_rows(h, l, n_seqs, max_t, true))) return r;
         if ((r = lm_head_rows(h, h->x, n_seqs, 0, 1))) return r;
     }
     if ((r = finish(h))) return r;
