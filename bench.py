@@ -187,11 +187,12 @@ def main():
     log(f"decode: {args.steps} steps in {dt * 1e3:.1f} ms -> {tok_s:.1f} tok/s")
 
     # per-kernel timing with HIP events on the library's stream
-    eng.prefill(prompt)
-    eng.set_profiling(True)
-    eng.decode(args.profile_steps)
     kbytes = decode_kernel_bytes(CFG)
     kernels = {}
+    eng.prefill(prompt)
+    eng.set_profiling(True)
+    if args.profile_steps > 0:
+        eng.decode(args.profile_steps)
     for name in ("qkv", "o", "glu", "down", "lm_head", "attn", "norm"):
         cnt, ms, _ = eng.profile(name)
         if cnt:
@@ -204,7 +205,7 @@ def main():
     eng.set_profiling(False)
     gemv_bytes = sum(kbytes[k] * kernels[k]["launches"] for k in kbytes if k in kernels)
     gemv_us = sum(kernels[k]["avg_us"] * kernels[k]["launches"] for k in kbytes if k in kernels)
-    glu = kernels["glu"]
+    glu = kernels.get("glu", {"gbs": None, "frac": None, "bytes": kbytes["glu"], "avg_us": None})
 
     # prefill: 512 tokens, MFMA utilisation of the GEMM kernels
     pre = None
@@ -250,8 +251,9 @@ def main():
         "roofline": {"bound": "hbm", "kernel": "gemv_glu (gate+up SiLU-GLU decode GEMV)",
                      "achieved": glu["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": glu["frac"],
                      "traffic": None, "bytes_per_launch": glu["bytes"], "avg_us": glu["avg_us"]},
-        "decode_gemv_gbs": round(gemv_bytes / (gemv_us * 1e-6) / 1e9, 1),
-        "decode_step_hbm_frac": round(gemv_bytes / args.profile_steps / (dt / args.steps) / 1e9 / HBM_PEAK_GBS, 4),
+        "decode_gemv_gbs": round(gemv_bytes / (gemv_us * 1e-6) / 1e9, 1) if gemv_us else None,
+        "decode_step_hbm_frac": (round(gemv_bytes / args.profile_steps / (dt / args.steps) / 1e9 / HBM_PEAK_GBS, 4)
+                                 if args.profile_steps else None),
         "kernels": kernels,
         "prefill": pre,
         "cpu_baseline": cpu,

@@ -50,13 +50,15 @@ TL_DEV void prologue_quant(const float4 (&xv)[KCH], int K, int8_t* xs8, float* r
 #pragma unroll
     for (int c = 0; c < KCH; c++) {
         const int idx = c * kNT + tid;
+        unsigned word = 0;  // bytes beyond K stay zero: they meet padded weight lanes
         if (idx * 4 < K) {
             const unsigned b0 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(xv[c].x, sf)));
             const unsigned b1 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(xv[c].y, sf)));
             const unsigned b2 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(xv[c].z, sf)));
             const unsigned b3 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(xv[c].w, sf)));
-            ((unsigned*)xs8)[idx] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+            word = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
         }
+        ((unsigned*)xs8)[idx] = word;
     }
     if (tid == 0) *xscale = s;
     __syncthreads();
@@ -123,13 +125,15 @@ TL_DEV void prologue_rmsnorm(const float4 (&xv)[KCH], const float4 (&gv)[KCH], i
 #pragma unroll
     for (int c = 0; c < KCH; c++) {
         const int idx = c * kNT + tid;
+        unsigned word = 0;
         if (idx * 4 < K) {
             const unsigned b0 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(av[c].x, sf)));
             const unsigned b1 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(av[c].y, sf)));
             const unsigned b2 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(av[c].z, sf)));
             const unsigned b3 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(av[c].w, sf)));
-            ((unsigned*)xs8)[idx] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+            word = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
         }
+        ((unsigned*)xs8)[idx] = word;
     }
     if (tid == 0) *xscale = s;
     __syncthreads();
@@ -151,27 +155,30 @@ __global__ __launch_bounds__(kNT) void gemv_fused_kernel(GemvArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int K = a.k;
     const int row0 = (blockIdx.x * kNW + wave) * R;
-    const int4 zero = make_int4(0, 0, 0, 0);
 
-    // 1) activation row first ...
+    // 1) activation row first (clamped indices, no branches) ...
     float4 xv[KCH], gv[KCH];
-    int4 xr[KCH];
+    v4i xr[KCH];
+    const int kq = K / 4 - 1;
     if (PRO == PRO_X8) {
 #pragma unroll
         for (int c = 0; c < KCH; c++) {
             const int off = c * 1024 + lane * 16;
-            xr[c] = off < K ? *(const int4*)(a.x + off) : zero;
+            xr[c] = ld16(a.x + min(off, K - 16));
         }
     } else {
 #pragma unroll
         for (int c = 0; c < KCH; c++) {
-            const int idx = c * kNT + tid;
-            xv[c] = idx * 4 < K ? ((const float4*)a.xf)[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
-            if (PRO == PRO_RMSNORM) gv[c] = idx * 4 < K ? ((const float4*)a.gamma)[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+            const int idx = min(c * kNT + tid, kq);
+            xv[c] = ((const float4*)a.xf)[idx];
+            if (PRO == PRO_RMSNORM) gv[c] = ((const float4*)a.gamma)[idx];
         }
     }
-    // 2) ... then every weight row of this wavefront
-    int4 wv[NM][R][KCH];
+    __builtin_amdgcn_sched_barrier(0);
+    // 2) ... then every weight row of this wavefront: unconditional 128-bit
+    // non-temporal loads; lanes past the end of a row read an in-bounds
+    // stand-in and meet zero activation bytes
+    v4i wv[NM][R][KCH];
 #pragma unroll
     for (int m = 0; m < NM; m++) {
         const int8_t* wb = m ? a.w2 : a.w;
@@ -179,25 +186,23 @@ __global__ __launch_bounds__(kNT) void gemv_fused_kernel(GemvArgs a) {
         for (int r = 0; r < R; r++) {
             const int8_t* wr = wb + (int64_t)min(row0 + r, a.n - 1) * K;
 #pragma unroll
-            for (int c = 0; c < KCH; c++) {
-                const int off = c * 1024 + lane * 16;
-                wv[m][r][c] = off < K ? *(const int4*)(wr + off) : zero;
-            }
+            for (int c = 0; c < KCH; c++) wv[m][r][c] = ld_nt16(wr + min(c * 1024 + lane * 16, K - 16));
         }
     }
+    __builtin_amdgcn_sched_barrier(0);
     // 3) prologue while the weights stream in
     double sx;
     if (PRO == PRO_X8) {
         sx = a.xs[0];
+#pragma unroll
+        for (int c = 0; c < KCH; c++)
+            if (c * 1024 + lane * 16 >= K) xr[c] = (v4i){0, 0, 0, 0};
     } else {
         if (PRO == PRO_QUANT) prologue_quant<KCH>(xv, K, xs8, red, &xscale);
         else prologue_rmsnorm<KCH>(xv, gv, K, a.eps, a.plan, sq, part, xs8, red, &xscale);
         sx = xscale;
 #pragma unroll
-        for (int c = 0; c < KCH; c++) {
-            const int off = c * 1024 + lane * 16;
-            xr[c] = off < K ? *(const int4*)(xs8 + off) : zero;
-        }
+        for (int c = 0; c < KCH; c++) xr[c] = ld16(xs8 + c * 1024 + lane * 16);
     }
     // 4) dot products and wavefront reductions (exact integers)
     int acc[NM][R];
@@ -207,7 +212,7 @@ __global__ __launch_bounds__(kNT) void gemv_fused_kernel(GemvArgs a) {
         for (int r = 0; r < R; r++) {
             int s = 0;
 #pragma unroll
-            for (int c = 0; c < KCH; c++) s = sdot4x4(wv[m][r][c], xr[c], s);
+            for (int c = 0; c < KCH; c++) s = sdot4v(wv[m][r][c], xr[c], s);
             acc[m][r] = wave_sum_i32(s);
         }
     // 5) epilogue
@@ -270,7 +275,7 @@ struct AttnDecodeArgs {
     float* out;           // [rows][D]
 };
 
-template <int HPW>
+template <int HPW, int KPF, int VPF>
 __global__ __launch_bounds__(256) void attention_decode_kernel(AttnDecodeArgs p) {
     extern __shared__ __align__(16) float dyn[];
     __shared__ __align__(16) int8_t qs[HPW][64];
@@ -299,45 +304,54 @@ __global__ __launch_bounds__(256) void attention_decode_kernel(AttnDecodeArgs p)
     const int T = pos + 1;
     const int tpad = (T + 63) & ~63;
     const int nblk = tpad >> 6;
+    const int ngrp = tpad >> 4;
+    const int64_t pl = p.kv.plane(seq, p.layer, g);
+    const int8_t* kp = p.kv.k + pl;
+    const int8_t* vp = p.kv.v + pl;
 
     float* v = dyn;                          // [W] this row's q|k|v
     float* s_buf = dyn + W;                  // [HPW][tpad] scores, then exps
     int8_t* p8 = (int8_t*)(s_buf + HPW * tpad);
     float* bsum = (float*)(p8 + HPW * tpad); // [HPW][nblk]
 
+    // 0) this row's q|k|v into LDS (just written by the projection kernel,
+    //    an L2 hit) ...
     const float* src = p.qkv + (int64_t)row * W;
-    for (int i = tid; i < W / 4; i += blockDim.x) ((float4*)v)[i] = ((const float4*)src)[i];
+    // every element a thread rotates has dimension tid % 64 (256 = 4 x 64)
+    const float cs = p.cosb[(int64_t)pos * kHeadDim + (tid & 63)];
+    const float sn = p.sinb[(int64_t)pos * kHeadDim + (tid & 63)];
+    for (int i = tid; i < W / 4; i += 256) ((float4*)v)[i] = ((const float4*)src)[i];
     __syncthreads();
+    // ... then the cached K/V rows this wavefront will use (rows 0..pos-1 are
+    //    final), in flight during the RoPE / quantization below; block and
+    //    group indices are clamped so the loads stay inside the plane and the
+    //    surplus copies are never used
+    v4i kreg[KPF][4], vreg[VPF];
+#pragma unroll
+    for (int i = 0; i < KPF; i++) {
+        const int8_t* kb = kp + (int64_t)min(wave + 4 * i, nblk - 1) * 4096 + lane * 16;
+#pragma unroll
+        for (int q = 0; q < 4; q++) kreg[i][q] = ld16(kb + q * 1024);
+    }
+#pragma unroll
+    for (int j = 0; j < VPF; j++) vreg[j] = ld16(vp + (int64_t)min(wave + 4 * j, ngrp - 1) * 1024 + lane * 16);
+    __builtin_amdgcn_sched_barrier(0);
 
-    const float* cp = p.cosb + (int64_t)pos * kHeadDim;
-    const float* sp = p.sinb + (int64_t)pos * kHeadDim;
     // RoPE of every Q element (the row's scale is the max over all heads)
     float mx = 0.0f;
-    float qr[(32 * 64 + 255) / 256];
-#pragma unroll
-    for (int k = 0; k < (32 * 64 + 255) / 256; k++) {
-        const int i = tid + k * 256;
-        qr[k] = 0.0f;
-        if (i < D) {
-            const int d = i & 63;
-            const float rot = d < 32 ? -v[i + 32] : v[i - 32];
-            qr[k] = (v[i] * cp[d]) + (rot * sp[d]);
-            mx = fmaxf(mx, fabsf(qr[k]));
-        }
-    }
-    for (int i = tid + 8 * 256; i < D; i += 256) {   // heads beyond 32 (not TinyLlama)
+    for (int i = tid; i < D; i += 256) {
         const int d = i & 63;
         const float rot = d < 32 ? -v[i + 32] : v[i - 32];
-        mx = fmaxf(mx, fabsf((v[i] * cp[d]) + (rot * sp[d])));
+        mx = fmaxf(mx, fabsf((v[i] * cs) + (rot * sn)));
     }
     mx = wave_max_f32(mx);
     if (lane == 0) red[wave] = mx;
-    // this row's K (after RoPE) and V of KV head g, quantized at the static scales
+    // this row's K (after RoPE) and V of KV head g at the static scales
     const float sk = p.kv_sk[p.layer * p.n_kv + g], sv = p.kv_sv[p.layer * p.n_kv + g];
     if (tid < 64) {
         const int i = D + g * 64 + tid, d = tid;
         const float rot = d < 32 ? -v[i + 32] : v[i - 32];
-        const float kr = (v[i] * cp[d]) + (rot * sp[d]);
+        const float kr = (v[i] * cs) + (rot * sn);
         knew[d] = sat_i8(__builtin_rintf(__fdiv_rn(kr, sk)));
     } else if (tid < 128) {
         const int d = tid - 64;
@@ -347,60 +361,50 @@ __global__ __launch_bounds__(256) void attention_decode_kernel(AttnDecodeArgs p)
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     const double s_q = quant_scale(mx);
     const float sfq = (float)s_q;
-#pragma unroll
-    for (int k = 0; k < (32 * 64 + 255) / 256; k++) {
-        const int i = tid + k * 256;
-        if (i >= h0 * 64 && i < (h0 + HPW) * 64) qs[(i >> 6) - h0][i & 63] = sat_i8(__builtin_rintf(__fdiv_rn(qr[k], sfq)));
-    }
-    for (int i = tid + 8 * 256; i < D; i += 256) {
-        if (i >= h0 * 64 && i < (h0 + HPW) * 64) {
-            const int d = i & 63;
-            const float rot = d < 32 ? -v[i + 32] : v[i - 32];
-            qs[(i >> 6) - h0][d] = sat_i8(__builtin_rintf(__fdiv_rn((v[i] * cp[d]) + (rot * sp[d]), sfq)));
-        }
+    for (int e = tid; e < HPW * 64; e += 256) {   // e % 64 == tid % 64: cs, sn apply
+        const int i = h0 * 64 + e, d = e & 63;
+        const float rot = d < 32 ? -v[i + 32] : v[i - 32];
+        qs[e >> 6][d] = sat_i8(__builtin_rintf(__fdiv_rn((v[i] * cs) + (rot * sn), sfq)));
     }
     if (tid < HPW) scl[tid] = (float)((s_q * (double)sk) * p.attn_scale);
-    const int64_t pl = p.kv.plane(seq, p.layer, g);
     if (h0 % G == 0 && tid < 64) {
         p.kv.k[pl + KvGeom::k_off(pos, tid)] = knew[tid];
         p.kv.v[pl + KvGeom::v_off(pos, tid)] = vnew[tid];
     }
     __syncthreads();
 
-    const int8_t* kp = p.kv.k + pl;
-    const int8_t* vp = p.kv.v + pl;
     // scores: lane <-> key inside a block of 64
     float lmax[HPW];
 #pragma unroll
     for (int h = 0; h < HPW; h++) lmax[h] = -INFINITY;
-    for (int b = wave; b < nblk; b += 4) {
+    auto score_block = [&](int b, v4i k0, v4i k1, v4i k2, v4i k3) {
         const int t = b * 64 + lane;
         if (t < T) {
-            int4 k0, k1, k2, k3;
-            if (t < pos) {
-                const int8_t* kb = kp + (int64_t)b * 4096 + lane * 16;
-                k0 = *(const int4*)(kb);
-                k1 = *(const int4*)(kb + 1024);
-                k2 = *(const int4*)(kb + 2048);
-                k3 = *(const int4*)(kb + 3072);
-            } else {
-                k0 = ((const int4*)knew)[0];
-                k1 = ((const int4*)knew)[1];
-                k2 = ((const int4*)knew)[2];
-                k3 = ((const int4*)knew)[3];
+            if (t == pos) {
+                k0 = ((const v4i*)knew)[0];
+                k1 = ((const v4i*)knew)[1];
+                k2 = ((const v4i*)knew)[2];
+                k3 = ((const v4i*)knew)[3];
             }
 #pragma unroll
             for (int h = 0; h < HPW; h++) {
-                const int4* q4 = (const int4*)qs[h];
-                int S = sdot4x4(k0, q4[0], 0);
-                S = sdot4x4(k1, q4[1], S);
-                S = sdot4x4(k2, q4[2], S);
-                S = sdot4x4(k3, q4[3], S);
+                const v4i* q4 = (const v4i*)qs[h];
+                int S = sdot4v(k0, q4[0], 0);
+                S = sdot4v(k1, q4[1], S);
+                S = sdot4v(k2, q4[2], S);
+                S = sdot4v(k3, q4[3], S);
                 const float sv2 = (float)S * scl[h];
                 s_buf[h * tpad + t] = sv2;
                 lmax[h] = fmaxf(lmax[h], sv2);
             }
         }
+    };
+#pragma unroll
+    for (int i = 0; i < KPF; i++)
+        if (wave + 4 * i < nblk) score_block(wave + 4 * i, kreg[i][0], kreg[i][1], kreg[i][2], kreg[i][3]);
+    for (int b = wave + 4 * KPF; b < nblk; b += 4) {
+        const int8_t* kb = kp + (int64_t)b * 4096 + lane * 16;
+        score_block(b, ld16(kb), ld16(kb + 1024), ld16(kb + 2048), ld16(kb + 3072));
     }
 #pragma unroll
     for (int h = 0; h < HPW; h++) {
@@ -448,20 +452,22 @@ __global__ __launch_bounds__(256) void attention_decode_kernel(AttnDecodeArgs p)
     int o[HPW];
 #pragma unroll
     for (int h = 0; h < HPW; h++) o[h] = 0;
-    const int ngrp = tpad >> 4;
     const int cpos = pos >> 4, bpos = pos & 15;
-    for (int c = wave; c < ngrp; c += 4) {
-        int4 vv = *(const int4*)(vp + (int64_t)c * 1024 + lane * 16);
+    auto pv_group = [&](int c, v4i vv) {
         if (c == cpos) {
             const unsigned nb = (uint8_t)vnew[lane];
             const int sh = (bpos & 3) * 8;
             const unsigned keep = ~(0xFFu << sh);
-            int* comp = (bpos >> 2) == 0 ? &vv.x : (bpos >> 2) == 1 ? &vv.y : (bpos >> 2) == 2 ? &vv.z : &vv.w;
-            *comp = (int)(((unsigned)*comp & keep) | (nb << sh));
+            const int q = bpos >> 2;
+            vv[q] = (int)(((unsigned)vv[q] & keep) | (nb << sh));
         }
 #pragma unroll
-        for (int h = 0; h < HPW; h++) o[h] = sdot4x4(vv, *(const int4*)(p8 + h * tpad + c * 16), o[h]);
-    }
+        for (int h = 0; h < HPW; h++) o[h] = sdot4v(vv, *(const v4i*)(p8 + h * tpad + c * 16), o[h]);
+    };
+#pragma unroll
+    for (int j = 0; j < VPF; j++)
+        if (wave + 4 * j < ngrp) pv_group(wave + 4 * j, vreg[j]);
+    for (int c = wave + 4 * VPF; c < ngrp; c += 4) pv_group(c, ld16(vp + (int64_t)c * 1024 + lane * 16));
 #pragma unroll
     for (int h = 0; h < HPW; h++) accs[wave][h][lane] = o[h];
     __syncthreads();
@@ -544,10 +550,10 @@ hipError_t launch_attention_decode(hipStream_t s, const float* qkv, int32_t rows
     AttnDecodeArgs p{qkv, n_heads, n_kv, rm, cos, sin, kv, layer, kv_sk, kv_sv, 1.0 / sqrt((double)kHeadDim), out};
     if (hpw == 1) {
         const size_t lds = sizeof(float) * W + (size_t)tpad * 4 + tpad + (tpad / 64) * 4 + 64;
-        hipLaunchKernelGGL(attention_decode_kernel<1>, dim3(n_heads, rows), dim3(256), lds, s, p);
+        hipLaunchKernelGGL((attention_decode_kernel<1, 2, 8>), dim3(n_heads, rows), dim3(256), lds, s, p);
     } else if (hpw == 8 && G == 8) {
         const size_t lds = sizeof(float) * W + (size_t)8 * tpad * 4 + 8 * tpad + 8 * (tpad / 64) * 4 + 64;
-        hipLaunchKernelGGL(attention_decode_kernel<8>, dim3(n_heads / 8, rows), dim3(256), lds, s, p);
+        hipLaunchKernelGGL((attention_decode_kernel<8, 2, 4>), dim3(n_heads / 8, rows), dim3(256), lds, s, p);
     } else {
         return hipErrorInvalidValue;
     }
@@ -564,11 +570,11 @@ hipError_t launch_embed_step(hipStream_t s, const int32_t* tok_by_seq, const int
 }
 
 hipError_t init_decode_kernels() {
-    hipError_t e = hipFuncSetAttribute((const void*)attention_decode_kernel<8>,
+    hipError_t e = hipFuncSetAttribute((const void*)attention_decode_kernel<8, 2, 4>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, 120 * 1024);
     if (e != hipSuccess) return e;
-    return hipFuncSetAttribute((const void*)attention_decode_kernel<1>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                               64 * 1024);
+    return hipFuncSetAttribute((const void*)attention_decode_kernel<1, 2, 8>,
+                               hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
 }
 
 }  // namespace tl

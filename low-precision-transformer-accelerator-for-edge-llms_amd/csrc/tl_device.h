@@ -110,6 +110,18 @@ TL_DEV unsigned long long wave_max_u64(unsigned long long v) {
     return v;
 }
 
+// 128-bit loads that stay 128-bit: weights stream through once (non-temporal)
+TL_DEV v4i ld_nt16(const int8_t* p) { return __builtin_nontemporal_load((const v4i*)p); }
+TL_DEV v4i ld16(const int8_t* p) { return *(const v4i*)p; }
+
+TL_DEV int sdot4v(v4i a, v4i b, int acc) {
+    acc = __builtin_amdgcn_sdot4(a[0], b[0], acc, false);
+    acc = __builtin_amdgcn_sdot4(a[1], b[1], acc, false);
+    acc = __builtin_amdgcn_sdot4(a[2], b[2], acc, false);
+    acc = __builtin_amdgcn_sdot4(a[3], b[3], acc, false);
+    return acc;
+}
+
 TL_DEV int sdot4x4(int4 a, int4 b, int acc) {
     acc = __builtin_amdgcn_sdot4(a.x, b.x, acc, false);
     acc = __builtin_amdgcn_sdot4(a.y, b.y, acc, false);
