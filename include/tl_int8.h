@@ -14,8 +14,11 @@
  *     259-268).
  *   - "dev" pointers are device (HBM) addresses, e.g. torch.Tensor.data_ptr()
  *     of a CUDA tensor; "host" pointers are ordinary host memory.
- *   - Every call runs on the handle's HIP stream and has completed when it
- *     returns, unless the name ends in _async.
+ *   - Every call runs on the handle's HIP stream (a non-blocking stream, not
+ *     ordered with any other) and has completed when it returns, unless the
+ *     name ends in _async.  Device inputs must therefore be complete when a
+ *     call is made: a caller that wrote them on another stream synchronizes
+ *     that stream first.
  *   - A handle is not thread safe: one host thread per handle.
  *   - Matrices are row-major; weights are [N][K] int8 (one output channel per
  *     K-contiguous row, docs/design_decisions.txt B3) with one float32 scale

@@ -135,6 +135,17 @@ def load_library() -> C.CDLL:
     return L
 
 
+def _fence(args) -> None:
+    """The library runs on its own non-blocking stream: device inputs written
+    by torch on torch's current stream must be complete before a call reads
+    them, so wait for that stream when any argument is a CUDA tensor."""
+    for a in args:
+        if getattr(a, "is_cuda", False):
+            import torch
+            torch.cuda.current_stream(a.device).synchronize()
+            return
+
+
 def _addr(x) -> int | None:
     """Device or host address of a torch tensor, a NumPy array or an int."""
     if x is None:
@@ -183,11 +194,13 @@ class Runtime:
         """Call tl_<name>(h, *args): tensors and arrays become their addresses,
         everything else (ints, floats, ctypes objects, None) passes through."""
         fn = getattr(self.lib, name)
+        _fence(args)
         conv = [_addr(a) if hasattr(a, "data_ptr") or hasattr(a, "__array_interface__") else a for a in args]
         self.check(fn(self.h, *conv), name)
 
     # ---- model state -------------------------------------------------------
     def load_layer(self, layer: int, w: list, s: list, g_in, g_post, src: int) -> None:
+        _fence([*w, *s, g_in, g_post])
         wa = (_vp * 7)(*[_addr(t) for t in w])
         sa = (_vp * 7)(*[_addr(t) for t in s])
         self.check(self.lib.tl_load_layer(self.h, layer, wa, sa, _addr(g_in), _addr(g_post), src), "tl_load_layer")

@@ -156,10 +156,15 @@ __global__ __launch_bounds__(kNT) void gemv_fused_kernel(GemvArgs a) {
     const int K = a.k;
     const int row0 = (blockIdx.x * kNW + wave) * R;
 
-    // 1) activation row first (clamped indices, no branches) ...
+    // 1) activation row and this lane's epilogue operands first (clamped
+    // indices, no branches): lane l < R finishes row row0 + l ...
     float4 xv[KCH], gv[KCH];
     v4i xr[KCH];
     const int kq = K / 4 - 1;
+    const int nl = min(row0 + min(lane, R - 1), a.n - 1);
+    const float wsl = a.ws[nl];
+    const float ws2l = (EPI == EPI_GLU) ? a.ws2[nl] : 0.0f;
+    const float resl = (EPI == EPI_DEQUANT_RES) ? a.residual[nl] : 0.0f;
     if (PRO == PRO_X8) {
 #pragma unroll
         for (int c = 0; c < KCH; c++) {
@@ -215,19 +220,24 @@ __global__ __launch_bounds__(kNT) void gemv_fused_kernel(GemvArgs a) {
             for (int c = 0; c < KCH; c++) s = sdot4v(wv[m][r][c], xr[c], s);
             acc[m][r] = wave_sum_i32(s);
         }
-    // 5) epilogue
-    if (EPI == EPI_ARGMAX) {
-        unsigned long long best = 0;
+    // 5) epilogue: the sums are wavefront-uniform; lane l < R takes row l's
+    int mine[NM];
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            const int n = row0 + r;
-            if (n < a.n) {
-                const float logit = (float)acc[0][r] * deq_mult(sx, a.ws[n]);
-                if (a.y && lane == 0) a.y[n] = logit;
-                const unsigned long long k = argmax_key(logit, n);
-                best = k > best ? k : best;
-            }
+    for (int m = 0; m < NM; m++) {
+        mine[m] = acc[m][0];
+#pragma unroll
+        for (int r = 1; r < R; r++) mine[m] = lane == r ? acc[m][r] : mine[m];
+    }
+    const int n = row0 + lane;
+    const bool live = lane < R && n < a.n;
+    if (EPI == EPI_ARGMAX) {
+        unsigned long long k = 0;
+        if (live) {
+            const float logit = (float)mine[0] * deq_mult(sx, wsl);
+            if (a.y) a.y[n] = logit;
+            k = argmax_key(logit, n);
         }
+        const unsigned long long best = wave_max_u64(k);
         if (lane == 0) wbest[wave] = best;
         __syncthreads();
         if (tid == 0) {
@@ -237,19 +247,15 @@ __global__ __launch_bounds__(kNT) void gemv_fused_kernel(GemvArgs a) {
         }
         return;
     }
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        const int n = row0 + r;
-        if (lane != r || n >= a.n) continue;
-        if (EPI == EPI_DEQUANT || EPI == EPI_DEQUANT_RES) {
-            float v = (float)acc[0][r] * deq_mult(sx, a.ws[n]);
-            if (EPI == EPI_DEQUANT_RES) v = a.residual[n] + v;
-            a.y[n] = v;
-        } else if (EPI == EPI_GLU) {
-            const float gt = (float)acc[0][r] * deq_mult(sx, a.ws[n]);
-            const float up = (float)acc[NM - 1][r] * deq_mult(sx, a.ws2[n]);
-            a.y[n] = tl_silu(gt) * up;
-        }
+    if (!live) return;
+    if (EPI == EPI_DEQUANT || EPI == EPI_DEQUANT_RES) {
+        float v = (float)mine[0] * deq_mult(sx, wsl);
+        if (EPI == EPI_DEQUANT_RES) v = resl + v;
+        a.y[n] = v;
+    } else if (EPI == EPI_GLU) {
+        const float gt = (float)mine[0] * deq_mult(sx, wsl);
+        const float up = (float)mine[NM - 1] * deq_mult(sx, ws2l);
+        a.y[n] = tl_silu(gt) * up;
     }
 }
 

@@ -1,0 +1,349 @@
+// tl_gemm.hip -- INT8 MFMA GEMM for prefill (M = prompt length):
+//   C[M][N] = A[M][K] . W[N][K]^T   (INT32, exact)   then a fused epilogue
+//   (dequantization per row/channel, + residual, or SiLU(gate) * up).
+//
+// v_mfma_i32_32x32x32_i8: a wavefront multiplies a 32x32 A fragment by a
+// 32x32 B fragment (K = 32) into 16 int32 accumulators per lane.  Each lane
+// supplies 16 consecutive K bytes of one A row and of one B row: lane l holds
+// row (l % 32), K bytes [(l / 32) * 16, +16); as long as A and B use the same
+// lane -> K assignment the integer result is exact.  Output: lane l, register
+// i holds C[8 (i / 4) + 4 (l / 32) + (i % 4)][l % 32].
+//
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "tl_device.h"
+#include "tl_internal.h"
+
+namespace tl {
+
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// LDS operand tiles hold rows of BK bytes = CPR 16-byte chunks.  Chunk c of
+// row r is stored at slot c ^ ((r >> S) & (CPR - 1)) with S = log2(16 / CPR):
+// the 16 lanes of one LDS pass, which read the same logical chunk of 16
+// consecutive rows (or write 16 chunks of the same row), then touch 16
+// distinct bank quads.
+template <int CPR>
+TL_DEV int swz(int row, int c) {
+    constexpr int S = CPR >= 16 ? 0 : (CPR == 8 ? 1 : 2);
+    return row * CPR + (c ^ ((row >> S) & (CPR - 1)));
+}
+
+// WM x WN x KS wavefronts.  A wavefront owns (32 TM) x (32 TN) outputs (of
+// each matrix for the GLU epilogue, which stages gate and up rows side by
+// side) and one of KS interleaved K slices of every step; with KS = 2 two
+// wavefronts share each SIMD, so one computes while the other waits on LDS,
+// and their partial sums meet in LDS at the end.  K advances BK per step
+// through a ring of three LDS buffers: while step s computes out of buffer
+// s % 3, step s + 2 is written into buffer (s + 2) % 3 from one of PD
+// register sets, whose global loads were issued PD steps earlier.
+template <int WM, int WN, int TM, int TN, int BK, int PD, int KS>
+struct GemmShape {
+    static constexpr int kWaves = WM * WN * KS;
+    static constexpr int kThreads = kWaves * 64;
+    static constexpr int BM = 32 * TM * WM, BN = 32 * TN * WN, CPR = BK / 16;
+    static constexpr int QS = BK / 32 / KS;   // 32-wide K slices per wavefront per step
+};
+
+template <int WM, int WN, int TM, int TN, int BK, int PD, int KS, int EPI>
+__global__ __launch_bounds__(WM * WN * KS * 64) void gemm32_kernel(GemmArgs a) {
+    using G = GemmShape<WM, WN, TM, TN, BK, PD, KS>;
+    constexpr int NT = G::kThreads, BM = G::BM, BN = G::BN, CPR = G::CPR, QS = G::QS;
+    constexpr int NB = (EPI == EPI_GLU) ? 2 : 1;
+    constexpr int ACH = BM * CPR, BCH = BN * CPR;   // 16-byte chunks per operand tile
+    static_assert(ACH % NT == 0 && BCH % NT == 0, "tile does not split evenly over threads");
+    static_assert(KS == 1 || KS == 2, "one or two K slices");
+    constexpr int APT = ACH / NT, BPT = BCH / NT;
+    constexpr int NBUF = 3;
+    constexpr int LDS_CHUNKS = NBUF * (ACH + NB * BCH);
+    // the K-slice reduction reuses the operand buffers
+    static_assert(KS == 1 || WM * WN * NB * TM * TN * 16 * 64 * 4 <= LDS_CHUNKS * 16, "reduction does not fit");
+    __shared__ v4i lds[LDS_CHUNKS];
+    auto sa = [&](int buf, int i) -> v4i& { return lds[buf * ACH + i]; };
+    auto sb = [&](int buf, int b, int i) -> v4i& { return lds[NBUF * ACH + (buf * NB + b) * BCH + i]; };
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int ks = wave / (WM * WN), wt = wave % (WM * WN);
+    const int wm = wt / WN, wn = wt % WN;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int kb = blockIdx.z * a.k_split;
+    const int ke = min(a.k, kb + a.k_split);
+    const int nfull = (ke - kb) / BK;              // full BK-wide steps
+    const int wtail = (ke - kb) - nfull * BK;      // width of a final partial step (multiple of 64)
+    const int nsteps = nfull + (wtail ? 1 : 0);
+
+    // staging: chunk c = tid + NT j -> row c / CPR, K chunk c % CPR
+    const int8_t* asrc[APT];
+    const int8_t* bsrc[NB][BPT];
+#pragma unroll
+    for (int j = 0; j < APT; j++) {
+        const int c = tid + NT * j;
+        asrc[j] = a.a + (int64_t)min(m0 + c / CPR, a.m - 1) * a.k;
+    }
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int j = 0; j < BPT; j++) {
+            const int c = tid + NT * j;
+            bsrc[b][j] = (b ? a.w2 : a.w) + (int64_t)min(n0 + c / CPR, a.n - 1) * a.k;
+        }
+    v4i ra[PD][APT], rb[PD][NB][BPT];
+    auto gload = [&](int set, int step) {
+        const int kk = kb + step * BK;
+        // a partial last step reloads its last valid chunk in the lanes past
+        // its width (in bounds)
+        const int lim = (step == nfull) ? wtail - 16 : BK - 16;
+#pragma unroll
+        for (int j = 0; j < APT; j++) {
+            const int c = tid + NT * j;
+            ra[set][j] = ld16(asrc[j] + kk + min((c % CPR) * 16, lim));
+        }
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int j = 0; j < BPT; j++) {
+                const int c = tid + NT * j;
+                rb[set][b][j] = ld16(bsrc[b][j] + kk + min((c % CPR) * 16, lim));
+            }
+    };
+    // A partial last step (width wtail) holds reloaded bytes past its width;
+    // its A chunks there are cleared in LDS, so every step can run all BK / 32
+    // K slices: cleared A times any B adds exactly zero.
+    auto lstore = [&](int set, int buf, int step) {
+#pragma unroll
+        for (int j = 0; j < APT; j++) {
+            const int c = tid + NT * j;
+            sa(buf, swz<CPR>(c / CPR, c % CPR)) = ra[set][j];
+        }
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int j = 0; j < BPT; j++) {
+                const int c = tid + NT * j;
+                sb(buf, b, swz<CPR>(c / CPR, c % CPR)) = rb[set][b][j];
+            }
+        if (step == nfull && wtail) {
+            const v4i zero = {0, 0, 0, 0};
+#pragma unroll
+            for (int j = 0; j < APT; j++) {
+                const int c = tid + NT * j;
+                if ((c % CPR) * 16 >= wtail) sa(buf, swz<CPR>(c / CPR, c % CPR)) = zero;
+            }
+        }
+    };
+
+    v16i acc[NB][TM][TN];
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc[b][i][j][e] = 0;
+
+    const int fr = lane & 31, fk = lane >> 5;   // fragment row, 16-byte chunk inside a K=32 slice
+    // all fragments of a step are read before its MFMAs start, so the LDS
+    // latency of later K slices overlaps the MFMAs of earlier ones
+    auto compute = [&](int buf) {
+        v4i af[QS][TM], bf[QS][NB][TN];
+#pragma unroll
+        for (int q = 0; q < QS; q++) {
+            const int kc = (ks * QS + q) * 2 + fk;
+#pragma unroll
+            for (int i = 0; i < TM; i++) af[q][i] = sa(buf, swz<CPR>(wm * 32 * TM + i * 32 + fr, kc));
+#pragma unroll
+            for (int b = 0; b < NB; b++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) bf[q][b][j] = sb(buf, b, swz<CPR>(wn * 32 * TN + j * 32 + fr, kc));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < QS; q++)
+#pragma unroll
+            for (int b = 0; b < NB; b++)
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        acc[b][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[q][i], bf[q][b][j], acc[b][i][j], 0, 0, 0);
+    };
+    // step s: write step s + 2 (register set (s + 2) % PD) into LDS buffer
+    // (s + 2) % 3, whose last reader, step s - 1, finished at the previous
+    // barrier; reload that register set with step s + 2 + PD; compute step s
+    // from buffer s % 3, written two steps ago; barrier.  Loads, LDS stores
+    // and barriers do not depend on data: the step index of a load past the
+    // end is clamped to the last step (a redundant, in-bounds reload; steps
+    // past the end are written to LDS but never read), so the wait before
+    // each LDS store covers exactly one step's loads and the PD - 1 steps
+    // after it stay in flight.
+    auto step = [&](int s, int u) {
+        const int set = (u + 2) % PD;
+        lstore(set, (s + 2) % NBUF, s + 2);
+        gload(set, min(s + 2 + PD, nsteps - 1));
+        compute(s % NBUF);
+        __syncthreads();
+    };
+    if (nsteps > 0) {
+#pragma unroll
+        for (int u = 0; u < PD; u++) gload(u, min(u, nsteps - 1));
+        lstore(0, 0, 0);
+        gload(0, min(PD, nsteps - 1));
+        lstore(1 % PD, 1, 1);
+        gload(1 % PD, min(PD + 1, nsteps - 1));
+        __syncthreads();
+        int s0 = 0;
+        for (; s0 + PD <= nsteps; s0 += PD) {
+#pragma unroll
+            for (int u = 0; u < PD; u++) step(s0 + u, u);
+        }
+#pragma unroll
+        for (int u = 0; u < PD - 1; u++)
+            if (s0 + u < nsteps) step(s0 + u, u);
+    }
+
+    if (KS == 2) {
+        // the last step ended with a barrier: LDS is free.  Slice 1 parks its
+        // partial sums (lane-contiguous), slice 0 adds them and runs the
+        // epilogue.
+        int* red = reinterpret_cast<int*>(lds);
+        if (ks == 1) {
+#pragma unroll
+            for (int b = 0; b < NB; b++)
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+#pragma unroll
+                        for (int e = 0; e < 16; e++)
+                            red[(((wt * NB + b) * TM + i) * TN + j) * 1024 + e * 64 + lane] = acc[b][i][j][e];
+        }
+        __syncthreads();
+        if (ks == 1) return;
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++)
+                        acc[b][i][j][e] += red[(((wt * NB + b) * TM + i) * TN + j) * 1024 + e * 64 + lane];
+    }
+
+    // epilogue.  Lane l, register e of a 32 x 32 block holds row
+    // 8 (e / 4) + 4 (l / 32) + e % 4, column l % 32.  Every load (row and
+    // channel scales, residual) is issued before the first store: the output
+    // could alias them as far as the compiler knows, and loads ordered after
+    // stores would cost one cache round trip per element.
+    const bool partial = gridDim.z > 1 || EPI == EPI_RAW;
+    const int64_t plane = (int64_t)a.m * a.n;
+    const int rbase = m0 + wm * 32 * TM + 4 * (lane >> 5);
+    const int cbase = n0 + wn * 32 * TN + (lane & 31);
+    if (partial) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const int n = cbase + j * 32;
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int m = rbase + i * 32 + 8 * (e >> 2) + (e & 3);
+                    if (m < a.m && n < a.n)
+#pragma unroll
+                        for (int b = 0; b < NB; b++)
+                            a.acc[(int64_t)(blockIdx.z * NB + b) * plane + (int64_t)m * a.n + n] = acc[b][i][j][e];
+                }
+            }
+        return;
+    }
+    double sx[TM][16];
+    float sw[NB][TN];
+    float res[TM][TN][EPI == EPI_DEQUANT_RES ? 16 : 1];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) sx[i][e] = a.as[min(rbase + i * 32 + 8 * (e >> 2) + (e & 3), a.m - 1)];
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        const int n = min(cbase + j * 32, a.n - 1);
+        sw[0][j] = a.ws[n];
+        if (EPI == EPI_GLU) sw[NB - 1][j] = a.ws2[n];
+    }
+    if (EPI == EPI_DEQUANT_RES) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int m = min(rbase + i * 32 + 8 * (e >> 2) + (e & 3), a.m - 1);
+                    res[i][j][e] = a.residual[(int64_t)m * a.n + min(cbase + j * 32, a.n - 1)];
+                }
+    }
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = cbase + j * 32;
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int m = rbase + i * 32 + 8 * (e >> 2) + (e & 3);
+                const float v0 = (float)acc[0][i][j][e] * deq_mult(sx[i][e], sw[0][j]);
+                float out;
+                if (EPI == EPI_GLU) {
+                    const float up = (float)acc[NB - 1][i][j][e] * deq_mult(sx[i][e], sw[NB - 1][j]);
+                    out = tl_silu(v0) * up;
+                } else if (EPI == EPI_DEQUANT_RES) {
+                    out = res[i][j][e] + v0;
+                } else {
+                    out = v0;
+                }
+                if (m < a.m && n < a.n) a.y[(int64_t)m * a.n + n] = out;
+            }
+        }
+}
+
+// Tile configurations (index = cfg):
+//        waves (M x N x K)  wave tile  block tile  BK   register sets
+//   0:   2 x 2 x 2          32 x 32    64 x 64     128  3    (default)
+//   1:   2 x 2 x 2          64 x 32    128 x 64    128  3
+//   2:   2 x 2 x 2          32 x 64    64 x 128    128  3
+//   3:   2 x 2 x 2          32 x 32    64 x 64     256  3
+template <int WM, int WN, int TM, int TN, int BK, int PD, int KS, int EPI>
+static void go32(hipStream_t s, const GemmArgs& a, int32_t splits) {
+    using G = GemmShape<WM, WN, TM, TN, BK, PD, KS>;
+    const dim3 grid((a.n + G::BN - 1) / G::BN, (a.m + G::BM - 1) / G::BM, splits);
+    hipLaunchKernelGGL((gemm32_kernel<WM, WN, TM, TN, BK, PD, KS, EPI>), grid, dim3(G::kThreads), 0, s, a);
+}
+
+template <int EPI>
+static bool shape32(hipStream_t s, const GemmArgs& a, int32_t splits, int cfg) {
+    switch (cfg) {
+        case 0: go32<2, 2, 1, 1, 128, 3, 2, EPI>(s, a, splits); return true;
+        case 1: go32<2, 2, 2, 1, 128, 3, 2, EPI>(s, a, splits); return true;
+        case 2: go32<2, 2, 1, 2, 128, 3, 2, EPI>(s, a, splits); return true;
+        case 3: go32<2, 2, 1, 1, 256, 3, 2, EPI>(s, a, splits); return true;
+        default: return false;
+    }
+}
+
+// M >= 64: 32x32x32 MFMA tiles; cfg selects the tile configuration above
+hipError_t launch_gemm32(hipStream_t s, int epi, const GemmArgs& a, int32_t splits, int32_t cfg) {
+    if (a.m <= 0 || a.n <= 0) return hipSuccess;
+    if (a.k <= 0 || a.k % 64 != 0 || a.k_split % 64 != 0 || splits < 1) return hipErrorInvalidValue;
+    bool ok = false;
+    switch (epi) {
+        case EPI_DEQUANT: ok = shape32<EPI_DEQUANT>(s, a, splits, cfg); break;
+        case EPI_DEQUANT_RES: ok = shape32<EPI_DEQUANT_RES>(s, a, splits, cfg); break;
+        case EPI_GLU: ok = shape32<EPI_GLU>(s, a, splits, cfg); break;
+        case EPI_RAW: ok = shape32<EPI_RAW>(s, a, splits, cfg); break;
+        default: break;
+    }
+    if (!ok) return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+}  // namespace tl

@@ -136,6 +136,7 @@ hipError_t launch_argmax_rows(hipStream_t s, const float* logits, int32_t rows, 
                               unsigned long long* keys);
 hipError_t init_kernels();
 hipError_t init_decode_kernels();
+hipError_t launch_gemm32(hipStream_t s, int epi, const GemmArgs& a, int32_t splits, int32_t cfg);
 hipError_t launch_gemv_fused(hipStream_t s, int pro, int epi, const GemvArgs& a);
 hipError_t launch_attention_decode(hipStream_t s, const float* qkv, int32_t rows, int32_t n_heads, int32_t n_kv,
                                    RowMap rm, const float* cos, const float* sin, KvGeom kv, int32_t layer,

@@ -118,56 +118,68 @@ __global__ void fill_u32_kernel(unsigned* p, int32_t n, unsigned v) {
 template <int R, int KCH, int EPI>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     constexpr int NM = (EPI == EPI_GLU) ? 2 : 1;
+    __shared__ unsigned long long wbest[4];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row0 = (blockIdx.x * 4 + wave) * R;
-    const int4 zero = make_int4(0, 0, 0, 0);
+    const int K = a.k;
 
-    int4 wv[NM][R][KCH];
+    // activation row and this lane's epilogue operands first (lane l < R
+    // finishes row row0 + l), then the weight rows: unconditional 128-bit
+    // loads at clamped in-bounds offsets; lanes past the end of a row meet
+    // activation bytes cleared below
+    v4i xv[KCH];
+#pragma unroll
+    for (int c = 0; c < KCH; c++) xv[c] = ld16(a.x + min(c * 1024 + lane * 16, K - 16));
+    const int nl = min(row0 + min(lane, R - 1), a.n - 1);
+    // (a raw-sum launch passes no multipliers)
+    const float wsl = (EPI != EPI_REQUANT || a.ws) ? a.ws[nl] : 0.0f;
+    const float ws2l = (EPI == EPI_GLU) ? a.ws2[nl] : 0.0f;
+    const float resl = (EPI == EPI_DEQUANT_RES) ? a.residual[nl] : 0.0f;
+    const double sx = (EPI == EPI_REQUANT) ? 0.0 : a.xs[0];
+    __builtin_amdgcn_sched_barrier(0);
+    v4i wv[NM][R][KCH];
 #pragma unroll
     for (int m = 0; m < NM; m++) {
         const int8_t* wb = m ? a.w2 : a.w;
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const int n = min(row0 + r, a.n - 1);
-            const int8_t* wr = wb + (int64_t)n * a.k;
+            const int8_t* wr = wb + (int64_t)min(row0 + r, a.n - 1) * K;
 #pragma unroll
-            for (int c = 0; c < KCH; c++) {
-                const int off = c * 1024 + lane * 16;
-                wv[m][r][c] = off < a.k ? *(const int4*)(wr + off) : zero;
-            }
+            for (int c = 0; c < KCH; c++) wv[m][r][c] = ld_nt16(wr + min(c * 1024 + lane * 16, K - 16));
         }
     }
-    int4 xv[KCH];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int c = 0; c < KCH; c++) {
-        const int off = c * 1024 + lane * 16;
-        xv[c] = off < a.k ? *(const int4*)(a.x + off) : zero;
-    }
+    for (int c = 0; c < KCH; c++)
+        if (c * 1024 + lane * 16 >= K) xv[c] = (v4i){0, 0, 0, 0};
     int acc[NM][R];
 #pragma unroll
     for (int m = 0; m < NM; m++)
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            int s = 0;
+            int sum = 0;
 #pragma unroll
-            for (int c = 0; c < KCH; c++) s = sdot4x4(wv[m][r][c], xv[c], s);
-            acc[m][r] = wave_sum_i32(s);
+            for (int c = 0; c < KCH; c++) sum = sdot4v(wv[m][r][c], xv[c], sum);
+            acc[m][r] = wave_sum_i32(sum);
         }
-
+    // the sums are wavefront-uniform; lane l < R takes row l's
+    int mine[NM];
+#pragma unroll
+    for (int m = 0; m < NM; m++) {
+        mine[m] = acc[m][0];
+#pragma unroll
+        for (int r = 1; r < R; r++) mine[m] = lane == r ? acc[m][r] : mine[m];
+    }
+    const int n = row0 + lane;
+    const bool live = lane < R && n < a.n;
     if (EPI == EPI_ARGMAX) {
-        __shared__ unsigned long long wbest[4];
-        unsigned long long best = 0;
-        const double sx = a.xs[0];
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const int n = row0 + r;
-            if (n < a.n) {
-                const float logit = (float)acc[0][r] * deq_mult(sx, a.ws[n]);
-                if (a.y && lane == 0) a.y[n] = logit;
-                const unsigned long long k = argmax_key(logit, n);
-                best = k > best ? k : best;
-            }
+        unsigned long long k = 0;
+        if (live) {
+            const float logit = (float)mine[0] * deq_mult(sx, wsl);
+            if (a.y) a.y[n] = logit;
+            k = argmax_key(logit, n);
         }
+        const unsigned long long best = wave_max_u64(k);
         if (lane == 0) wbest[wave] = best;
         __syncthreads();
         if (threadIdx.x == 0) {
@@ -177,24 +189,18 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         }
         return;
     }
-
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        const int n = row0 + r;
-        if (lane != r || n >= a.n) continue;
-        if (a.acc) a.acc[n] = acc[0][r];
-        if (EPI == EPI_REQUANT) {
-            if (a.y8) a.y8[n] = sat_i8(__builtin_rintf((float)acc[0][r] * a.ws[n]));
-        } else if (EPI == EPI_DEQUANT || EPI == EPI_DEQUANT_RES) {
-            float v = (float)acc[0][r] * deq_mult(a.xs[0], a.ws[n]);
-            if (EPI == EPI_DEQUANT_RES) v = a.residual[n] + v;
-            a.y[n] = v;
-        } else if (EPI == EPI_GLU) {
-            const double sx = a.xs[0];
-            const float gt = (float)acc[0][r] * deq_mult(sx, a.ws[n]);
-            const float up = (float)acc[NM - 1][r] * deq_mult(sx, a.ws2[n]);
-            a.y[n] = tl_silu(gt) * up;
-        }
+    if (!live) return;
+    if (a.acc) a.acc[n] = mine[0];
+    if (EPI == EPI_REQUANT) {
+        if (a.y8) a.y8[n] = sat_i8(__builtin_rintf((float)mine[0] * wsl));
+    } else if (EPI == EPI_DEQUANT || EPI == EPI_DEQUANT_RES) {
+        float v = (float)mine[0] * deq_mult(sx, wsl);
+        if (EPI == EPI_DEQUANT_RES) v = resl + v;
+        a.y[n] = v;
+    } else if (EPI == EPI_GLU) {
+        const float gt = (float)mine[0] * deq_mult(sx, wsl);
+        const float up = (float)mine[NM - 1] * deq_mult(sx, ws2l);
+        a.y[n] = tl_silu(gt) * up;
     }
 }
 

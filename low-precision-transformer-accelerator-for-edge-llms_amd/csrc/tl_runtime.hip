@@ -101,6 +101,7 @@ struct tl_handle {
     std::string err;
 
     bool use_graphs = true;
+    int gemm_cfg = -1;                    // < 0: choose the MFMA tile configuration per shape
     std::vector<hipGraphExec_t> graphs;   // captured batch-1 decode step per sequence
 
     bool profiling = false;
@@ -247,7 +248,18 @@ int32_t ensure_partials(tl_handle* h, size_t need) {
 
 int32_t run_gemm(tl_handle* h, int epi, GemmArgs a, int kclass) {
     const int nb = epi == EPI_GLU ? 2 : 1;
-    // split K when the output tiles alone cannot fill the 256 CUs
+    const double bytes = (double)a.m * a.k + (double)nb * a.n * a.k + (double)a.m * a.n * 4.0;
+    if (a.m >= 64) {
+        // 32x32x32 MFMA tiles; 64 x 64 blocks with two K-slice wavefront
+        // groups measured fastest at M = 512 (TL_GEMM_CFG overrides)
+        const int cfg = h->gemm_cfg >= 0 ? h->gemm_cfg : 0;
+        a.k_split = a.k;
+        Prof p(h, kclass, bytes);
+        TL_LAUNCH(h, launch_gemm32(h->stream, epi, a, 1, cfg));
+        return TL_OK;
+    }
+    // small M (batched decode): 16x16x64 tiles, split K until the output tiles
+    // plus K splits cover the chip
     const int bm = a.m <= 32 ? 32 : 64;
     const int64_t tiles = (int64_t)((a.m + bm - 1) / bm) * ((a.n + 63) / 64);
     int splits = 1;
@@ -260,7 +272,6 @@ int32_t run_gemm(tl_handle* h, int epi, GemmArgs a, int kclass) {
         if (r) return r;
         a.acc = h->partials;
     }
-    const double bytes = (double)a.m * a.k + (double)nb * a.n * a.k + (double)a.m * a.n * 4.0;
     Prof p(h, kclass, bytes);
     TL_LAUNCH(h, launch_gemm(h->stream, epi, a, splits));
     if (splits > 1) TL_LAUNCH(h, launch_gemm_reduce(h->stream, epi, a, splits));
@@ -580,6 +591,7 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
     if ((e = init_kernels())) return bad(e);
     if ((e = init_decode_kernels())) return bad(e);
     if (const char* env = std::getenv("TL_NO_GRAPHS")) h->use_graphs = env[0] == '0';
+    if (const char* env = std::getenv("TL_GEMM_CFG")) h->gemm_cfg = std::atoi(env);
     if ((e = hipStreamSynchronize(h->stream))) return bad(e);
     *out = h;
     return TL_OK;

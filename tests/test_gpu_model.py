@@ -210,3 +210,30 @@ def test_graph_replay_equals_direct_launches(small_model):
     eng.set_profiling(False)
     assert_bits_equal(graph_toks, direct_toks, "tokens")
     eng.close()
+
+
+def test_prefill_512_tinyllama_shape():
+    """A 512-token prefill (M = 512 MFMA GEMMs, causal prefill attention) of a
+    2-layer TinyLlama-shape model with the full 32000-entry vocabulary equals
+    token-by-token decode in the oracle: next token, its logit and every K/V
+    cache row."""
+    cfg = dict(oracle.TINYLLAMA_CFG, n_layers=2)
+    m = oracle.synthetic_model(cfg, seed=21)
+    prompt = np.random.default_rng(8).integers(0, cfg["vocab"], 512).astype(np.int32)
+    eng = engine_for(m)
+    tok, lg = eng.prefill(prompt)
+    orc = oracle.Oracle(m)
+    kc, vc = m.new_cache()
+    x = None
+    for i, t in enumerate(prompt):
+        x = orc.embed(int(t))
+        for layer in range(cfg["n_layers"]):
+            x = orc.decode_row(layer, i, x, kc, vc)
+    want_tok, want_lg = orc.lm_head(x)
+    assert (tok, lg) == (want_tok, want_lg)
+    for layer in range(cfg["n_layers"]):
+        for g in range(cfg["n_kv_heads"]):
+            k, v = eng.kv_read(0, layer, g, 0, prompt.size)
+            assert_bits_equal(k, kc[layer, g, :prompt.size], f"K layer {layer} head {g}")
+            assert_bits_equal(v, vc[layer, g, :prompt.size], f"V layer {layer} head {g}")
+    eng.close()
