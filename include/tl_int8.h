@@ -138,6 +138,11 @@ int32_t tl_silu_mul(tl_handle *h, const float *g, const float *u, int64_t n, flo
  * and P x V contractions of gemm_operand_router.sv:99-113). */
 int32_t tl_attention(tl_handle *h, int32_t seq, int32_t layer, int32_t pos0, int32_t rows,
                      const int8_t *q8, const double *q_scale, float *out);
+/* dequantize_int32 (GI:45-46) with the optional bias of quantized_linear
+ * (GI:72-73): y[r][c] = f32(acc[r][c]) * f32(input_scale * weight_scale)
+ * (+ bias[c]); acc and y dev [rows][cols], bias dev [cols] or NULL. */
+int32_t tl_dequantize_i32(tl_handle *h, const int32_t *acc, int64_t rows, int32_t cols, double input_scale,
+                          double weight_scale, const float *bias, float *y);
 /* RoPE + Q quantization + K/V static quantization and cache append for rows
  * of Q|K|V projections (GI:150-154, design_decisions A7/B2). */
 int32_t tl_qkv_append(tl_handle *h, int32_t seq, int32_t layer, int32_t pos0, int32_t rows,
@@ -154,6 +159,14 @@ int32_t tl_embed(tl_handle *h, const int32_t *tokens, int32_t rows, float *x);
 /* One decoder layer (GI:256-281) for one token of sequence seq at position
  * pos, x [D] dev updated in place, appends the token's K/V rows. */
 int32_t tl_decode_layer(tl_handle *h, int32_t seq, int32_t layer, int32_t pos, float *x);
+/* mixed_precision_decoder_layer (GI:256-281) over `rows` consecutive tokens of
+ * sequence seq at positions pos0..pos0+rows-1 (causal attention over the
+ * cache, whose rows for these positions it writes); x [rows][D] dev in place. */
+int32_t tl_layer_rows(tl_handle *h, int32_t seq, int32_t layer, int32_t pos0, int32_t rows, float *x);
+/* forward_mixed (GI:437-467) with the quantized LM head: prefill of tokens [n]
+ * (host) as tl_prefill, plus the logits of every position into logits, dev
+ * [n][V]; the sequence can then continue with tl_decode. */
+int32_t tl_prefill_logits(tl_handle *h, int32_t seq, const int32_t *tokens, int32_t n, float *logits);
 /* Prefill (GI:437-467 over the prompt): tokens [n] host at positions 0..n-1 of
  * sequence seq, all layers, KV cache written, next token greedy (host). */
 int32_t tl_prefill(tl_handle *h, int32_t seq, const int32_t *tokens, int32_t n, int32_t *next_token,

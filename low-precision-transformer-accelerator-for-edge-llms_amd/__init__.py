@@ -6,8 +6,10 @@ INT32 GEMV/GEMM with fused requantize/dequantize epilogues, GQA attention over
 an INT8 KV cache with static per-layer/per-KV-head scales, RMSNorm, RoPE,
 softmax, SiLU-GLU, residuals and greedy argmax.  Hand-written HIP kernels sit
 behind a C-ABI (include/tl_int8.h, libtl_int8.so); this package is the Python
-host side (ctypes), mirroring the operator surface of the reference's NumPy
-golden model.
+host side (ctypes): ``engine.Engine`` (device-resident model, KV-cache
+generation) and, with the reference's own names and arguments, ``tinyllama``
+(model/tinyllama.py primitives, weight archive) and ``tinyllama_gemm_int8``
+(model/tinyllama_gemm_int8.py operator surface).
 
 The package directory name is not a Python identifier; load it with
 ``__graft_entry__.load_package()`` (it registers the alias ``lpta``).

@@ -82,6 +82,9 @@ SIGNATURES = {
     "tl_lm_head_argmax": (_i32, [_vp, _vp, _i32p, _f32p, _vp]),
     "tl_embed": (_i32, [_vp, _vp, _i32, _vp]),
     "tl_decode_layer": (_i32, [_vp, _i32, _i32, _i32, _vp]),
+    "tl_layer_rows": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp]),
+    "tl_prefill_logits": (_i32, [_vp, _i32, _vp, _i32, _vp]),
+    "tl_dequantize_i32": (_i32, [_vp, _vp, C.c_int64, _i32, C.c_double, C.c_double, _vp, _vp]),
     "tl_prefill": (_i32, [_vp, _i32, _vp, _i32, _i32p, _f32p]),
     "tl_decode": (_i32, [_vp, _i32, _i32, _i32, _vp, _vp, _i32p, _i32p]),
     "tl_generate": (_i32, [_vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _i32p, _i32p]),

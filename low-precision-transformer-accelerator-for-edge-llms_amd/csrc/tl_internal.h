@@ -126,6 +126,8 @@ hipError_t launch_rope(hipStream_t s, float* v, int32_t rows, int32_t n_heads, c
                        const float* cos, const float* sin);
 hipError_t launch_softmax_rows(hipStream_t s, const float* x, int32_t rows, int32_t n, float* p);
 hipError_t launch_silu_mul(hipStream_t s, const float* g, const float* u, int64_t n, float* y);
+hipError_t launch_dequant_i32(hipStream_t s, const int32_t* acc, int64_t n, int32_t cols, float m,
+                              const float* bias, float* y);
 hipError_t launch_embed(hipStream_t s, const int32_t* tokens, int32_t rows, int32_t d, int32_t vocab,
                         const int8_t* emb, const float* emb_s, float* x);
 hipError_t launch_reset_keys(hipStream_t s, unsigned long long* keys, int32_t n);

@@ -629,6 +629,19 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(const float* __restri
     for (int i = tid; i < n; i += blockDim.x) pr[i] = __fdiv_rn(pr[i], total);
 }
 
+// GI:45-46 (+ bias, GI:72-73): y = f32(acc) * m (+ b[col]); the multiplier m
+// = f32(input_scale * weight_scale) is formed on the host in double, as the
+// golden forms its Python-float product before the float32 multiply.  Without
+// a bias nothing is added (adding +0 would turn -0 into +0).
+__global__ __launch_bounds__(256) void dequant_i32_kernel(const int32_t* __restrict__ acc, int64_t n, int32_t cols,
+                                                          float m, const float* __restrict__ bias,
+                                                          float* __restrict__ y) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const float v = (float)acc[i] * m;
+        y[i] = bias ? v + bias[i % cols] : v;
+    }
+}
+
 __global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__ g,
                                                        const float* __restrict__ u, int64_t n,
                                                        float* __restrict__ y) {
@@ -900,6 +913,14 @@ hipError_t launch_silu_mul(hipStream_t s, const float* g, const float* u, int64_
     if (n <= 0) return hipSuccess;
     const int blocks = (int)std::min<int64_t>(4096, (n + 255) / 256);
     hipLaunchKernelGGL(silu_mul_kernel, dim3(blocks), dim3(256), 0, s, g, u, n, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant_i32(hipStream_t s, const int32_t* acc, int64_t n, int32_t cols, float m,
+                              const float* bias, float* y) {
+    if (n <= 0) return hipSuccess;
+    const int blocks = (int)std::min<int64_t>(4096, (n + 255) / 256);
+    hipLaunchKernelGGL(dequant_i32_kernel, dim3(blocks), dim3(256), 0, s, acc, n, cols, m, bias, y);
     return hipGetLastError();
 }
 

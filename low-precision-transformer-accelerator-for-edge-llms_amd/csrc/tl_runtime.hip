@@ -932,8 +932,13 @@ int32_t tl_decode_layer(tl_handle* h, int32_t seq, int32_t layer, int32_t pos, f
     return finish(h);
 }
 
-int32_t tl_prefill(tl_handle* h, int32_t seq, const int32_t* tokens, int32_t n, int32_t* next_token, float* next_logit) {
-    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+}  // extern "C"
+
+namespace {
+
+// embedding + all layers over n prompt tokens of sequence seq (positions
+// 0..n-1); leaves the final hidden rows in h->x
+int32_t prefill_layers(tl_handle* h, int32_t seq, const int32_t* tokens, int32_t n) {
     const tl_config& c = h->cfg;
     TL_REQ(h, seq >= 0 && seq < h->max_seqs, "sequence out of range");
     TL_REQ(h, tokens && n >= 1, "Input token sequence is empty");
@@ -950,6 +955,13 @@ int32_t tl_prefill(tl_handle* h, int32_t seq, const int32_t* tokens, int32_t n, 
     TL_LAUNCH(h, launch_embed(h->stream, h->tokens, n, h->D, h->cfg.vocab, h->emb, h->emb_s, h->x));
     for (int l = 0; l < c.n_layers; l++)
         if ((r = layer_rows(h, l, n, n, false))) return r;
+    return TL_OK;
+}
+
+// next-token bookkeeping from the last prompt row, then wait and report
+int32_t prefill_finish(tl_handle* h, int32_t seq, int32_t n, int32_t* next_token, float* next_logit) {
+    const tl_config& c = h->cfg;
+    int32_t r;
     if ((r = lm_head_rows(h, h->x + (size_t)(n - 1) * h->D, 1, seq, 0))) return r;
     if ((r = finish(h))) return r;
     h->host_cursor[seq] = n;
@@ -957,6 +969,58 @@ int32_t tl_prefill(tl_handle* h, int32_t seq, const int32_t* tokens, int32_t n, 
     if (next_token) TL_HIP(h, hipMemcpy(next_token, h->tokens_out + (size_t)seq * c.max_pos, sizeof(int32_t), hipMemcpyDeviceToHost));
     if (next_logit) TL_HIP(h, hipMemcpy(next_logit, h->logit_out + (size_t)seq * c.max_pos, sizeof(float), hipMemcpyDeviceToHost));
     return TL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t tl_prefill(tl_handle* h, int32_t seq, const int32_t* tokens, int32_t n, int32_t* next_token, float* next_logit) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    int32_t r = prefill_layers(h, seq, tokens, n);
+    if (r) return r;
+    return prefill_finish(h, seq, n, next_token, next_logit);
+}
+
+int32_t tl_prefill_logits(tl_handle* h, int32_t seq, const int32_t* tokens, int32_t n, float* logits) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, logits, "null pointer");
+    int32_t r = prefill_layers(h, seq, tokens, n);
+    if (r) return r;
+    const tl_config& c = h->cfg;
+    {
+        Prof p(h, TL_K_NORM, (double)n * h->D * 9.0);
+        TL_LAUNCH(h, launch_rmsnorm_quant(h->stream, h->x, h->g_final, n, h->D, c.rms_eps, h->plan, nullptr, h->a8, h->as));
+    }
+    GemmArgs a{};
+    a.a = h->a8; a.w = h->lm_w; a.as = h->as; a.ws = h->lm_s; a.y = logits; a.m = n; a.n = c.vocab; a.k = h->D;
+    if ((r = run_gemm(h, EPI_DEQUANT, a, TL_K_LMHEAD))) return r;
+    return prefill_finish(h, seq, n, nullptr, nullptr);
+}
+
+int32_t tl_layer_rows(tl_handle* h, int32_t seq, int32_t layer, int32_t pos0, int32_t rows, float* x) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    const tl_config& c = h->cfg;
+    TL_REQ(h, seq >= 0 && seq < h->max_seqs && layer >= 0 && layer < c.n_layers, "index out of range");
+    TL_REQ(h, rows >= 1 && rows <= h->max_rows, "row count out of range");
+    TL_REQ(h, pos0 >= 0 && pos0 + rows <= c.max_pos, "Sequence length exceeds max_position_embeddings");
+    TL_REQ(h, x, "null pointer");
+    if (!h->layers[layer].wqkv) return fail(h, TL_ERR_BAD_DESCRIPTOR, "layer not loaded");
+    int32_t r = upload_rows(h, rows, seq, false, pos0);
+    if (r) return r;
+    TL_HIP(h, hipMemcpyAsync(h->x, x, sizeof(float) * h->D * rows, hipMemcpyDeviceToDevice, h->stream));
+    if ((r = layer_rows(h, layer, rows, pos0 + rows, rows == 1))) return r;
+    TL_HIP(h, hipMemcpyAsync(x, h->x, sizeof(float) * h->D * rows, hipMemcpyDeviceToDevice, h->stream));
+    return finish(h);
+}
+
+int32_t tl_dequantize_i32(tl_handle* h, const int32_t* acc, int64_t rows, int32_t cols, double input_scale,
+                          double weight_scale, const float* bias, float* y) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, acc && y && rows >= 0 && cols > 0, "bad dequantize arguments");
+    const float m = (float)(input_scale * weight_scale);
+    TL_LAUNCH(h, launch_dequant_i32(h->stream, acc, rows * cols, cols, m, bias, y));
+    return finish(h);
 }
 
 int32_t tl_decode(tl_handle* h, int32_t seq, int32_t max_new, int32_t eos_id, const volatile int32_t* abort_flag,

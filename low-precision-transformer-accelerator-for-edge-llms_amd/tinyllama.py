@@ -1,13 +1,101 @@
-"""Host-side counterparts of model/tinyllama.py (TL) needed by the INT8 path.
+"""The primitives of model/tinyllama.py (TL) on the MI355X path.
 
-Only table construction lives here; every per-token computation runs in the
-HIP library (see ops.py for the operator surface of TL's primitives).
+Same names, arguments and return types as the reference module: NumPy in,
+NumPy out, with every per-element computation done by the HIP library.
+- rms_norm and apply_rope are bit-exact to the reference;
+- softmax and silu use the library's own exp and agree with the reference to
+  about 1e-6 relative;
+- build_rope_cache keeps the reference's float32 NumPy steps (the table is an
+  input of the forward pass, not a per-token computation);
+- causal_mask, repeat_kv and rotate_half are index operations.
+TinyLlamaWeights / load_weights read the reference's .npz weight archive
+(TL:198-267 key schema).
+
+Device memory is torch CUDA tensors used as plain buffers.
 """
 from __future__ import annotations
 
 import numpy as np
 
+from ._native import Runtime
 
+# ---------------------------------------------------------------------------
+# device plumbing: small operator handles and torch buffers
+# ---------------------------------------------------------------------------
+_OP_HANDLES: dict = {}
+
+
+def round_pos(n: int) -> int:
+    """Handle position counts are positive multiples of 64."""
+    return max(64, -(-int(n) // 64) * 64)
+
+
+def op_runtime(eps: float = 1e-5, max_pos: int = 64) -> Runtime:
+    """A minimal handle for operator calls.  The library reads the RMSNorm
+    epsilon from the handle's configuration and RoPE tables hold max_pos rows
+    (rounded up to a multiple of 64), so handles are cached per (float32 eps,
+    max_pos)."""
+    key = (float(np.float32(eps)), round_pos(max_pos))
+    rt = _OP_HANDLES.get(key)
+    if rt is None:
+        cfg = dict(hidden=64, intermediate=64, n_layers=1, n_heads=1, n_kv_heads=1, head_dim=64, vocab=64,
+                   max_pos=key[1], rms_eps=np.float32(eps), rope_theta=10000.0)
+        rt = Runtime(cfg)
+        _OP_HANDLES[key] = rt
+    return rt
+
+
+def set_rope_rows(rt: Runtime, cos: np.ndarray, sin: np.ndarray, n: int) -> None:
+    """Load rows 0..n-1 of a cos/sin table into rt's RoPE table (rows past n,
+    up to the handle's size, are zero and never read)."""
+    rows = rt.cfg["max_pos"]
+    c = np.zeros((rows, 64), np.float32)
+    s = np.zeros((rows, 64), np.float32)
+    c[:n] = cos[:n]
+    s[:n] = sin[:n]
+    rt.call("tl_set_rope_table", c, s, rows)
+
+
+def dev(a, dtype=None):
+    """NumPy array -> torch CUDA tensor (a copy)."""
+    import torch
+    a = np.require(a if dtype is None else np.asarray(a, dtype=dtype), requirements=["C", "W"])
+    return torch.from_numpy(a).cuda()
+
+
+def empty(shape, dtype):
+    import torch
+    tdt = {np.float32: torch.float32, np.float64: torch.float64, np.int8: torch.int8,
+           np.int32: torch.int32}[np.dtype(dtype).type]
+    return torch.empty(tuple(int(s) for s in shape), dtype=tdt, device="cuda")
+
+
+def host(t) -> np.ndarray:
+    return t.detach().cpu().numpy()
+
+
+# ---------------------------------------------------------------------------
+# TL:45-50
+# ---------------------------------------------------------------------------
+def rms_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """x * 1/sqrt(mean(x^2) + eps) * w over the last axis, in float32."""
+    x_fp = np.asarray(x, dtype=np.float32)
+    w_fp = np.asarray(w, dtype=np.float32)
+    n = x_fp.shape[-1]
+    rows = int(np.prod(x_fp.shape[:-1], dtype=np.int64))
+    if rows == 0:
+        return np.empty(x_fp.shape, np.float32)
+    rt = op_runtime(eps)
+    y = empty((rows, n), np.float32)
+    q = empty((rows, n), np.int8)
+    s = empty((rows,), np.float64)
+    rt.call("tl_rmsnorm_quant", dev(x_fp.reshape(rows, n)), dev(np.broadcast_to(w_fp, (n,))), rows, n, y, q, s)
+    return host(y).reshape(x_fp.shape)
+
+
+# ---------------------------------------------------------------------------
+# TL:59-80
+# ---------------------------------------------------------------------------
 def build_rope_cache(seq_len: int, head_dim: int, rope_theta: float) -> tuple[np.ndarray, np.ndarray]:
     """RoPE cos/sin tables [seq_len][head_dim] in float32 (TL:59-66).
 
@@ -22,3 +110,176 @@ def build_rope_cache(seq_len: int, head_dim: int, rope_theta: float) -> tuple[np
     angles = np.outer(np.arange(seq_len, dtype=np.float32), inv_freq)
     angles = np.concatenate([angles, angles], axis=-1)
     return np.cos(angles).astype(np.float32), np.sin(angles).astype(np.float32)
+
+
+def rotate_half(x: np.ndarray) -> np.ndarray:
+    """TL:69-71: (x1, x2) -> (-x2, x1) over the last axis."""
+    half = x.shape[-1] // 2
+    return np.concatenate([-x[..., half:], x[..., :half]], axis=-1)
+
+
+def _rope_heads(v: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
+    """q or k [heads][seq][64] rotated at positions 0..seq-1 by the library."""
+    heads, seq, hd = v.shape
+    if hd != 64:
+        raise ValueError("head_dim must be 64")
+    if seq == 0:
+        return np.empty(v.shape, np.float32)
+    if cos.shape[0] < seq or sin.shape[0] < seq:
+        raise ValueError("RoPE table shorter than the sequence")
+    rt = op_runtime(max_pos=seq)
+    set_rope_rows(rt, cos, sin, seq)
+    rows = dev(np.ascontiguousarray(np.asarray(v, np.float32).transpose(1, 0, 2)).reshape(seq, heads * hd))
+    rt.call("tl_rope", rows, seq, heads, dev(np.arange(seq, dtype=np.int32)))
+    return host(rows).reshape(seq, heads, hd).transpose(1, 0, 2).copy()
+
+
+def apply_rope(q: np.ndarray, k: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """TL:74-80: q [Hq][seq][hd], k [Hkv][seq][hd] rotated at positions 0..seq-1."""
+    return _rope_heads(q, cos, sin), _rope_heads(k, cos, sin)
+
+
+# ---------------------------------------------------------------------------
+# TL:89-103
+# ---------------------------------------------------------------------------
+def causal_mask(seq_len: int) -> np.ndarray:
+    return np.tril(np.ones((seq_len, seq_len), dtype=bool))
+
+
+def repeat_kv(x: np.ndarray, n_rep: int) -> np.ndarray:
+    """GQA index map: KV head h serves query heads h*n_rep .. h*n_rep+n_rep-1."""
+    if n_rep == 1:
+        return x
+    return np.repeat(x, n_rep, axis=0)
+
+
+def softmax(x: np.ndarray, axis: int = -1) -> np.ndarray:
+    """Softmax over the last axis, in float32 on the library's kernel."""
+    if axis not in (-1, np.ndim(x) - 1):
+        raise ValueError("softmax runs over the last axis")
+    x_fp = np.asarray(x, dtype=np.float32)
+    n = x_fp.shape[-1]
+    rows = int(np.prod(x_fp.shape[:-1], dtype=np.int64))
+    if rows == 0 or n == 0:
+        return np.empty(x_fp.shape, np.float32)
+    p = empty((rows, n), np.float32)
+    op_runtime().call("tl_softmax_rows", dev(x_fp.reshape(rows, n)), rows, n, p)
+    return host(p).reshape(x_fp.shape)
+
+
+# ---------------------------------------------------------------------------
+# TL:159-161
+# ---------------------------------------------------------------------------
+def silu(x: np.ndarray) -> np.ndarray:
+    """x / (1 + exp(-clip(x, -60, 60))) in float32."""
+    x_fp = np.asarray(x, dtype=np.float32)
+    if x_fp.size == 0:
+        return np.empty(x_fp.shape, np.float32)
+    y = empty((x_fp.size,), np.float32)
+    op_runtime().call("tl_silu_mul", dev(x_fp.ravel()), None, x_fp.size, y)
+    return host(y).reshape(x_fp.shape)
+
+
+# ---------------------------------------------------------------------------
+# TL:198-267: the weight archive
+# ---------------------------------------------------------------------------
+class TinyLlamaWeights:
+    """The reference's weight archive: ``meta_*`` geometry keys,
+    ``embed_w`` [V][D], ``final_norm_w``, ``lm_head_w`` [D][V] and per layer
+    ``layer{i}_{q,k,v,o,gate,up,down}_w`` ([K][N], x @ W) with optional
+    ``_b`` biases and ``layer{i}_{input,post}_norm_w``.  Loaded with
+    ``np.load`` (no pickle).  ``from_arrays`` builds the same object from a
+    dict of arrays and a cfg (for synthetic models).
+
+    Optional static KV-cache scales may ride along as ``kv_k_scale`` /
+    ``kv_v_scale`` [L][Hkv] float32 arrays; without them the INT8 path
+    calibrates them on the first prompt it sees.
+    """
+
+    def __init__(self, path: str | None = None, compute_dtype=np.float32, cache_arrays: bool = False,
+                 data=None):
+        self.path = path
+        self.data = np.load(path) if data is None else data
+        self.compute_dtype = compute_dtype
+        self.cache_arrays = cache_arrays
+        self._cache: dict = {}
+        d = self.data
+        self.cfg = {
+            "model_id": str(np.asarray(d["meta_model_id"]).item()),
+            "hidden_size": int(d["meta_hidden_size"]),
+            "intermediate_size": int(d["meta_intermediate_size"]),
+            "num_hidden_layers": int(d["meta_num_hidden_layers"]),
+            "num_attention_heads": int(d["meta_num_attention_heads"]),
+            "num_key_value_heads": int(d["meta_num_key_value_heads"]),
+            "head_dim": int(d["meta_head_dim"]),
+            "vocab_size": int(d["meta_vocab_size"]),
+            "max_position_embeddings": int(d["meta_max_position_embeddings"]),
+            "rms_norm_eps": float(d["meta_rms_norm_eps"]),
+            "rope_theta": float(d["meta_rope_theta"]),
+        }
+        self.cfg["num_key_value_groups"] = self.cfg["num_attention_heads"] // self.cfg["num_key_value_heads"]
+        self.cfg["attn_scale"] = 1.0 / np.sqrt(self.cfg["head_dim"])
+
+    @classmethod
+    def from_arrays(cls, arrays: dict) -> "TinyLlamaWeights":
+        return cls(data=_DictArchive(arrays))
+
+    def _files(self):
+        return self.data.files
+
+    def _array(self, key: str) -> np.ndarray:
+        if self.cache_arrays and key in self._cache:
+            return self._cache[key]
+        arr = self.data[key]
+        if arr.dtype != self.compute_dtype:
+            arr = arr.astype(self.compute_dtype, copy=False)
+        if self.cache_arrays:
+            self._cache[key] = arr
+        return arr
+
+    def _optional_array(self, key: str):
+        return self._array(key) if key in self._files() else None
+
+    def embed(self, token_ids) -> np.ndarray:
+        return self._array("embed_w")[token_ids]
+
+    def final_norm_w(self) -> np.ndarray:
+        return self._array("final_norm_w")
+
+    def lm_head_w(self) -> np.ndarray:
+        return self._array("lm_head_w")
+
+    def kv_scales(self):
+        """(k_scales, v_scales) [L][Hkv] float32 if the archive carries them."""
+        if "kv_k_scale" in self._files() and "kv_v_scale" in self._files():
+            return (np.asarray(self.data["kv_k_scale"], np.float32), np.asarray(self.data["kv_v_scale"], np.float32))
+        return None
+
+    def layer(self, idx: int) -> dict:
+        out = {}
+        for n in ("q", "k", "v", "o"):
+            out[f"{n}_w"] = self._array(f"layer{idx}_{n}_w")
+        for n in ("q", "k", "v", "o"):
+            out[f"{n}_b"] = self._optional_array(f"layer{idx}_{n}_b")
+        for n in ("gate", "up", "down"):
+            out[f"{n}_w"] = self._array(f"layer{idx}_{n}_w")
+        for n in ("gate", "up", "down"):
+            out[f"{n}_b"] = self._optional_array(f"layer{idx}_{n}_b")
+        out["input_norm_w"] = self._array(f"layer{idx}_input_norm_w")
+        out["post_norm_w"] = self._array(f"layer{idx}_post_norm_w")
+        return out
+
+
+class _DictArchive:
+    """A dict of arrays with the ``files`` / ``__getitem__`` face of np.load."""
+
+    def __init__(self, arrays: dict):
+        self._a = {k: np.asarray(v) for k, v in arrays.items()}
+        self.files = list(self._a)
+
+    def __getitem__(self, k):
+        return self._a[k]
+
+
+def load_weights(path: str, compute_dtype=np.float32, cache_arrays: bool = False) -> TinyLlamaWeights:
+    return TinyLlamaWeights(path, compute_dtype=compute_dtype, cache_arrays=cache_arrays)

@@ -76,3 +76,34 @@ def test_pairwise_plan_widths():
     h = ctypes.c_void_p()
     bad = _native.TlConfig(64 * 3 * 7, 1408, 1, 21, 3, 64, 64, 128, 1e-5, 1e4)  # 1344 -> 672 -> 336 -> 168 -> 84
     assert lib.tl_create(ctypes.byref(bad), 1, ctypes.byref(h)) == _native.TL_ERR_UNSUPPORTED
+
+
+def test_golden_surface_host_logic(tmp_path):
+    """Host-only parts of the reference-surface mirror: token-id parsing and
+    its errors (GI:340-375), the layer-count check (GI:356-358) and the weight
+    archive reader (TL:198-267 key schema)."""
+    import numpy as np
+    import lpta.tinyllama as tl
+    import lpta.tinyllama_gemm_int8 as gi
+    assert gi.parse_token_ids(" 1, 2 ,3,") == [1, 2, 3] and gi.parse_token_ids(None) is None
+    with pytest.raises(ValueError, match="Provide either"):
+        gi.resolve_token_ids(None, None, None)
+    with pytest.raises(ValueError, match="--token-ids is required"):
+        gi.resolve_token_ids("hello", None, None)
+    with pytest.raises(ValueError, match="empty"):
+        gi.resolve_token_ids(None, ",", None)
+    with pytest.raises(ValueError, match="between 1 and 22"):
+        gi.validate_layer_count({"num_hidden_layers": 22}, 0)
+    meta = {"meta_model_id": np.array("m"), "meta_hidden_size": np.array(64), "meta_intermediate_size": np.array(128),
+            "meta_num_hidden_layers": np.array(1), "meta_num_attention_heads": np.array(1),
+            "meta_num_key_value_heads": np.array(1), "meta_head_dim": np.array(64), "meta_vocab_size": np.array(10),
+            "meta_max_position_embeddings": np.array(32), "meta_rms_norm_eps": np.array(1e-5, np.float32),
+            "meta_rope_theta": np.array(10000.0, np.float32)}
+    arrays = dict(meta, embed_w=np.ones((10, 64), np.float16), layer0_q_w=np.zeros((64, 64), np.float16),
+                  layer0_q_b=np.zeros(64, np.float16), layer0_input_norm_w=np.ones(64, np.float16))
+    np.savez(tmp_path / "w.npz", **arrays)
+    w = tl.load_weights(str(tmp_path / "w.npz"))
+    assert w.cfg["num_key_value_groups"] == 1 and w.cfg["hidden_size"] == 64 and w.cfg["model_id"] == "m"
+    assert w.embed([1, 3]).shape == (2, 64) and w.embed([1]).dtype == np.float32
+    assert w.kv_scales() is None
+    assert w._optional_array("layer0_k_b") is None and w._optional_array("layer0_q_b").dtype == np.float32
