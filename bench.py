@@ -140,6 +140,97 @@ def cpu_baseline(host, cfg, eng, prompt_len, first_token, gpu_tokens, n_steps, t
     return n_steps / dt, got, got == [int(t) for t in gpu_tokens[:n_steps]]
 
 
+def bench_gemv_q_proj(eng, seed, launches=200, copies=96):
+    """Single INT8 GEMV + per-channel requantize, the Q-projection shape: x int8
+    [2048], W int8 [2048][2048] uniform in [-127, 127], m U[1e-3, 1e-2].  The
+    weights rotate over `copies` distinct buffers (384 MB) so every launch
+    streams from HBM rather than the 256 MB Infinity Cache; kernel time from
+    HIP events on the library's stream."""
+    import torch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    n = k = 2048
+    ws = [torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda", generator=g) for _ in range(copies)]
+    x = torch.randint(-127, 128, (k,), dtype=torch.int8, device="cuda", generator=g)
+    m = torch.rand(n, device="cuda", generator=g) * 9e-3 + 1e-3
+    y = torch.empty(n, dtype=torch.int8, device="cuda")
+    acc = torch.empty(n, dtype=torch.int32, device="cuda")
+    for i in range(copies):
+        eng.rt.call("tl_gemv_i8_requant", x, ws[i], m, n, k, y, acc)
+    eng.set_profiling(True)
+    for i in range(launches):
+        eng.rt.call("tl_gemv_i8_requant", x, ws[i % copies], m, n, k, y, acc)
+    cnt, ms, _ = eng.profile("qkv")
+    eng.set_profiling(False)
+    avg_us = ms * 1e3 / cnt
+    nbytes = n * k + k + n * 4 + n
+    gbs = nbytes / (avg_us * 1e-6) / 1e9
+    return {"workload": "INT8 GEMV + requantize, x[1x2048] . W[2048x2048]^T, per-channel fp32 multipliers",
+            "launches": cnt, "avg_us": round(avg_us, 3), "bytes": nbytes, "gbs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "weights_rotated_over": copies}
+
+
+def bench_decode_layer(eng, calls=64):
+    """One TinyLlama-shape decoder layer, one decode step at position 512 over
+    the 512 rows a prefill left in the cache: the sum of its five kernels'
+    average HIP-event times."""
+    import torch
+    x = torch.randn(CFG["hidden"], device="cuda")
+    x0 = x.clone()
+    for _ in range(4):
+        x.copy_(x0)
+        eng.decode_layer(x, layer=0, pos=512)
+    eng.set_profiling(True)
+    for _ in range(calls):
+        x.copy_(x0)
+        eng.decode_layer(x, layer=0, pos=512)
+    per = {}
+    for name in ("qkv", "attn", "o", "glu", "down"):
+        cnt, ms, _ = eng.profile(name)
+        per[name] = round(ms * 1e3 / cnt, 3) if cnt else None
+    eng.set_profiling(False)
+    total_us = sum(v for v in per.values() if v)
+    kb = decode_kernel_bytes(CFG)
+    nbytes = kb["qkv"] + kb["o"] + kb["glu"] + kb["down"] + CFG["n_kv_heads"] * 512 * 128
+    gbs = nbytes / (total_us * 1e-6) / 1e9
+    return {"workload": "one TinyLlama-shape decoder layer, decode step at position 512 (512 cached rows)",
+            "kernel_us": per, "us": round(total_us, 3), "bytes": nbytes, "gbs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def bench_batch(model_eng_factory, host_seed, B=32, ctx=2048, steps=64):
+    """Batched decode: B sequences, each with a (ctx - steps)-row seeded INT8 KV
+    cache, then `steps` decode steps of all B together (M = B GEMMs)."""
+    import torch
+    eng = model_eng_factory(B)
+    rng = np.random.default_rng(host_seed)
+    start = ctx - steps
+    for b in range(B):
+        for layer in range(CFG["n_layers"]):
+            for g in range(CFG["n_kv_heads"]):
+                k = rng.integers(-127, 128, (start, 64), dtype=np.int8)
+                v = rng.integers(-127, 128, (start, 64), dtype=np.int8)
+                eng.kv_write(b, layer, g, 0, k, v)
+    toks = rng.integers(0, CFG["vocab"], B).astype(np.int32)
+    pos = np.full(B, start, np.int32)
+    eng.decode_batch(toks, pos - 8, 8)  # warm-up over rows start-8..start-1
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out = eng.decode_batch(toks, pos, steps)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    eng.close()
+    weights = sum(decode_kernel_bytes(CFG)[k] for k in ("qkv", "o", "glu", "down")) * CFG["n_layers"] \
+        + decode_kernel_bytes(CFG)["lm_head"]
+    kv = B * CFG["n_layers"] * CFG["n_kv_heads"] * 128 * (start + steps / 2)
+    step_s = dt / steps
+    return {"workload": f"batched INT8 decode, {B} sequences x {start}-row seeded KV cache, {steps} steps",
+            "tok_s": round(B * steps / dt, 1), "ms_per_step": round(step_s * 1e3, 3),
+            "hbm_bytes_per_step": int(weights + kv),
+            "gbs": round((weights + kv) / step_s / 1e9, 1),
+            "frac": round((weights + kv) / step_s / 1e9 / HBM_PEAK_GBS, 4), "tokens_out": int(out.size)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -152,6 +243,7 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--no-extras", action="store_true", help="skip the GEMV, layer and batch-32 workloads")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this build measures the single-GPU hot path only "
@@ -228,6 +320,14 @@ def main():
                "mfma_frac": round(ops / (gemm_ms * 1e-3) / I8_PEAK_OPS, 4)}
         log(f"prefill {args.prefill_len}: {pre}")
 
+    extras = None
+    if not args.no_extras:
+        extras = {"gemv_q_proj": bench_gemv_q_proj(eng, args.seed)}
+        log(f"gemv q_proj: {extras['gemv_q_proj']}")
+        if args.prefill_len >= 512:
+            extras["decode_layer"] = bench_decode_layer(eng)
+            log(f"decode layer: {extras['decode_layer']}")
+
     cpu = None
     if not args.no_cpu and args.cpu_steps > 0:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
@@ -238,6 +338,26 @@ def main():
                          f"sequence from the GPU's {args.prompt}-token KV cache",
                "tokens_match_gpu": bool(match)}
         log(f"cpu baseline: {cpu}")
+
+    if extras is not None:
+        # the batch needs its own handle (32 KV caches); free the batch-1 model first
+        layers_host = host
+        eng.close()
+        del eng
+        torch.cuda.empty_cache()
+
+        def factory(B):
+            e = Engine(CFG, max_seqs=B)
+            for i, L in enumerate(layers_host["layers"]):
+                e.load_layer(i, L)
+            e.load_lm_head(layers_host["lm_w"], layers_host["lm_s"], layers_host["g_final"])
+            e.load_embedding(layers_host["emb"], layers_host["emb_s"])
+            e.set_kv_scales(layers_host["kv_sk"], layers_host["kv_sv"])
+            return e
+
+        extras["batch32"] = bench_batch(factory, args.seed + 7)
+        log(f"batch 32: {extras['batch32']}")
+        eng = None
 
     out = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
@@ -257,8 +377,10 @@ def main():
         "kernels": kernels,
         "prefill": pre,
         "cpu_baseline": cpu,
+        "workloads": extras,
     }
-    eng.close()
+    if eng is not None:
+        eng.close()
     print(json.dumps(out), flush=True)
 
 

@@ -281,16 +281,22 @@ struct AttnDecodeArgs {
     float* out;           // [rows][D]
 };
 
-template <int HPW, int KPF, int VPF>
-__global__ __launch_bounds__(256) void attention_decode_kernel(AttnDecodeArgs p) {
+// NW wavefronts per workgroup; wavefront w takes key blocks w, w + NW, ...
+// (and value groups likewise).  Past the KPF / VPF blocks prefetched during
+// the Q/K/V post-processing, each wavefront loads KB key blocks (VB value
+// groups) before it computes any of them, so one memory latency covers
+// several blocks.
+template <int HPW, int KPF, int VPF, int NW>
+__global__ __launch_bounds__(NW * 64) void attention_decode_kernel(AttnDecodeArgs p) {
+    constexpr int NT = NW * 64, KB = HPW > 1 ? 2 : 4, VB = HPW > 1 ? 4 : 8;
     extern __shared__ __align__(16) float dyn[];
     __shared__ __align__(16) int8_t qs[HPW][64];
     __shared__ __align__(16) int8_t knew[64];
     __shared__ __align__(16) int8_t vnew[64];
-    __shared__ float red[16];
+    __shared__ float red[NW];
     __shared__ float scl[HPW], mrow[HPW], tot[HPW];
-    __shared__ float wmax[4][HPW];
-    __shared__ int accs[4][HPW][64];
+    __shared__ float wmax[NW][HPW];
+    __shared__ int accs[NW][HPW][64];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int G = p.n_heads / p.n_kv;
@@ -323,10 +329,10 @@ __global__ __launch_bounds__(256) void attention_decode_kernel(AttnDecodeArgs p)
     // 0) this row's q|k|v into LDS (just written by the projection kernel,
     //    an L2 hit) ...
     const float* src = p.qkv + (int64_t)row * W;
-    // every element a thread rotates has dimension tid % 64 (256 = 4 x 64)
+    // every element a thread rotates has dimension tid % 64 (NT = NW x 64)
     const float cs = p.cosb[(int64_t)pos * kHeadDim + (tid & 63)];
     const float sn = p.sinb[(int64_t)pos * kHeadDim + (tid & 63)];
-    for (int i = tid; i < W / 4; i += 256) ((float4*)v)[i] = ((const float4*)src)[i];
+    for (int i = tid; i < W / 4; i += NT) ((float4*)v)[i] = ((const float4*)src)[i];
     __syncthreads();
     // ... then the cached K/V rows this wavefront will use (rows 0..pos-1 are
     //    final), in flight during the RoPE / quantization below; block and
@@ -335,17 +341,17 @@ __global__ __launch_bounds__(256) void attention_decode_kernel(AttnDecodeArgs p)
     v4i kreg[KPF][4], vreg[VPF];
 #pragma unroll
     for (int i = 0; i < KPF; i++) {
-        const int8_t* kb = kp + (int64_t)min(wave + 4 * i, nblk - 1) * 4096 + lane * 16;
+        const int8_t* kb = kp + (int64_t)min(wave + NW * i, nblk - 1) * 4096 + lane * 16;
 #pragma unroll
         for (int q = 0; q < 4; q++) kreg[i][q] = ld16(kb + q * 1024);
     }
 #pragma unroll
-    for (int j = 0; j < VPF; j++) vreg[j] = ld16(vp + (int64_t)min(wave + 4 * j, ngrp - 1) * 1024 + lane * 16);
+    for (int j = 0; j < VPF; j++) vreg[j] = ld16(vp + (int64_t)min(wave + NW * j, ngrp - 1) * 1024 + lane * 16);
     __builtin_amdgcn_sched_barrier(0);
 
     // RoPE of every Q element (the row's scale is the max over all heads)
     float mx = 0.0f;
-    for (int i = tid; i < D; i += 256) {
+    for (int i = tid; i < D; i += NT) {
         const int d = i & 63;
         const float rot = d < 32 ? -v[i + 32] : v[i - 32];
         mx = fmaxf(mx, fabsf((v[i] * cs) + (rot * sn)));
@@ -364,10 +370,12 @@ __global__ __launch_bounds__(256) void attention_decode_kernel(AttnDecodeArgs p)
         vnew[d] = sat_i8(__builtin_rintf(__fdiv_rn(v[D + KVD + g * 64 + d], sv)));
     }
     __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    mx = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) mx = fmaxf(mx, red[w]);
     const double s_q = quant_scale(mx);
     const float sfq = (float)s_q;
-    for (int e = tid; e < HPW * 64; e += 256) {   // e % 64 == tid % 64: cs, sn apply
+    for (int e = tid; e < HPW * 64; e += NT) {   // e % 64 == tid % 64: cs, sn apply
         const int i = h0 * 64 + e, d = e & 63;
         const float rot = d < 32 ? -v[i + 32] : v[i - 32];
         qs[e >> 6][d] = sat_i8(__builtin_rintf(__fdiv_rn((v[i] * cs) + (rot * sn), sfq)));
@@ -407,10 +415,18 @@ __global__ __launch_bounds__(256) void attention_decode_kernel(AttnDecodeArgs p)
     };
 #pragma unroll
     for (int i = 0; i < KPF; i++)
-        if (wave + 4 * i < nblk) score_block(wave + 4 * i, kreg[i][0], kreg[i][1], kreg[i][2], kreg[i][3]);
-    for (int b = wave + 4 * KPF; b < nblk; b += 4) {
-        const int8_t* kb = kp + (int64_t)b * 4096 + lane * 16;
-        score_block(b, ld16(kb), ld16(kb + 1024), ld16(kb + 2048), ld16(kb + 3072));
+        if (wave + NW * i < nblk) score_block(wave + NW * i, kreg[i][0], kreg[i][1], kreg[i][2], kreg[i][3]);
+    for (int b0 = wave + NW * KPF; b0 < nblk; b0 += NW * KB) {
+        v4i kk[KB][4];
+#pragma unroll
+        for (int i = 0; i < KB; i++) {
+            const int8_t* kb = kp + (int64_t)min(b0 + NW * i, nblk - 1) * 4096 + lane * 16;
+#pragma unroll
+            for (int q = 0; q < 4; q++) kk[i][q] = ld16(kb + q * 1024);
+        }
+#pragma unroll
+        for (int i = 0; i < KB; i++)
+            if (b0 + NW * i < nblk) score_block(b0 + NW * i, kk[i][0], kk[i][1], kk[i][2], kk[i][3]);
     }
 #pragma unroll
     for (int h = 0; h < HPW; h++) {
@@ -418,10 +434,14 @@ __global__ __launch_bounds__(256) void attention_decode_kernel(AttnDecodeArgs p)
         if (lane == 0) wmax[wave][h] = m;
     }
     __syncthreads();
-    if (tid < HPW) mrow[tid] = fmaxf(fmaxf(wmax[0][tid], wmax[1][tid]), fmaxf(wmax[2][tid], wmax[3][tid]));
+    if (tid < HPW) {
+        float m = wmax[0][tid];
+        for (int w = 1; w < NW; w++) m = fmaxf(m, wmax[w][tid]);
+        mrow[tid] = m;
+    }
     __syncthreads();
     // exponentials and the block-64 butterfly sums
-    for (int b = wave; b < nblk; b += 4) {
+    for (int b = wave; b < nblk; b += NW) {
         const int t = b * 64 + lane;
 #pragma unroll
         for (int h = 0; h < HPW; h++) {
@@ -472,15 +492,24 @@ __global__ __launch_bounds__(256) void attention_decode_kernel(AttnDecodeArgs p)
     };
 #pragma unroll
     for (int j = 0; j < VPF; j++)
-        if (wave + 4 * j < ngrp) pv_group(wave + 4 * j, vreg[j]);
-    for (int c = wave + 4 * VPF; c < ngrp; c += 4) pv_group(c, ld16(vp + (int64_t)c * 1024 + lane * 16));
+        if (wave + NW * j < ngrp) pv_group(wave + NW * j, vreg[j]);
+    for (int c0 = wave + NW * VPF; c0 < ngrp; c0 += NW * VB) {
+        v4i vv[VB];
+#pragma unroll
+        for (int j = 0; j < VB; j++) vv[j] = ld16(vp + (int64_t)min(c0 + NW * j, ngrp - 1) * 1024 + lane * 16);
+#pragma unroll
+        for (int j = 0; j < VB; j++)
+            if (c0 + NW * j < ngrp) pv_group(c0 + NW * j, vv[j]);
+    }
 #pragma unroll
     for (int h = 0; h < HPW; h++) accs[wave][h][lane] = o[h];
     __syncthreads();
     const float pv_mult = deq_mult(1.0 / 127.0, sv);
     for (int i = tid; i < HPW * 64; i += blockDim.x) {
         const int h = i >> 6, d = i & 63;
-        const int O = accs[0][h][d] + accs[1][h][d] + accs[2][h][d] + accs[3][h][d];
+        int O = 0;
+#pragma unroll
+        for (int w = 0; w < NW; w++) O += accs[w][h][d];
         p.out[(int64_t)row * D + (int64_t)(h0 + h) * kHeadDim + d] = (float)O * pv_mult;
     }
 }
@@ -556,10 +585,10 @@ hipError_t launch_attention_decode(hipStream_t s, const float* qkv, int32_t rows
     AttnDecodeArgs p{qkv, n_heads, n_kv, rm, cos, sin, kv, layer, kv_sk, kv_sv, 1.0 / sqrt((double)kHeadDim), out};
     if (hpw == 1) {
         const size_t lds = sizeof(float) * W + (size_t)tpad * 4 + tpad + (tpad / 64) * 4 + 64;
-        hipLaunchKernelGGL((attention_decode_kernel<1, 2, 8>), dim3(n_heads, rows), dim3(256), lds, s, p);
+        hipLaunchKernelGGL((attention_decode_kernel<1, 2, 8, 4>), dim3(n_heads, rows), dim3(256), lds, s, p);
     } else if (hpw == 8 && G == 8) {
         const size_t lds = sizeof(float) * W + (size_t)8 * tpad * 4 + 8 * tpad + 8 * (tpad / 64) * 4 + 64;
-        hipLaunchKernelGGL((attention_decode_kernel<8, 2, 4>), dim3(n_heads / 8, rows), dim3(256), lds, s, p);
+        hipLaunchKernelGGL((attention_decode_kernel<8, 2, 4, 8>), dim3(n_heads / 8, rows), dim3(512), lds, s, p);
     } else {
         return hipErrorInvalidValue;
     }
@@ -576,10 +605,10 @@ hipError_t launch_embed_step(hipStream_t s, const int32_t* tok_by_seq, const int
 }
 
 hipError_t init_decode_kernels() {
-    hipError_t e = hipFuncSetAttribute((const void*)attention_decode_kernel<8, 2, 4>,
+    hipError_t e = hipFuncSetAttribute((const void*)attention_decode_kernel<8, 2, 4, 8>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, 120 * 1024);
     if (e != hipSuccess) return e;
-    return hipFuncSetAttribute((const void*)attention_decode_kernel<1, 2, 8>,
+    return hipFuncSetAttribute((const void*)attention_decode_kernel<1, 2, 8, 4>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
 }
 
