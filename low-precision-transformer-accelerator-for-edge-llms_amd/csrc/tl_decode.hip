@@ -21,123 +21,9 @@
 
 #include "tl_device.h"
 #include "tl_internal.h"
+#include "tl_prologue.h"
 
 namespace tl {
-
-constexpr int kNT = 256;   // threads per workgroup of the fused GEMV
-constexpr int kNW = kNT / 64;
-
-// ---------------------------------------------------------------------------
-// activation prologues: f32 row (K elements, 4 per float4 chunk) -> INT8 row
-// in LDS (natural byte order) + its float64 scale
-// ---------------------------------------------------------------------------
-template <int KCH>
-TL_DEV void prologue_quant(const float4 (&xv)[KCH], int K, int8_t* xs8, float* red, double* xscale) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    float mx = 0.0f;
-#pragma unroll
-    for (int c = 0; c < KCH; c++) {
-        if ((c * kNT + tid) * 4 < K) {
-            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(xv[c].x), fabsf(xv[c].y)), fmaxf(fabsf(xv[c].z), fabsf(xv[c].w))));
-        }
-    }
-    mx = wave_max_f32(mx);
-    if (lane == 0) red[wave] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    const double s = quant_scale(mx);
-    const float sf = (float)s;
-#pragma unroll
-    for (int c = 0; c < KCH; c++) {
-        const int idx = c * kNT + tid;
-        unsigned word = 0;  // bytes beyond K stay zero: they meet padded weight lanes
-        if (idx * 4 < K) {
-            const unsigned b0 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(xv[c].x, sf)));
-            const unsigned b1 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(xv[c].y, sf)));
-            const unsigned b2 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(xv[c].z, sf)));
-            const unsigned b3 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(xv[c].w, sf)));
-            word = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-        }
-        ((unsigned*)xs8)[idx] = word;
-    }
-    if (tid == 0) *xscale = s;
-    __syncthreads();
-}
-
-template <int KCH>
-TL_DEV void prologue_rmsnorm(const float4 (&xv)[KCH], const float4 (&gv)[KCH], int K, float eps, PwPlan plan,
-                             float* sq, float* part, int8_t* xs8, float* red, double* xscale) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-#pragma unroll
-    for (int c = 0; c < KCH; c++) {
-        const int idx = c * kNT + tid;
-        if (idx * 4 < K) {
-            float4 q;
-            q.x = xv[c].x * xv[c].x;
-            q.y = xv[c].y * xv[c].y;
-            q.z = xv[c].z * xv[c].z;
-            q.w = xv[c].w * xv[c].w;
-            ((float4*)sq)[idx] = q;
-        }
-    }
-    __syncthreads();
-    // NumPy pairwise tree: eight strided accumulators per leaf ...
-    const int L = plan.n_leaves, len = plan.leaf_len;
-    for (int p = tid; p < 8 * L; p += kNT) {
-        const float* a = sq + (p >> 3) * len;
-        const int j = p & 7;
-        float r = a[j];
-        for (int i = 8; i < len; i += 8) r = r + a[i + j];
-        part[p] = r;
-    }
-    __syncthreads();
-    // ... combined per leaf, then leaves pairwise across lanes of wave 0
-    if (wave == 0) {
-        float v = 0.0f;
-        if (lane < L) {
-            const float* r = part + 8 * lane;
-            v = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
-        }
-        for (int off = 1; off < L; off <<= 1) v = v + __shfl_xor(v, off);
-        if (lane == 0) red[8] = v;
-    }
-    __syncthreads();
-    const float var = __fdiv_rn(red[8], (float)K);
-    const float inv = __fdiv_rn(1.0f, __builtin_sqrtf(var + eps));
-    float4 av[KCH];
-    float mx = 0.0f;
-#pragma unroll
-    for (int c = 0; c < KCH; c++) {
-        if ((c * kNT + tid) * 4 < K) {
-            av[c].x = (xv[c].x * inv) * gv[c].x;
-            av[c].y = (xv[c].y * inv) * gv[c].y;
-            av[c].z = (xv[c].z * inv) * gv[c].z;
-            av[c].w = (xv[c].w * inv) * gv[c].w;
-            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(av[c].x), fabsf(av[c].y)), fmaxf(fabsf(av[c].z), fabsf(av[c].w))));
-        }
-    }
-    mx = wave_max_f32(mx);
-    if (lane == 0) red[wave] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    const double s = quant_scale(mx);
-    const float sf = (float)s;
-#pragma unroll
-    for (int c = 0; c < KCH; c++) {
-        const int idx = c * kNT + tid;
-        unsigned word = 0;
-        if (idx * 4 < K) {
-            const unsigned b0 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(av[c].x, sf)));
-            const unsigned b1 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(av[c].y, sf)));
-            const unsigned b2 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(av[c].z, sf)));
-            const unsigned b3 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(av[c].w, sf)));
-            word = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-        }
-        ((unsigned*)xs8)[idx] = word;
-    }
-    if (tid == 0) *xscale = s;
-    __syncthreads();
-}
 
 // ---------------------------------------------------------------------------
 // fused decode GEMV: y = epilogue(W . prologue(x)); 4 wavefronts x R rows

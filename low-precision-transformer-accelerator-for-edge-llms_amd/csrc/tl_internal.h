@@ -138,6 +138,63 @@ hipError_t launch_argmax_rows(hipStream_t s, const float* logits, int32_t rows, 
                               unsigned long long* keys);
 hipError_t init_kernels();
 hipError_t init_decode_kernels();
+// persistent batch-1 decode (tl_persist.hip)
+struct PLayer {
+    const int8_t* wqkv;
+    const float* sqkv;
+    const int8_t* wo;
+    const float* so;
+    const int8_t* wg;
+    const float* sg;
+    const int8_t* wu;
+    const float* su;
+    const int8_t* wd;
+    const float* sd;
+    const float* g_in;
+    const float* g_post;
+};
+
+struct PersistArgs {
+    const PLayer* layers;
+    int32_t n_layers;
+    const int8_t* lm_w;
+    const float* lm_s;
+    const float* g_final;
+    const int8_t* emb;
+    const float* emb_s;
+    const float* cosb;
+    const float* sinb;
+    KvGeom kv;
+    const float* kv_sk;
+    const float* kv_sv;
+    PwPlan plan;
+    float eps;
+    double attn_scale;
+    int32_t D, F, H, Hkv, V;
+    float* t_qkv;       // [D + 2 KVD]
+    float* t_att;       // [D]
+    float* t_xa;        // [D]  x after the attention block
+    float* t_h;         // [F]
+    float* t_x;         // [D]  layer output
+    unsigned* ctr;      // [8 phases][8 slices][32] producer counters (zero at launch)
+    unsigned long long* keys;  // [max steps] argmax key of each step (zero at launch)
+    unsigned* done;     // [max steps] workgroups that folded their rows into keys[step]
+    unsigned* err;
+    int32_t* status;    // [0] steps completed
+    int32_t seq, n_steps, eos_id, out_stride;
+    int32_t* token_cur;
+    int32_t* cursor;
+    int32_t* n_gen;
+    int32_t* tokens_out;
+    float* logit_out;
+};
+
+size_t persist_lds_bytes(int32_t qkv, int32_t f, int32_t max_pos);
+bool persist_supported(int32_t d, int32_t f, int32_t qkv);
+hipError_t launch_persist_decode(hipStream_t s, const PersistArgs& args, int32_t grid, size_t lds);
+hipError_t launch_fill_u32(hipStream_t s, unsigned* p, int32_t n, unsigned v);
+hipError_t persist_occupancy(int32_t d, int32_t f, size_t lds, int* blocks_per_cu);
+
 hipError_t launch_gemm32(hipStream_t s, int epi, const GemmArgs& a, int32_t splits, int32_t cfg);
 hipError_t launch_gemv_fused(hipStream_t s, int pro, int epi, const GemvArgs& a);
 hipError_t launch_attention_decode(hipStream_t s, const float* qkv, int32_t rows, int32_t n_heads, int32_t n_kv,

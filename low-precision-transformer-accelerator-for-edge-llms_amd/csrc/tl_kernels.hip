@@ -924,6 +924,12 @@ hipError_t launch_dequant_i32(hipStream_t s, const int32_t* acc, int64_t n, int3
     return hipGetLastError();
 }
 
+hipError_t launch_fill_u32(hipStream_t s, unsigned* p, int32_t n, unsigned v) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, s, p, n, v);
+    return hipGetLastError();
+}
+
 hipError_t launch_embed(hipStream_t s, const int32_t* tokens, int32_t rows, int32_t d, int32_t vocab,
                         const int8_t* emb, const float* emb_s, float* x) {
     if (rows <= 0) return hipSuccess;

@@ -37,6 +37,9 @@ struct LayerDev {
     float* g_post = nullptr;
 };
 
+constexpr int kPersistChunk = 64;   // decode steps per persistent launch at most
+constexpr int kPersistCounters = 8 * 8 * 32;   // phases x XCD slices x one 128-byte line
+
 struct ProfEvent {
     int kclass;
     hipEvent_t start, stop;
@@ -101,6 +104,21 @@ struct tl_handle {
     std::string err;
 
     bool use_graphs = true;
+
+    // persistent decode (tl_persist.hip)
+    bool use_persist = false;             // TL_PERSIST=1 turns on the single-kernel decode
+    bool persist_ok = false;              // geometry and occupancy allow it
+    int32_t persist_grid = 0;             // one workgroup per CU
+    size_t persist_lds = 0;
+    PLayer* d_players = nullptr;          // device copy of the layer pointers
+    bool players_dirty = true;
+    float* t_buf = nullptr;               // exchanged vectors: qkv | att | xa | h | x
+    size_t t_count = 0;
+    unsigned* pctr = nullptr;             // [kPersistCounters] phase counters
+    unsigned long long* pkeys = nullptr;  // [kPersistChunk] argmax key per step
+    unsigned* pdone = nullptr;            // [kPersistChunk]
+    unsigned* perr = nullptr;
+    int32_t* pstatus = nullptr;
     int gemm_cfg = -1;                    // < 0: choose the MFMA tile configuration per shape
     std::vector<hipGraphExec_t> graphs;   // captured batch-1 decode step per sequence
 
@@ -462,6 +480,53 @@ int32_t decode_step1(tl_handle* h, int32_t seq, int32_t max_t) {
     return lm_head_rows(h, h->x, 1, seq, 1);
 }
 
+// n_steps (<= kPersistChunk) greedy decode steps of sequence seq in one
+// persistent launch; stops after eos_id when it comes.  Waits for the launch.
+int32_t persist_run(tl_handle* h, int32_t seq, int32_t n_steps, int32_t eos_id, int32_t* steps_done) {
+    const tl_config& c = h->cfg;
+    if (h->players_dirty) {
+        std::vector<PLayer> pl(c.n_layers);
+        for (int l = 0; l < c.n_layers; l++) {
+            const LayerDev& L = h->layers[l];
+            pl[l] = PLayer{L.wqkv, L.sqkv, L.wo, L.so, L.wg, L.sg, L.wu, L.su, L.wd, L.sd, L.g_in, L.g_post};
+        }
+        TL_HIP(h, hipMemcpy(h->d_players, pl.data(), sizeof(PLayer) * c.n_layers, hipMemcpyHostToDevice));
+        h->players_dirty = false;
+    }
+    TL_LAUNCH(h, launch_fill_u32(h->stream, h->pctr, kPersistCounters, 0u));
+    TL_LAUNCH(h, launch_reset_keys(h->stream, h->pkeys, n_steps));
+    TL_LAUNCH(h, launch_fill_u32(h->stream, h->pdone, n_steps, 0u));
+    TL_LAUNCH(h, launch_fill_u32(h->stream, h->perr, 1, 0u));
+    PersistArgs a{};
+    a.layers = h->d_players;
+    a.n_layers = c.n_layers;
+    a.lm_w = h->lm_w; a.lm_s = h->lm_s; a.g_final = h->g_final;
+    a.emb = h->emb; a.emb_s = h->emb_s;
+    a.cosb = h->rope_cos; a.sinb = h->rope_sin;
+    a.kv = h->kv; a.kv_sk = h->kv_sk; a.kv_sv = h->kv_sv;
+    a.plan = h->plan; a.eps = c.rms_eps; a.attn_scale = 1.0 / sqrt((double)kHeadDim);
+    a.D = h->D; a.F = h->F; a.H = c.n_heads; a.Hkv = c.n_kv_heads; a.V = c.vocab;
+    a.t_qkv = h->t_buf;
+    a.t_att = a.t_qkv + h->QKV;
+    a.t_xa = a.t_att + h->D;
+    a.t_h = a.t_xa + h->D;
+    a.t_x = a.t_h + h->F;
+    a.ctr = h->pctr;
+    a.keys = h->pkeys; a.done = h->pdone; a.err = h->perr; a.status = h->pstatus;
+    a.seq = seq; a.n_steps = n_steps; a.eos_id = eos_id; a.out_stride = c.max_pos;
+    a.token_cur = h->token_cur; a.cursor = h->cursor; a.n_gen = h->n_gen;
+    a.tokens_out = h->tokens_out; a.logit_out = h->logit_out;
+    TL_LAUNCH(h, launch_persist_decode(h->stream, a, h->persist_grid, h->persist_lds));
+    int32_t st[2] = {0, 0};
+    unsigned err = 0;
+    TL_HIP(h, hipMemcpyAsync(&err, h->perr, sizeof err, hipMemcpyDeviceToHost, h->stream));
+    TL_HIP(h, hipMemcpyAsync(st, h->pstatus, sizeof(int32_t), hipMemcpyDeviceToHost, h->stream));
+    TL_HIP(h, hipStreamSynchronize(h->stream));
+    if (err) return fail(h, TL_ERR_INTERNAL, "persistent decode: a dependency wait timed out");
+    *steps_done = st[0];
+    return TL_OK;
+}
+
 int32_t decode_graph_launch(tl_handle* h, int32_t seq) {
     if ((int)h->graphs.size() < h->max_seqs) h->graphs.assign(h->max_seqs, nullptr);
     if (!h->graphs[seq]) {
@@ -577,6 +642,22 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
     h->kv.n_layers = c.n_layers;
     h->kv.n_kv_heads = c.n_kv_heads;
     h->kv.max_pos = c.max_pos;
+    h->t_count = (size_t)h->QKV + 3 * (size_t)D + (size_t)F;
+    if ((e = dalloc(h, &h->d_players, (size_t)c.n_layers)) || (e = dalloc(h, &h->t_buf, h->t_count)) ||
+        (e = dalloc(h, &h->pkeys, (size_t)kPersistChunk)) || (e = dalloc(h, &h->pdone, (size_t)kPersistChunk)) ||
+        (e = dalloc(h, &h->perr, 1)) || (e = dalloc(h, &h->pstatus, 4)) ||
+        (e = dalloc(h, &h->pctr, (size_t)kPersistCounters)))
+        return bad(e);
+    {
+        // persistent decode: one workgroup per CU, all resident at once, and at
+        // least one workgroup per query head for the attention phase
+        int per_cu = 0;
+        h->persist_grid = prop.multiProcessorCount;
+        h->persist_lds = persist_lds_bytes(h->QKV, F, c.max_pos);
+        h->persist_ok = persist_supported(D, F, h->QKV) && h->persist_grid >= c.n_heads &&
+                        persist_occupancy(D, F, h->persist_lds, &per_cu) == hipSuccess && per_cu >= 1;
+        (void)hipGetLastError();
+    }
     if ((e = hipMemsetAsync(h->kv.k, 0, kv_bytes, h->stream)) || (e = hipMemsetAsync(h->kv.v, 0, kv_bytes, h->stream)) ||
         (e = hipMemsetAsync(h->keys, 0, sizeof(unsigned long long) * max_seqs, h->stream)) ||
         (e = hipMemsetAsync(h->cursor, 0, sizeof(int32_t) * max_seqs, h->stream)) ||
@@ -591,6 +672,7 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
     if ((e = init_kernels())) return bad(e);
     if ((e = init_decode_kernels())) return bad(e);
     if (const char* env = std::getenv("TL_NO_GRAPHS")) h->use_graphs = env[0] == '0';
+    if (const char* env = std::getenv("TL_PERSIST")) h->use_persist = env[0] == '1';
     if (const char* env = std::getenv("TL_GEMM_CFG")) h->gemm_cfg = std::atoi(env);
     if ((e = hipStreamSynchronize(h->stream))) return bad(e);
     *out = h;
@@ -661,6 +743,7 @@ int32_t tl_load_layer(tl_handle* h, int32_t layer, const int8_t* const w[7], con
     TL_HIP(h, copy_in(h, L.sd, s[6], sizeof(float) * D, src));
     TL_HIP(h, copy_in(h, L.g_in, g_in, sizeof(float) * D, src));
     TL_HIP(h, copy_in(h, L.g_post, g_post, sizeof(float) * D, src));
+    h->players_dirty = true;
     return finish(h);
 }
 
@@ -1037,6 +1120,37 @@ int32_t tl_decode(tl_handle* h, int32_t seq, int32_t max_new, int32_t eos_id, co
     const bool per_step = eos_id >= 0 || abort_flag;
     const int32_t first = h->host_ngen[seq];
     int32_t r;
+    if (h->use_persist && h->persist_ok && !h->profiling) {
+        // persistent kernel: up to kPersistChunk steps per launch (one at a
+        // time when the host may abort); EOS is checked on the device
+        int32_t done = 0;
+        while (done < max_new) {
+            if (abort_flag && *abort_flag) {
+                if (stop_reason) *stop_reason = TL_STOP_HOST_ABORT;
+                break;
+            }
+            const int32_t chunk = abort_flag ? 1 : std::min(max_new - done, kPersistChunk);
+            int32_t got = 0;
+            if ((r = persist_run(h, seq, chunk, eos_id, &got))) return r;
+            h->host_cursor[seq] += got;
+            h->host_ngen[seq] += got;
+            done += got;
+            if (got < chunk) break;   // stopped after EOS
+            if (eos_id >= 0) {
+                int32_t last = -1;
+                TL_HIP(h, hipMemcpy(&last, h->tokens_out + (size_t)seq * c.max_pos + first + done - 1, sizeof last,
+                                    hipMemcpyDeviceToHost));
+                if (last == eos_id) break;
+            }
+        }
+        *n_out = done;
+        if (done > 0)
+            TL_HIP(h, hipMemcpy(tokens_out, h->tokens_out + (size_t)seq * c.max_pos + first, sizeof(int32_t) * done,
+                                hipMemcpyDeviceToHost));
+        if (stop_reason && *stop_reason == TL_STOP_NONE)
+            *stop_reason = (eos_id >= 0 && done > 0 && tokens_out[done - 1] == eos_id) ? TL_STOP_EOS : TL_STOP_MAX_TOKENS;
+        return TL_OK;
+    }
     if ((r = upload_rows(h, 1, seq, false, h->host_cursor[seq]))) return r;
     for (int step = 0; step < max_new; step++) {
         if (abort_flag && *abort_flag) {

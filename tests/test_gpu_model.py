@@ -65,7 +65,14 @@ def small_model():
     return oracle.synthetic_model(dict(oracle.SMALL_CFG), seed=11)
 
 
-def test_generate_matches_oracle(small_model):
+# the two batch-1 decode paths: per-layer kernels replayed as a HIP graph
+# (default) and the single persistent kernel (TL_PERSIST=1 at engine creation)
+DECODE_PATHS = pytest.mark.parametrize("persist", ["0", "1"], ids=["graph", "persistent"])
+
+
+@DECODE_PATHS
+def test_generate_matches_oracle(small_model, persist, monkeypatch):
+    monkeypatch.setenv("TL_PERSIST", persist)
     eng = engine_for(small_model)
     prompt = np.array([5, 17, 1000, 3, 3, 2047, 64], np.int32)
     got, stop = eng.generate(prompt, 24)
@@ -98,8 +105,10 @@ def test_prefill_cache_equals_sequential_decode(small_model):
     eng.close()
 
 
-def test_generate_eos_and_abort(small_model):
+@DECODE_PATHS
+def test_generate_eos_and_abort(small_model, persist, monkeypatch):
     import ctypes
+    monkeypatch.setenv("TL_PERSIST", persist)
     eng = engine_for(small_model)
     prompt = np.array([1, 2, 3], np.int32)
     free, _ = eng.generate(prompt, 12)
@@ -236,4 +245,29 @@ def test_prefill_512_tinyllama_shape():
             k, v = eng.kv_read(0, layer, g, 0, prompt.size)
             assert_bits_equal(k, kc[layer, g, :prompt.size], f"K layer {layer} head {g}")
             assert_bits_equal(v, vc[layer, g, :prompt.size], f"V layer {layer} head {g}")
+    eng.close()
+
+
+@DECODE_PATHS
+def test_generate_tinyllama_shape_matches_oracle(persist, monkeypatch):
+    """Greedy generation on a 2-layer TinyLlama-shape model (hidden 2048, FFN
+    5632, 32/4 heads, vocab 32000), on either decode path: the oracle's token
+    ids and KV rows."""
+    monkeypatch.setenv("TL_PERSIST", persist)
+    cfg = dict(oracle.TINYLLAMA_CFG, n_layers=2)
+    m = oracle.synthetic_model(cfg, seed=31)
+    prompt = np.random.default_rng(9).integers(0, cfg["vocab"], 20).astype(np.int32)
+    eng = engine_for(m)
+    got, stop = eng.generate(prompt, 12)
+    assert stop == "max_tokens"
+    orc = oracle.Oracle(m)
+    kc, vc = m.new_cache()
+    want, _ = orc.generate(prompt, 12, cache=(kc, vc))
+    assert_bits_equal(got, want, "token ids")
+    n = prompt.size + 11   # rows written: prompt + every fed-back token but the last
+    for layer in range(2):
+        for g in range(4):
+            k, v = eng.kv_read(0, layer, g, 0, n)
+            assert_bits_equal(k, kc[layer, g, :n], f"K layer {layer} head {g}")
+            assert_bits_equal(v, vc[layer, g, :n], f"V layer {layer} head {g}")
     eng.close()
