@@ -400,6 +400,217 @@ __global__ __launch_bounds__(NW * 64) void attention_decode_kernel(AttnDecodeArg
     }
 }
 
+// ---------------------------------------------------------------------------
+// decode attention, one workgroup (4 wavefronts) per (row, query head), same
+// arithmetic as attention_decode_kernel<1, ...>.  Wavefront w owns the key
+// blocks b = w + 4 i (64 keys each) for scores, exponentials, probabilities
+// and P.V (the V groups 4 b .. 4 b + 3 are the same keys), so only the row's
+// Q scale, the score maximum, the block sums and the output cross
+// wavefronts: four barriers.  The K/V rows of the first KPF blocks are
+// requested right after the few Q/K/V values this workgroup needs, before
+// any of them is awaited.  Every wavefront keeps its own copy of the head's
+// INT8 Q and of this row's INT8 K (lane d <-> dimension d; RoPE's partner
+// dimension d ^ 32 is lane d ^ 32 of the same wavefront).
+// ---------------------------------------------------------------------------
+constexpr int kRowQPerThread = 16;   // Q width <= 16 x 256
+
+template <int KPF>
+__global__ __launch_bounds__(256) void attention_row_kernel(AttnDecodeArgs p) {
+    constexpr int NW = 4, KB = 4;
+    extern __shared__ __align__(16) float dyn[];
+    __shared__ __align__(16) int8_t qs[NW][64];
+    __shared__ __align__(16) int8_t kn[NW][64];
+    __shared__ float red[NW], wmax[NW];
+    __shared__ int accs[NW][64];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int G = p.n_heads / p.n_kv;
+    int h0 = blockIdx.x;
+    if (p.n_heads == 32 && p.n_kv == 4) {
+        // the 8 query heads of a KV head on two XCDs (workgroups go round-robin
+        // over the 8 XCDs), so its K/V rows are shared through their L2 caches
+        const int xcd = h0 & 7, slot = h0 >> 3;
+        h0 = (xcd >> 1) * 8 + (xcd & 1) * 4 + slot;
+    }
+    const int g = h0 / G, row = blockIdx.y;
+    const int D = p.n_heads * kHeadDim, KVD = p.n_kv * kHeadDim, W = D + 2 * KVD;
+    const int pos = p.rm.pos[row], seq = p.rm.seq[row];
+    const int T = pos + 1, tpad = (T + 63) & ~63, nblk = tpad >> 6;
+    const int64_t pl = p.kv.plane(seq, p.layer, g);
+    const int8_t* kp = p.kv.k + pl;
+    const int8_t* vp = p.kv.v + pl;
+    float* s_buf = dyn;                          // [tpad] scores, then exponentials
+    int8_t* p8 = (int8_t*)(dyn + tpad);          // [tpad]
+    float* bsum = (float*)(p8 + tpad);           // [nblk]
+    const float* src = p.qkv + (int64_t)row * W;
+    const int d = lane;
+
+    // 1) RoPE factors, every Q element (the row's scale is the max over all
+    //    heads; element tid + 256 j has dimension d), this head's Q, this
+    //    row's K and V (clamped, in-bounds indices) ...
+    const float cs = p.cosb[(int64_t)pos * kHeadDim + d];
+    const float sn = p.sinb[(int64_t)pos * kHeadDim + d];
+    const int nq = D / kNT;   // D is a multiple of 256 (64 x heads, heads % 4 == 0 checked at launch)
+    float qv[kRowQPerThread];
+#pragma unroll
+    for (int j = 0; j < kRowQPerThread; j++) qv[j] = src[min(tid + kNT * j, D - 1)];
+    const float qh = src[h0 * kHeadDim + d];
+    const float kx = src[D + g * kHeadDim + d];
+    const float vx = src[D + KVD + g * kHeadDim + d];
+    const float sk = p.kv_sk[p.layer * p.n_kv + g], sv = p.kv_sv[p.layer * p.n_kv + g];
+    // ... then the cached K/V rows of this wavefront's first KPF blocks (rows
+    //    0..pos-1 are final; block indices clamped inside the plane, surplus
+    //    copies unused)
+    v4i kreg[KPF][4], vreg[KPF][4];
+#pragma unroll
+    for (int i = 0; i < KPF; i++) {
+        const int b = min(wave + NW * i, nblk - 1);
+#pragma unroll
+        for (int q = 0; q < 4; q++) kreg[i][q] = ld16(kp + (int64_t)b * 4096 + q * 1024 + lane * 16);
+#pragma unroll
+        for (int q = 0; q < 4; q++) vreg[i][q] = ld16(vp + (int64_t)(4 * b + q) * 1024 + lane * 16);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2) RoPE of every Q element -> row maximum
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kRowQPerThread; j++) {
+        const float o = __shfl_xor(qv[j], 32);
+        const float rot = d < 32 ? -o : o;
+        if (j < nq) mx = fmaxf(mx, fabsf((qv[j] * cs) + (rot * sn)));
+    }
+    mx = wave_max_f32(mx);
+    if (lane == 0) red[wave] = mx;
+    // this head's rotated Q, this row's K (RoPE, static scale) and V
+    const float qo = __shfl_xor(qh, 32), ko = __shfl_xor(kx, 32);
+    const float qr = (qh * cs) + ((d < 32 ? -qo : qo) * sn);
+    const float kr = (kx * cs) + ((d < 32 ? -ko : ko) * sn);
+    const int8_t k8 = sat_i8(__builtin_rintf(__fdiv_rn(kr, sk)));
+    const int8_t v8 = sat_i8(__builtin_rintf(__fdiv_rn(vx, sv)));
+    kn[wave][d] = k8;
+    if (h0 % G == 0 && wave == 0) {   // the first query head of the KV head appends the row
+        p.kv.k[pl + KvGeom::k_off(pos, d)] = k8;
+        p.kv.v[pl + KvGeom::v_off(pos, d)] = v8;
+    }
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const double s_q = quant_scale(mx);
+    qs[wave][d] = sat_i8(__builtin_rintf(__fdiv_rn(qr, (float)s_q)));
+    const float scl = (float)((s_q * (double)sk) * p.attn_scale);
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");   // qs, kn: written and read by this wavefront
+
+    // 3) scores of this wavefront's keys (lane <-> key)
+    const v4i* q4 = (const v4i*)qs[wave];
+    const v4i* kn4 = (const v4i*)kn[wave];
+    float lmax = -INFINITY;
+    auto score_block = [&](int b, v4i k0, v4i k1, v4i k2, v4i k3) {
+        const int t = b * 64 + lane;
+        if (t < T) {
+            if (t == pos) {
+                k0 = kn4[0];
+                k1 = kn4[1];
+                k2 = kn4[2];
+                k3 = kn4[3];
+            }
+            int S = sdot4v(k0, q4[0], 0);
+            S = sdot4v(k1, q4[1], S);
+            S = sdot4v(k2, q4[2], S);
+            S = sdot4v(k3, q4[3], S);
+            const float s = (float)S * scl;
+            s_buf[t] = s;
+            lmax = fmaxf(lmax, s);
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < KPF; i++)
+        if (wave + NW * i < nblk) score_block(wave + NW * i, kreg[i][0], kreg[i][1], kreg[i][2], kreg[i][3]);
+    for (int b0 = wave + NW * KPF; b0 < nblk; b0 += NW * KB) {
+        v4i kk[KB][4];
+#pragma unroll
+        for (int i = 0; i < KB; i++) {
+            const int8_t* kb = kp + (int64_t)min(b0 + NW * i, nblk - 1) * 4096 + lane * 16;
+#pragma unroll
+            for (int q = 0; q < 4; q++) kk[i][q] = ld16(kb + q * 1024);
+        }
+#pragma unroll
+        for (int i = 0; i < KB; i++)
+            if (b0 + NW * i < nblk) score_block(b0 + NW * i, kk[i][0], kk[i][1], kk[i][2], kk[i][3]);
+    }
+    lmax = wave_max_f32(lmax);
+    if (lane == 0) wmax[wave] = lmax;
+    __syncthreads();
+    const float m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+
+    // 4) exponentials and block-64 butterfly sums of this wavefront's keys
+    for (int b = wave; b < nblk; b += NW) {
+        const int t = b * 64 + lane;
+        float e = 0.0f;
+        if (t < T) {
+            e = tl_expf(s_buf[t] - m);
+            s_buf[t] = e;
+        }
+        const float bs = wave_butterfly_sum(e);
+        if (lane == 0) bsum[b] = bs;
+    }
+    __syncthreads();
+    float tot = 0.0f;
+    for (int b = 0; b < nblk; b++) tot = tot + bsum[b];
+
+    // 5) INT8 probabilities of this wavefront's keys, then P . V over the
+    //    same keys (lane <-> dimension; this row's V is v8 of lane d)
+    for (int b = wave; b < nblk; b += NW) {
+        const int t = b * 64 + lane;
+        int8_t pq = 0;
+        if (t < T) {
+            float pr = __builtin_rintf(__fdiv_rn(s_buf[t], tot) * 127.0f);
+            pr = pr < 0.0f ? 0.0f : (pr > 127.0f ? 127.0f : pr);
+            pq = (int8_t)(int)pr;
+        }
+        p8[t] = pq;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");   // p8 of these keys: this wavefront's
+    int o = 0;
+    const int cpos = pos >> 4, bpos = pos & 15;
+    auto pv_group = [&](int c, v4i vv) {
+        if (c == cpos) {
+            const unsigned nb = (uint8_t)v8;
+            const int sh = (bpos & 3) * 8;
+            const unsigned keep = ~(0xFFu << sh);
+            const int q = bpos >> 2;
+            vv[q] = (int)(((unsigned)vv[q] & keep) | (nb << sh));
+        }
+        o = sdot4v(vv, *(const v4i*)(p8 + c * 16), o);
+    };
+#pragma unroll
+    for (int i = 0; i < KPF; i++) {
+        const int b = wave + NW * i;
+        if (b < nblk)
+#pragma unroll
+            for (int q = 0; q < 4; q++) pv_group(4 * b + q, vreg[i][q]);
+    }
+    for (int b0 = wave + NW * KPF; b0 < nblk; b0 += NW * KB) {
+        v4i vv[KB][4];
+#pragma unroll
+        for (int i = 0; i < KB; i++) {
+            const int b = min(b0 + NW * i, nblk - 1);
+#pragma unroll
+            for (int q = 0; q < 4; q++) vv[i][q] = ld16(vp + (int64_t)(4 * b + q) * 1024 + lane * 16);
+        }
+#pragma unroll
+        for (int i = 0; i < KB; i++)
+            if (b0 + NW * i < nblk)
+#pragma unroll
+                for (int q = 0; q < 4; q++) pv_group(4 * (b0 + NW * i) + q, vv[i][q]);
+    }
+    accs[wave][lane] = o;
+    __syncthreads();
+    if (tid < 64) {
+        const int O = accs[0][tid] + accs[1][tid] + accs[2][tid] + accs[3][tid];
+        p.out[(int64_t)row * D + (int64_t)h0 * kHeadDim + tid] = (float)O * deq_mult(1.0 / 127.0, sv);
+    }
+}
+
 // embedding of each row's current token and the row's position (= its
 // sequence's cursor) for this step
 __global__ __launch_bounds__(256) void embed_step_kernel(const int32_t* __restrict__ tok_by_seq,
@@ -469,7 +680,10 @@ hipError_t launch_attention_decode(hipStream_t s, const float* qkv, int32_t rows
     const int D = n_heads * kHeadDim, W = D + 2 * n_kv * kHeadDim;
     const int tpad = (max_t + 63) & ~63;
     AttnDecodeArgs p{qkv, n_heads, n_kv, rm, cos, sin, kv, layer, kv_sk, kv_sv, 1.0 / sqrt((double)kHeadDim), out};
-    if (hpw == 1) {
+    if (hpw == 1 && n_heads % 4 == 0 && D <= kRowQPerThread * kNT) {
+        const size_t lds = (size_t)tpad * 5 + (tpad / 64) * 4 + 16;
+        hipLaunchKernelGGL((attention_row_kernel<2>), dim3(n_heads, rows), dim3(256), lds, s, p);
+    } else if (hpw == 1) {
         const size_t lds = sizeof(float) * W + (size_t)tpad * 4 + tpad + (tpad / 64) * 4 + 64;
         hipLaunchKernelGGL((attention_decode_kernel<1, 2, 8, 4>), dim3(n_heads, rows), dim3(256), lds, s, p);
     } else if (hpw == 8 && G == 8) {
@@ -493,6 +707,9 @@ hipError_t launch_embed_step(hipStream_t s, const int32_t* tok_by_seq, const int
 hipError_t init_decode_kernels() {
     hipError_t e = hipFuncSetAttribute((const void*)attention_decode_kernel<8, 2, 4, 8>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, 120 * 1024);
+    if (e != hipSuccess) return e;
+    e = hipFuncSetAttribute((const void*)attention_row_kernel<2>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            120 * 1024);
     if (e != hipSuccess) return e;
     return hipFuncSetAttribute((const void*)attention_decode_kernel<1, 2, 8, 4>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);

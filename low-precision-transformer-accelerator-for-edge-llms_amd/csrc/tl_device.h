@@ -153,10 +153,15 @@ TL_DEV float block_pairwise_sum(const float* sq, PwPlan plan, float* scr) {
     float* lv0 = scr + 8 * L;    // [L]
     float* lv1 = lv0 + L;        // [L]
     for (int idx = tid; idx < 8 * L; idx += nt) {
-        const float* a = sq + (idx >> 3) * len;
-        const int j = idx & 7;
-        float r = a[j];
-        for (int i = 8; i < len; i += 8) r = r + a[i + j];
+        // leaf_len <= 128: at most 16 steps, read before the in-order sum
+        const float* a = sq + (idx >> 3) * len + (idx & 7);
+        float v[16];
+#pragma unroll
+        for (int t = 0; t < 16; t++) v[t] = a[min(8 * t, len - 8)];
+        float r = v[0];
+#pragma unroll
+        for (int t = 1; t < 16; t++)
+            if (8 * t < len) r = r + v[t];
         part[idx] = r;
     }
     __syncthreads();

@@ -20,6 +20,7 @@
 
 #include "tl_device.h"
 #include "tl_internal.h"
+#include "tl_prologue.h"
 
 namespace tl {
 
@@ -79,6 +80,57 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const float* __restr
         if (FLOAT_SCALE) ((float*)scales)[row] = sf;
         else ((double*)scales)[row] = s;
     }
+}
+
+// the same two row operations for rows of width n <= 1024 KCH, n % 64 == 0,
+// 16-byte aligned, one workgroup per row: float4 loads, the decode GEMV
+// prologues (identical arithmetic: NumPy pairwise tree, per-row scale), and
+// 16-byte stores of the INT8 row
+template <int PRO, int KCH>
+__global__ __launch_bounds__(kNT) void rows_prologue_kernel(const float* __restrict__ x, const float* __restrict__ g,
+                                                           int32_t n, float eps, PwPlan plan, int8_t* __restrict__ q,
+                                                           double* __restrict__ scales) {
+    __shared__ __align__(16) int8_t xs8[KCH * 1024];
+    __shared__ __align__(16) float sq[PRO == PRO_RMSNORM ? KCH * 1024 : 4];
+    __shared__ float part[PRO == PRO_RMSNORM ? 8 * 64 : 4];
+    __shared__ float red[16];
+    __shared__ double xscale;
+    const int tid = threadIdx.x, row = blockIdx.x;
+    const float4* xr = (const float4*)(x + (int64_t)row * n);
+    const int kq = n / 4 - 1;
+    float4 xv[KCH], gv[KCH];
+#pragma unroll
+    for (int c = 0; c < KCH; c++) {
+        const int idx = min(c * kNT + tid, kq);
+        xv[c] = xr[idx];
+        if (PRO == PRO_RMSNORM) gv[c] = ((const float4*)g)[idx];
+    }
+    if (PRO == PRO_QUANT) prologue_quant<KCH>(xv, n, xs8, red, &xscale);
+    else prologue_rmsnorm<KCH>(xv, gv, n, eps, plan, sq, part, xs8, red, &xscale);
+    int8_t* qr = q + (int64_t)row * n;
+    for (int o = tid * 16; o < n; o += kNT * 16) *(v4i*)(qr + o) = *(const v4i*)(xs8 + o);
+    if (tid == 0) scales[row] = xscale;
+}
+
+template <int PRO>
+static hipError_t launch_rows_prologue(hipStream_t s, const float* x, const float* g, int32_t rows, int32_t n,
+                                       float eps, PwPlan plan, int8_t* q, double* scales) {
+    const dim3 grid(rows), block(kNT);
+    switch ((n + 1023) / 1024) {
+        case 1: hipLaunchKernelGGL((rows_prologue_kernel<PRO, 1>), grid, block, 0, s, x, g, n, eps, plan, q, scales); break;
+        case 2: hipLaunchKernelGGL((rows_prologue_kernel<PRO, 2>), grid, block, 0, s, x, g, n, eps, plan, q, scales); break;
+        case 3: hipLaunchKernelGGL((rows_prologue_kernel<PRO, 3>), grid, block, 0, s, x, g, n, eps, plan, q, scales); break;
+        case 4: hipLaunchKernelGGL((rows_prologue_kernel<PRO, 4>), grid, block, 0, s, x, g, n, eps, plan, q, scales); break;
+        case 5: hipLaunchKernelGGL((rows_prologue_kernel<PRO, 5>), grid, block, 0, s, x, g, n, eps, plan, q, scales); break;
+        case 6: hipLaunchKernelGGL((rows_prologue_kernel<PRO, 6>), grid, block, 0, s, x, g, n, eps, plan, q, scales); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+static bool rows_fast_ok(const void* x, const void* g, const void* q, int32_t n) {
+    const uintptr_t bits = (uintptr_t)x | (uintptr_t)g | (uintptr_t)q;
+    return n % 64 == 0 && n <= 6 * 1024 && bits % 16 == 0;
 }
 
 // per-tensor quantize_int8 over n elements (two passes: global max, then quantize)
@@ -761,6 +813,8 @@ hipError_t launch_rmsnorm_quant(hipStream_t s, const float* x, const float* g, i
                                 int32_t n, float eps, PwPlan plan, float* y, int8_t* q,
                                 double* scales) {
     if (rows <= 0) return hipSuccess;
+    if (!y && plan.n_leaves <= 64 && rows_fast_ok(x, g, q, n))
+        return launch_rows_prologue<PRO_RMSNORM>(s, x, g, rows, n, eps, plan, q, scales);
     const size_t lds = sizeof(float) * ((size_t)2 * n + 10 * (size_t)plan.n_leaves + 16);
     hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3(rows), dim3(256), lds, s, x, g, n, eps, plan, y, q, scales);
     return hipGetLastError();
@@ -769,6 +823,8 @@ hipError_t launch_rmsnorm_quant(hipStream_t s, const float* x, const float* g, i
 hipError_t launch_quantize_rows(hipStream_t s, const float* x, int32_t rows, int32_t n, int8_t* q,
                                 double* scales) {
     if (rows <= 0) return hipSuccess;
+    if (rows_fast_ok(x, nullptr, q, n))
+        return launch_rows_prologue<PRO_QUANT>(s, x, nullptr, rows, n, 0.0f, PwPlan{8, 1}, q, scales);
     hipLaunchKernelGGL(quantize_rows_kernel<false>, dim3(rows), dim3(256), 0, s, x, n, q, (void*)scales);
     return hipGetLastError();
 }

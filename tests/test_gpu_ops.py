@@ -98,6 +98,11 @@ def test_rmsnorm_quant(rt, n, rows):
     assert_bits_equal(host(y), want_y, "rmsnorm")
     assert_bits_equal(host(q), want_q, "q")
     assert_bits_equal(host(s), want_s, "scale")
+    # without the float output: the one-workgroup-per-row vectorized kernel
+    q2, s2 = empty((rows, n), np.int8), empty(rows, np.float64)
+    rt.call("tl_rmsnorm_quant", dev(x), dev(g), rows, n, None, q2, s2)
+    assert_bits_equal(host(q2), want_q, "q (no float output)")
+    assert_bits_equal(host(s2), want_s, "scale (no float output)")
 
 
 def test_quantize_rows_and_tensor(rt):
@@ -109,6 +114,13 @@ def test_quantize_rows_and_tensor(rt):
     want_q, want_s = oracle.quantize_rows(x)
     assert_bits_equal(host(q), want_q, "rows q")
     assert_bits_equal(host(s), want_s, "rows s")
+    # a width that is not a multiple of 64 takes the general row kernel
+    xo = np.ascontiguousarray(x[:, :1000])
+    qo, so = empty((4, 1000), np.int8), empty(4, np.float64)
+    rt.call("tl_quantize_rows", dev(xo), 4, 1000, qo, so)
+    want_qo, want_so = oracle.quantize_rows(xo)
+    assert_bits_equal(host(qo), want_qo, "rows q (n = 1000)")
+    assert_bits_equal(host(so), want_so, "rows s (n = 1000)")
     qt, st = empty((4, 5632), np.int8), empty(1, np.float64)
     rt.call("tl_quantize_tensor", dev(x), x.size, qt, st)
     wq, ws = oracle.quantize_int8(x)
