@@ -231,6 +231,19 @@ def bench_batch(model_eng_factory, host_seed, B=32, ctx=2048, steps=64):
             "frac": round((weights + kv) / step_s / 1e9 / HBM_PEAK_GBS, 4), "tokens_out": int(out.size)}
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter's reading for a
+    device-to-device copy of known size), or None when it has not been measured."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f).get(kernel)
+    except (OSError, ValueError):
+        return None
+    return None if rec is None else rec.get("traffic_bytes")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -244,6 +257,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--no-extras", action="store_true", help="skip the GEMV, layer and batch-32 workloads")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="only copy this many MiB device to device once (a kernel of known traffic for "
+                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this build measures the single-GPU hot path only "
@@ -253,6 +269,15 @@ def main():
         sys.exit("prompt + steps exceeds the 2048-position context")
 
     import torch
+    if args.copy_calibration_mib > 0:
+        n = args.copy_calibration_mib << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "read": n, "written": n}), flush=True)
+        return
     import __graft_entry__
     __graft_entry__.load_package()
     from lpta.engine import Engine
@@ -370,7 +395,8 @@ def main():
                    "kv_cache": "int8, static per-layer/per-kv-head scales"},
         "roofline": {"bound": "hbm", "kernel": "gemv_glu (gate+up SiLU-GLU decode GEMV)",
                      "achieved": glu["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": glu["frac"],
-                     "traffic": None, "bytes_per_launch": glu["bytes"], "avg_us": glu["avg_us"]},
+                     "traffic": measured_traffic("gemv_glu"), "bytes_per_launch": glu["bytes"],
+                     "avg_us": glu["avg_us"]},
         "decode_gemv_gbs": round(gemv_bytes / (gemv_us * 1e-6) / 1e9, 1) if gemv_us else None,
         "decode_step_hbm_frac": (round(gemv_bytes / args.profile_steps / (dt / args.steps) / 1e9 / HBM_PEAK_GBS, 4)
                                  if args.profile_steps else None),

@@ -642,12 +642,12 @@ static hipError_t gemv_fused_r(hipStream_t s, const GemvArgs& a) {
     const int kch = cdiv(a.k, 1024);
     const dim3 grid(cdiv(a.n, kNW * R)), block(kNT);
     switch (kch) {
-        case 1: hipLaunchKernelGGL((gemv_fused_kernel<PRO, EPI, R, 1>), grid, block, 0, s, a); break;
-        case 2: hipLaunchKernelGGL((gemv_fused_kernel<PRO, EPI, R, 2>), grid, block, 0, s, a); break;
-        case 3: hipLaunchKernelGGL((gemv_fused_kernel<PRO, EPI, R, 3>), grid, block, 0, s, a); break;
-        case 4: hipLaunchKernelGGL((gemv_fused_kernel<PRO, EPI, R, 4>), grid, block, 0, s, a); break;
-        case 5: hipLaunchKernelGGL((gemv_fused_kernel<PRO, EPI, R, 5>), grid, block, 0, s, a); break;
-        case 6: hipLaunchKernelGGL((gemv_fused_kernel<PRO, EPI, R, 6>), grid, block, 0, s, a); break;
+        case 1: TL_KLAUNCH((gemv_fused_kernel<PRO, EPI, R, 1>), grid, block, 0, s, a); break;
+        case 2: TL_KLAUNCH((gemv_fused_kernel<PRO, EPI, R, 2>), grid, block, 0, s, a); break;
+        case 3: TL_KLAUNCH((gemv_fused_kernel<PRO, EPI, R, 3>), grid, block, 0, s, a); break;
+        case 4: TL_KLAUNCH((gemv_fused_kernel<PRO, EPI, R, 4>), grid, block, 0, s, a); break;
+        case 5: TL_KLAUNCH((gemv_fused_kernel<PRO, EPI, R, 5>), grid, block, 0, s, a); break;
+        case 6: TL_KLAUNCH((gemv_fused_kernel<PRO, EPI, R, 6>), grid, block, 0, s, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -682,13 +682,13 @@ hipError_t launch_attention_decode(hipStream_t s, const float* qkv, int32_t rows
     AttnDecodeArgs p{qkv, n_heads, n_kv, rm, cos, sin, kv, layer, kv_sk, kv_sv, 1.0 / sqrt((double)kHeadDim), out};
     if (hpw == 1 && n_heads % 4 == 0 && D <= kRowQPerThread * kNT) {
         const size_t lds = (size_t)tpad * 5 + (tpad / 64) * 4 + 16;
-        hipLaunchKernelGGL((attention_row_kernel<2>), dim3(n_heads, rows), dim3(256), lds, s, p);
+        TL_KLAUNCH((attention_row_kernel<2>), dim3(n_heads, rows), dim3(256), lds, s, p);
     } else if (hpw == 1) {
         const size_t lds = sizeof(float) * W + (size_t)tpad * 4 + tpad + (tpad / 64) * 4 + 64;
-        hipLaunchKernelGGL((attention_decode_kernel<1, 2, 8, 4>), dim3(n_heads, rows), dim3(256), lds, s, p);
+        TL_KLAUNCH((attention_decode_kernel<1, 2, 8, 4>), dim3(n_heads, rows), dim3(256), lds, s, p);
     } else if (hpw == 8 && G == 8) {
         const size_t lds = sizeof(float) * W + (size_t)8 * tpad * 4 + 8 * tpad + 8 * (tpad / 64) * 4 + 64;
-        hipLaunchKernelGGL((attention_decode_kernel<8, 2, 4, 8>), dim3(n_heads / 8, rows), dim3(512), lds, s, p);
+        TL_KLAUNCH((attention_decode_kernel<8, 2, 4, 8>), dim3(n_heads / 8, rows), dim3(512), lds, s, p);
     } else {
         return hipErrorInvalidValue;
     }
@@ -699,7 +699,7 @@ hipError_t launch_embed_step(hipStream_t s, const int32_t* tok_by_seq, const int
                              const int32_t* cursor, int32_t* row_pos, int32_t d, int32_t vocab, const int8_t* emb,
                              const float* emb_s, float* x) {
     if (rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(embed_step_kernel, dim3(rows), dim3(256), 0, s, tok_by_seq, seq_of_row, cursor, row_pos, d,
+    TL_KLAUNCH(embed_step_kernel, dim3(rows), dim3(256), 0, s, tok_by_seq, seq_of_row, cursor, row_pos, d,
                        vocab, emb, emb_s, x);
     return hipGetLastError();
 }

@@ -316,7 +316,7 @@ template <int WM, int WN, int TM, int TN, int BK, int PD, int KS, int EPI>
 static void go32(hipStream_t s, const GemmArgs& a, int32_t splits) {
     using G = GemmShape<WM, WN, TM, TN, BK, PD, KS>;
     const dim3 grid((a.n + G::BN - 1) / G::BN, (a.m + G::BM - 1) / G::BM, splits);
-    hipLaunchKernelGGL((gemm32_kernel<WM, WN, TM, TN, BK, PD, KS, EPI>), grid, dim3(G::kThreads), 0, s, a);
+    TL_KLAUNCH((gemm32_kernel<WM, WN, TM, TN, BK, PD, KS, EPI>), grid, dim3(G::kThreads), 0, s, a);
 }
 
 template <int EPI>

@@ -2,6 +2,7 @@
 // the C++ runtime (tl_runtime.hip).  Not part of the public C-ABI.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -209,5 +210,28 @@ hipError_t launch_kv_scatter(hipStream_t s, KvGeom kv, int32_t seq, int32_t laye
                              int32_t t0, int32_t n, const int8_t* k_rows, const int8_t* v_rows);
 hipError_t launch_kv_gather(hipStream_t s, KvGeom kv, int32_t seq, int32_t layer, int32_t g,
                             int32_t t0, int32_t n, int8_t* k_rows, int8_t* v_rows);
+
+// Kernel timing for the profiler.  While a profiled operation runs, its
+// first kernel records `start` when that kernel starts and every kernel
+// records `stop` when it ends: the dispatch's own timestamps, without queue or
+// launch time, so the durations are those a kernel trace reports.
+struct KernelTiming {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+    bool used = false;
+};
+KernelTiming& kernel_timing();   // this host thread's
+
+#define TL_KLAUNCH(kernel, grid, block, lds, stream, ...)                                                   \
+    do {                                                                                                   \
+        ::tl::KernelTiming& kt_ = ::tl::kernel_timing();                                                   \
+        if (kt_.stop) {                                                                                    \
+            hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, kt_.used ? nullptr : kt_.start, kt_.stop, \
+                                  0, __VA_ARGS__);                                                         \
+            kt_.used = true;                                                                               \
+        } else {                                                                                           \
+            hipLaunchKernelGGL(kernel, grid, block, lds, stream, __VA_ARGS__);                             \
+        }                                                                                                  \
+    } while (0)
 
 }  // namespace tl

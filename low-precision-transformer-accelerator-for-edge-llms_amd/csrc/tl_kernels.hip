@@ -117,12 +117,12 @@ static hipError_t launch_rows_prologue(hipStream_t s, const float* x, const floa
                                        float eps, PwPlan plan, int8_t* q, double* scales) {
     const dim3 grid(rows), block(kNT);
     switch ((n + 1023) / 1024) {
-        case 1: hipLaunchKernelGGL((rows_prologue_kernel<PRO, 1>), grid, block, 0, s, x, g, n, eps, plan, q, scales); break;
-        case 2: hipLaunchKernelGGL((rows_prologue_kernel<PRO, 2>), grid, block, 0, s, x, g, n, eps, plan, q, scales); break;
-        case 3: hipLaunchKernelGGL((rows_prologue_kernel<PRO, 3>), grid, block, 0, s, x, g, n, eps, plan, q, scales); break;
-        case 4: hipLaunchKernelGGL((rows_prologue_kernel<PRO, 4>), grid, block, 0, s, x, g, n, eps, plan, q, scales); break;
-        case 5: hipLaunchKernelGGL((rows_prologue_kernel<PRO, 5>), grid, block, 0, s, x, g, n, eps, plan, q, scales); break;
-        case 6: hipLaunchKernelGGL((rows_prologue_kernel<PRO, 6>), grid, block, 0, s, x, g, n, eps, plan, q, scales); break;
+        case 1: TL_KLAUNCH((rows_prologue_kernel<PRO, 1>), grid, block, 0, s, x, g, n, eps, plan, q, scales); break;
+        case 2: TL_KLAUNCH((rows_prologue_kernel<PRO, 2>), grid, block, 0, s, x, g, n, eps, plan, q, scales); break;
+        case 3: TL_KLAUNCH((rows_prologue_kernel<PRO, 3>), grid, block, 0, s, x, g, n, eps, plan, q, scales); break;
+        case 4: TL_KLAUNCH((rows_prologue_kernel<PRO, 4>), grid, block, 0, s, x, g, n, eps, plan, q, scales); break;
+        case 5: TL_KLAUNCH((rows_prologue_kernel<PRO, 5>), grid, block, 0, s, x, g, n, eps, plan, q, scales); break;
+        case 6: TL_KLAUNCH((rows_prologue_kernel<PRO, 6>), grid, block, 0, s, x, g, n, eps, plan, q, scales); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -816,7 +816,7 @@ hipError_t launch_rmsnorm_quant(hipStream_t s, const float* x, const float* g, i
     if (!y && plan.n_leaves <= 64 && rows_fast_ok(x, g, q, n))
         return launch_rows_prologue<PRO_RMSNORM>(s, x, g, rows, n, eps, plan, q, scales);
     const size_t lds = sizeof(float) * ((size_t)2 * n + 10 * (size_t)plan.n_leaves + 16);
-    hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3(rows), dim3(256), lds, s, x, g, n, eps, plan, y, q, scales);
+    TL_KLAUNCH(rmsnorm_quant_kernel, dim3(rows), dim3(256), lds, s, x, g, n, eps, plan, y, q, scales);
     return hipGetLastError();
 }
 
@@ -825,24 +825,24 @@ hipError_t launch_quantize_rows(hipStream_t s, const float* x, int32_t rows, int
     if (rows <= 0) return hipSuccess;
     if (rows_fast_ok(x, nullptr, q, n))
         return launch_rows_prologue<PRO_QUANT>(s, x, nullptr, rows, n, 0.0f, PwPlan{8, 1}, q, scales);
-    hipLaunchKernelGGL(quantize_rows_kernel<false>, dim3(rows), dim3(256), 0, s, x, n, q, (void*)scales);
+    TL_KLAUNCH(quantize_rows_kernel<false>, dim3(rows), dim3(256), 0, s, x, n, q, (void*)scales);
     return hipGetLastError();
 }
 
 hipError_t launch_quantize_weight_rows(hipStream_t s, const float* w, int32_t rows, int32_t n,
                                        int8_t* q, float* scales) {
     if (rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(quantize_rows_kernel<true>, dim3(rows), dim3(256), 0, s, w, n, q, (void*)scales);
+    TL_KLAUNCH(quantize_rows_kernel<true>, dim3(rows), dim3(256), 0, s, w, n, q, (void*)scales);
     return hipGetLastError();
 }
 
 hipError_t launch_quantize_tensor(hipStream_t s, const float* x, int64_t n, int8_t* q,
                                   double* scale, float* scratch_max) {
     unsigned* mx = (unsigned*)scratch_max;
-    hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(64), 0, s, mx, 1, 0u);
+    TL_KLAUNCH(fill_u32_kernel, dim3(1), dim3(64), 0, s, mx, 1, 0u);
     const int blocks = (int)std::min<int64_t>(1024, std::max<int64_t>(1, (n + 255) / 256));
-    if (n > 0) hipLaunchKernelGGL(tensor_absmax_kernel, dim3(blocks), dim3(256), 0, s, x, n, mx);
-    hipLaunchKernelGGL(tensor_quant_kernel, dim3(blocks), dim3(256), 0, s, x, n, mx, q, scale);
+    if (n > 0) TL_KLAUNCH(tensor_absmax_kernel, dim3(blocks), dim3(256), 0, s, x, n, mx);
+    TL_KLAUNCH(tensor_quant_kernel, dim3(blocks), dim3(256), 0, s, x, n, mx, q, scale);
     return hipGetLastError();
 }
 
@@ -851,12 +851,12 @@ static hipError_t gemv_r(hipStream_t s, const GemvArgs& a) {
     const int kch = ceil_div(a.k, 1024);
     const dim3 grid(ceil_div(a.n, 4 * R)), block(256);
     switch (kch) {
-        case 1: hipLaunchKernelGGL((gemv_kernel<R, 1, EPI>), grid, block, 0, s, a); break;
-        case 2: hipLaunchKernelGGL((gemv_kernel<R, 2, EPI>), grid, block, 0, s, a); break;
-        case 3: hipLaunchKernelGGL((gemv_kernel<R, 3, EPI>), grid, block, 0, s, a); break;
-        case 4: hipLaunchKernelGGL((gemv_kernel<R, 4, EPI>), grid, block, 0, s, a); break;
-        case 5: hipLaunchKernelGGL((gemv_kernel<R, 5, EPI>), grid, block, 0, s, a); break;
-        case 6: hipLaunchKernelGGL((gemv_kernel<R, 6, EPI>), grid, block, 0, s, a); break;
+        case 1: TL_KLAUNCH((gemv_kernel<R, 1, EPI>), grid, block, 0, s, a); break;
+        case 2: TL_KLAUNCH((gemv_kernel<R, 2, EPI>), grid, block, 0, s, a); break;
+        case 3: TL_KLAUNCH((gemv_kernel<R, 3, EPI>), grid, block, 0, s, a); break;
+        case 4: TL_KLAUNCH((gemv_kernel<R, 4, EPI>), grid, block, 0, s, a); break;
+        case 5: TL_KLAUNCH((gemv_kernel<R, 5, EPI>), grid, block, 0, s, a); break;
+        case 6: TL_KLAUNCH((gemv_kernel<R, 6, EPI>), grid, block, 0, s, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -890,7 +890,7 @@ template <int WTM, int WTN, int EPI>
 static void gemm_go(hipStream_t s, const GemmArgs& a, int32_t splits) {
     constexpr int BM = 32 * WTM, BN = 32 * WTN;
     const dim3 grid(ceil_div(a.n, BN), ceil_div(a.m, BM), splits);
-    hipLaunchKernelGGL((gemm_kernel<WTM, WTN, EPI>), grid, dim3(256), 0, s, a);
+    TL_KLAUNCH((gemm_kernel<WTM, WTN, EPI>), grid, dim3(256), 0, s, a);
 }
 
 template <int EPI>
@@ -915,10 +915,10 @@ hipError_t launch_gemm(hipStream_t s, int epi, const GemmArgs& a, int32_t splits
 hipError_t launch_gemm_reduce(hipStream_t s, int epi, const GemmArgs& a, int32_t splits) {
     const int blocks = (int)std::min<int64_t>(2048, ((int64_t)a.m * a.n + 255) / 256);
     switch (epi) {
-        case EPI_DEQUANT: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_DEQUANT>, dim3(blocks), dim3(256), 0, s, a, splits); break;
-        case EPI_DEQUANT_RES: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_DEQUANT_RES>, dim3(blocks), dim3(256), 0, s, a, splits); break;
-        case EPI_GLU: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_GLU>, dim3(blocks), dim3(256), 0, s, a, splits); break;
-        case EPI_RAW: hipLaunchKernelGGL(gemm_reduce_kernel<EPI_RAW>, dim3(blocks), dim3(256), 0, s, a, splits); break;
+        case EPI_DEQUANT: TL_KLAUNCH(gemm_reduce_kernel<EPI_DEQUANT>, dim3(blocks), dim3(256), 0, s, a, splits); break;
+        case EPI_DEQUANT_RES: TL_KLAUNCH(gemm_reduce_kernel<EPI_DEQUANT_RES>, dim3(blocks), dim3(256), 0, s, a, splits); break;
+        case EPI_GLU: TL_KLAUNCH(gemm_reduce_kernel<EPI_GLU>, dim3(blocks), dim3(256), 0, s, a, splits); break;
+        case EPI_RAW: TL_KLAUNCH(gemm_reduce_kernel<EPI_RAW>, dim3(blocks), dim3(256), 0, s, a, splits); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -931,7 +931,7 @@ hipError_t launch_qkv_post(hipStream_t s, const float* qkv, int32_t rows, int32_
     if (rows <= 0) return hipSuccess;
     const int D = n_heads * kHeadDim, KVD = n_kv_heads * kHeadDim;
     const size_t lds = sizeof(float) * ((size_t)(D + 2 * KVD) + D + KVD);
-    hipLaunchKernelGGL(qkv_post_kernel, dim3(rows), dim3(256), lds, s, qkv, n_heads, n_kv_heads, rm,
+    TL_KLAUNCH(qkv_post_kernel, dim3(rows), dim3(256), lds, s, qkv, n_heads, n_kv_heads, rm,
                        cos, sin, kv, layer, kv_sk, kv_sv, q8, q_scale, q_rot_out);
     return hipGetLastError();
 }
@@ -946,7 +946,7 @@ hipError_t launch_attention(hipStream_t s, const int8_t* q8, const double* q_sca
     const int tpad = (max_t + 63) & ~63;
     const size_t lds = (size_t)G * tpad * sizeof(float) + (size_t)G * tpad + (size_t)G * (tpad / 64) * sizeof(float) + 16;
     const double attn_scale = 1.0 / sqrt((double)kHeadDim);
-    hipLaunchKernelGGL(attention_kernel, dim3(n_kv_heads, rows), dim3(256), lds, s, q8, q_scale, n_heads,
+    TL_KLAUNCH(attention_kernel, dim3(n_kv_heads, rows), dim3(256), lds, s, q8, q_scale, n_heads,
                        n_kv_heads, rm, kv, layer, kv_sk, kv_sv, attn_scale, out);
     return hipGetLastError();
 }
@@ -954,21 +954,21 @@ hipError_t launch_attention(hipStream_t s, const int8_t* q8, const double* q_sca
 hipError_t launch_rope(hipStream_t s, float* v, int32_t rows, int32_t n_heads, const int32_t* pos,
                        const float* cos, const float* sin) {
     if (rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(rope_kernel, dim3(rows), dim3(256), sizeof(float) * n_heads * kHeadDim, s, v,
+    TL_KLAUNCH(rope_kernel, dim3(rows), dim3(256), sizeof(float) * n_heads * kHeadDim, s, v,
                        n_heads, pos, cos, sin);
     return hipGetLastError();
 }
 
 hipError_t launch_softmax_rows(hipStream_t s, const float* x, int32_t rows, int32_t n, float* p) {
     if (rows <= 0 || n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(softmax_rows_kernel, dim3(rows), dim3(256), sizeof(float) * ((n + 63) / 64), s, x, n, p);
+    TL_KLAUNCH(softmax_rows_kernel, dim3(rows), dim3(256), sizeof(float) * ((n + 63) / 64), s, x, n, p);
     return hipGetLastError();
 }
 
 hipError_t launch_silu_mul(hipStream_t s, const float* g, const float* u, int64_t n, float* y) {
     if (n <= 0) return hipSuccess;
     const int blocks = (int)std::min<int64_t>(4096, (n + 255) / 256);
-    hipLaunchKernelGGL(silu_mul_kernel, dim3(blocks), dim3(256), 0, s, g, u, n, y);
+    TL_KLAUNCH(silu_mul_kernel, dim3(blocks), dim3(256), 0, s, g, u, n, y);
     return hipGetLastError();
 }
 
@@ -976,32 +976,32 @@ hipError_t launch_dequant_i32(hipStream_t s, const int32_t* acc, int64_t n, int3
                               const float* bias, float* y) {
     if (n <= 0) return hipSuccess;
     const int blocks = (int)std::min<int64_t>(4096, (n + 255) / 256);
-    hipLaunchKernelGGL(dequant_i32_kernel, dim3(blocks), dim3(256), 0, s, acc, n, cols, m, bias, y);
+    TL_KLAUNCH(dequant_i32_kernel, dim3(blocks), dim3(256), 0, s, acc, n, cols, m, bias, y);
     return hipGetLastError();
 }
 
 hipError_t launch_fill_u32(hipStream_t s, unsigned* p, int32_t n, unsigned v) {
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(fill_u32_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, s, p, n, v);
+    TL_KLAUNCH(fill_u32_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, s, p, n, v);
     return hipGetLastError();
 }
 
 hipError_t launch_embed(hipStream_t s, const int32_t* tokens, int32_t rows, int32_t d, int32_t vocab,
                         const int8_t* emb, const float* emb_s, float* x) {
     if (rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(embed_kernel, dim3(rows), dim3(256), 0, s, tokens, d, vocab, emb, emb_s, x);
+    TL_KLAUNCH(embed_kernel, dim3(rows), dim3(256), 0, s, tokens, d, vocab, emb, emb_s, x);
     return hipGetLastError();
 }
 
 hipError_t launch_reset_keys(hipStream_t s, unsigned long long* keys, int32_t n) {
-    hipLaunchKernelGGL(reset_keys_kernel, dim3(ceil_div(n, 64)), dim3(64), 0, s, keys, n);
+    TL_KLAUNCH(reset_keys_kernel, dim3(ceil_div(n, 64)), dim3(64), 0, s, keys, n);
     return hipGetLastError();
 }
 
 hipError_t launch_finalize_tokens(hipStream_t s, unsigned long long* keys, int32_t rows,
                                   int32_t* token_cur, int32_t* tokens_out, int32_t out_stride,
                                   int32_t* n_gen, int32_t* cursor, float* best_logit, int32_t advance) {
-    hipLaunchKernelGGL(finalize_tokens_kernel, dim3(ceil_div(rows, 64)), dim3(64), 0, s, keys, rows,
+    TL_KLAUNCH(finalize_tokens_kernel, dim3(ceil_div(rows, 64)), dim3(64), 0, s, keys, rows,
                        token_cur, tokens_out, out_stride, n_gen, cursor, best_logit, advance);
     return hipGetLastError();
 }
@@ -1009,7 +1009,7 @@ hipError_t launch_finalize_tokens(hipStream_t s, unsigned long long* keys, int32
 hipError_t launch_argmax_rows(hipStream_t s, const float* logits, int32_t rows, int32_t n,
                               unsigned long long* keys) {
     if (rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(argmax_rows_kernel, dim3(rows), dim3(256), 0, s, logits, n, keys);
+    TL_KLAUNCH(argmax_rows_kernel, dim3(rows), dim3(256), 0, s, logits, n, keys);
     return hipGetLastError();
 }
 
@@ -1022,7 +1022,7 @@ hipError_t init_kernels() {
 
 hipError_t launch_step_rows(hipStream_t s, const int32_t* seq_of_row, int32_t rows,
                             const int32_t* cursor, int32_t* row_pos) {
-    hipLaunchKernelGGL(step_rows_kernel, dim3(ceil_div(rows, 64)), dim3(64), 0, s, seq_of_row, rows,
+    TL_KLAUNCH(step_rows_kernel, dim3(ceil_div(rows, 64)), dim3(64), 0, s, seq_of_row, rows,
                        cursor, row_pos);
     return hipGetLastError();
 }
@@ -1030,7 +1030,7 @@ hipError_t launch_step_rows(hipStream_t s, const int32_t* seq_of_row, int32_t ro
 hipError_t launch_kv_scatter(hipStream_t s, KvGeom kv, int32_t seq, int32_t layer, int32_t g,
                              int32_t t0, int32_t n, const int8_t* k_rows, const int8_t* v_rows) {
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(kv_scatter_kernel, dim3(ceil_div((int64_t)n * kHeadDim, 256)), dim3(256), 0, s,
+    TL_KLAUNCH(kv_scatter_kernel, dim3(ceil_div((int64_t)n * kHeadDim, 256)), dim3(256), 0, s,
                        kv, kv.plane(seq, layer, g), t0, n, k_rows, v_rows);
     return hipGetLastError();
 }
@@ -1038,7 +1038,7 @@ hipError_t launch_kv_scatter(hipStream_t s, KvGeom kv, int32_t seq, int32_t laye
 hipError_t launch_kv_gather(hipStream_t s, KvGeom kv, int32_t seq, int32_t layer, int32_t g,
                             int32_t t0, int32_t n, int8_t* k_rows, int8_t* v_rows) {
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(kv_gather_kernel, dim3(ceil_div((int64_t)n * kHeadDim, 256)), dim3(256), 0, s,
+    TL_KLAUNCH(kv_gather_kernel, dim3(ceil_div((int64_t)n * kHeadDim, 256)), dim3(256), 0, s,
                        kv, kv.plane(seq, layer, g), t0, n, k_rows, v_rows);
     return hipGetLastError();
 }

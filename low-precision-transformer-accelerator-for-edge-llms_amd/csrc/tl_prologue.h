@@ -132,105 +132,4 @@ TL_DEV void prologue_rmsnorm(const float4 (&xv)[KCH], const float4 (&gv)[KCH], i
     __syncthreads();
 }
 
-// ---------------------------------------------------------------------------
-// NumPy pairwise sum of x[i]^2 over the perfect tree of `plan` with one
-// barrier.  Accumulator a = 8 leaf + j (j < 8) sums the squares at
-// leaf * len + j + 8 s, s < len / 8, in order, in a lane of its own (thread a
-// for pass 0, a - 256 for pass 1).  Butterflies over lane distance 1, 2, 4
-// then combine the eight accumulators of a leaf as
-// ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7)), and distances 8, 16, 32
-// the leaves of a wavefront pairwise; subtrees of eight leaves meet in LDS
-// and are combined pairwise by every thread.  Each addition adds the same
-// two operands as NumPy's tree (a + b and b + a round alike).
-// NP = 1 covers up to 32 leaves (256 accumulators), NP = 2 up to 64.
-// ---------------------------------------------------------------------------
-template <int NP>
-TL_DEV void sumsq_load(const float* x, PwPlan plan, float (&v)[NP][16]) {
-    const int nacc = 8 * plan.n_leaves, len = plan.leaf_len;
-#pragma unroll
-    for (int p = 0; p < NP; p++) {
-        const int a = min((int)threadIdx.x + p * kNT, nacc - 1);   // lanes past the last accumulator: a stand-in
-        const float* src = x + (a >> 3) * len + (a & 7);
-#pragma unroll
-        for (int t = 0; t < 16; t++) v[p][t] = src[min(8 * t, len - 8)];
-    }
-}
-
-template <int NP>
-TL_DEV float sumsq_reduce(const float (&v)[NP][16], PwPlan plan, float* red /* 8 floats */) {
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int nacc = 8 * plan.n_leaves, len = plan.leaf_len;
-#pragma unroll
-    for (int p = 0; p < NP; p++) {
-        const int a = tid + p * kNT;
-        float r = v[p][0] * v[p][0];
-#pragma unroll
-        for (int t = 1; t < 16; t++) {
-            const float q = v[p][t] * v[p][t];
-            if (8 * t < len) r = r + q;
-        }
-        r = r + __shfl_xor(r, 1);
-        r = r + __shfl_xor(r, 2);
-        r = r + __shfl_xor(r, 4);
-        for (int off = 8; off < 64 && off < nacc; off <<= 1) r = r + __shfl_xor(r, off);
-        // lane 0 of each group of 64 accumulators holds that subtree's sum
-        if (lane == 0 && a < nacc) red[a >> 6] = r;
-    }
-    __syncthreads();
-    const int nsub = nacc > 64 ? nacc >> 6 : 1;
-    float t[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) t[i] = i < nsub ? red[i] : 0.0f;
-#pragma unroll
-    for (int w = 8; w > 1; w >>= 1)
-        if (w <= nsub)
-#pragma unroll
-            for (int i = 0; i < w / 2; i++) t[i] = t[2 * i] + t[2 * i + 1];
-    return t[0];
-}
-
-// RMSNorm prologue with the squares summed by sumsq_reduce (v from
-// sumsq_load, issued with the activation loads): three barriers
-template <int KCH, int NP>
-TL_DEV void prologue_rmsnorm_v(const float4 (&xv)[KCH], const float4 (&gv)[KCH], const float (&v)[NP][16], int K,
-                               float eps, PwPlan plan, int8_t* xs8, float* red, double* xscale) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const float sum = sumsq_reduce<NP>(v, plan, red + 8);
-    const float var = __fdiv_rn(sum, (float)K);
-    const float inv = __fdiv_rn(1.0f, __builtin_sqrtf(var + eps));
-    float4 av[KCH];
-    float mx = 0.0f;
-#pragma unroll
-    for (int c = 0; c < KCH; c++) {
-        if ((c * kNT + tid) * 4 < K) {
-            av[c].x = (xv[c].x * inv) * gv[c].x;
-            av[c].y = (xv[c].y * inv) * gv[c].y;
-            av[c].z = (xv[c].z * inv) * gv[c].z;
-            av[c].w = (xv[c].w * inv) * gv[c].w;
-            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(av[c].x), fabsf(av[c].y)), fmaxf(fabsf(av[c].z), fabsf(av[c].w))));
-        }
-    }
-    mx = wave_max_f32(mx);
-    if (lane == 0) red[wave] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    const double s = quant_scale(mx);
-    const float sf = (float)s;
-#pragma unroll
-    for (int c = 0; c < KCH; c++) {
-        const int idx = c * kNT + tid;
-        unsigned word = 0;
-        if (idx * 4 < K) {
-            const unsigned b0 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(av[c].x, sf)));
-            const unsigned b1 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(av[c].y, sf)));
-            const unsigned b2 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(av[c].z, sf)));
-            const unsigned b3 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(av[c].w, sf)));
-            word = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-        }
-        ((unsigned*)xs8)[idx] = word;
-    }
-    if (tid == 0) *xscale = s;
-    __syncthreads();
-}
-
 }  // namespace tl

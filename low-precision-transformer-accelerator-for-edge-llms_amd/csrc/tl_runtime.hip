@@ -161,6 +161,15 @@ hipError_t dalloc(tl_handle* h, T** p, size_t count) {
     return e;
 }
 
+}  // namespace
+
+KernelTiming& tl::kernel_timing() {
+    thread_local KernelTiming t;
+    return t;
+}
+
+namespace {
+
 hipEvent_t take_event(tl_handle* h) {
     if (!h->event_pool.empty()) {
         hipEvent_t e = h->event_pool.back();
@@ -172,26 +181,34 @@ hipEvent_t take_event(tl_handle* h) {
     return e;
 }
 
-// optional per-kernel-class timing with events on the handle's stream
+// optional per-kernel-class timing: the kernels of one operation carry the
+// start / stop events themselves (see TL_KLAUNCH)
 struct Prof {
     tl_handle* h;
     int kc;
     double bytes;
-    hipEvent_t a = nullptr;
-    Prof(tl_handle* hh, int k, double b) : h(hh), kc(k), bytes(b) {
-        if (h->profiling) {
-            a = take_event(h);
-            if (a) hipEventRecord(a, h->stream);
-        }
+    hipEvent_t a = nullptr, b = nullptr;
+    KernelTiming saved;
+    Prof(tl_handle* hh, int k, double bb) : h(hh), kc(k), bytes(bb) {
+        if (!h->profiling) return;
+        a = take_event(h);
+        b = take_event(h);
+        if (!a || !b) return;
+        saved = kernel_timing();
+        kernel_timing() = KernelTiming{a, b, false};
     }
     ~Prof() {
-        if (h->profiling && a) {
-            hipEvent_t b = take_event(h);
-            if (b) {
-                hipEventRecord(b, h->stream);
+        if (!h->profiling) return;
+        if (a && b) {
+            const bool used = kernel_timing().used;
+            kernel_timing() = saved;
+            if (used) {
                 h->prof_pending.push_back({kc, a, b, bytes});
+                return;
             }
         }
+        if (a) h->event_pool.push_back(a);
+        if (b) h->event_pool.push_back(b);
     }
 };
 
