@@ -14,6 +14,7 @@ namespace tl {
 #define TL_DEV __device__ __forceinline__
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
 
 // ---------------------------------------------------------------------------
 // scalar helpers

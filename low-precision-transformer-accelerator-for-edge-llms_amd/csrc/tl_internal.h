@@ -119,6 +119,10 @@ hipError_t launch_qkv_post(hipStream_t s, const float* qkv, int32_t rows, int32_
                            int32_t n_kv_heads, RowMap rm, const float* cos, const float* sin,
                            KvGeom kv, int32_t layer, const float* kv_sk, const float* kv_sv,
                            int8_t* q8, double* q_scale, float* q_rot_out);
+constexpr int kTileMaxKeys = 4096;   // context limit of launch_attention_tiles (LDS)
+hipError_t launch_attention_tiles(hipStream_t s, const int8_t* q8, const double* q_scale, int32_t rows,
+                                  int32_t n_heads, int32_t n_kv_heads, int32_t seq, int32_t pos0, KvGeom kv,
+                                  int32_t layer, const float* kv_sk, const float* kv_sv, float* out);
 hipError_t launch_attention(hipStream_t s, const int8_t* q8, const double* q_scale, int32_t rows,
                             int32_t n_heads, int32_t n_kv_heads, RowMap rm, KvGeom kv,
                             int32_t layer, const float* kv_sk, const float* kv_sv, float* out,
@@ -139,6 +143,7 @@ hipError_t launch_argmax_rows(hipStream_t s, const float* logits, int32_t rows, 
                               unsigned long long* keys);
 hipError_t init_kernels();
 hipError_t init_decode_kernels();
+hipError_t init_prefill_kernels();
 // persistent batch-1 decode (tl_persist.hip)
 struct PLayer {
     const int8_t* wqkv;

@@ -617,6 +617,177 @@ __global__ __launch_bounds__(256) void attention_kernel(const int8_t* __restrict
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// prefill attention on i8 MFMA (v_mfma_i32_32x32x32_i8), same arithmetic as
+// attention_kernel: one workgroup (4 wavefronts) per (query head, tile of 32
+// consecutive rows of one sequence at positions pos0 + r).  The INT8 cache
+// layouts are the MFMA operand fragments: lane l of a K fragment holds 16
+// dimensions of key l % 32 (one 16-byte chunk of the K plane), lane l of a V
+// fragment 16 keys of dimension l % 32 (one chunk of the V plane).  In the
+// 32 x 32 output lane l, register i holds row 8 (i / 4) + 4 (l / 32) + i % 4
+// and key (or dimension) l % 32.
+//   pass A  S = Q K^T per 32-key tile, row maxima over each row's keys
+//   pass B  exponentials; a 64-key block is two tiles, so the block-64
+//           butterfly is the sum of the two tiles' values (distance 32) and
+//           then lane distances 16 .. 1 -- the order of the decode kernels;
+//           row totals in block order
+//   pass C  p8 = rne(127 e / total) into LDS (rows x keys)
+//   pass D  O = P8 . V per 32-key chunk, integer partials added in LDS
+// Scores are recomputed per pass (K is an L2 hit), so LDS does not grow with
+// the context beyond the INT8 probabilities.
+// ---------------------------------------------------------------------------
+struct AttnTileArgs {
+    const int8_t* q8;        // [rows][D]
+    const double* q_scale;   // [rows]
+    int32_t n_heads, n_kv, rows, seq, pos0, layer;
+    KvGeom kv;
+    const float* kv_sk;
+    const float* kv_sv;
+    double attn_scale;
+    float* out;              // [rows][D]
+};
+
+__global__ __launch_bounds__(256) void attention_tile_kernel(AttnTileArgs p) {
+    extern __shared__ __align__(16) int8_t tile_lds[];
+    __shared__ float scl[32], mrow[32], tot[32];
+    __shared__ float wmax[4][32];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 31, hi = lane >> 5;
+    const int h = blockIdx.x, r0 = blockIdx.y * 32;
+    const int G = p.n_heads / p.n_kv, g = h / G;
+    const int nr = min(32, p.rows - r0);
+    const int pos_first = p.pos0 + r0;
+    const int T = pos_first + nr;                  // the tile's last row sees keys 0 .. T - 1
+    const int tpad = (T + 63) & ~63, nblk = tpad >> 6;
+    int8_t* p8 = tile_lds;                         // [32][tpad]
+    float* bsum = (float*)(tile_lds + 32 * tpad);  // [32][nblk]
+    int* accs = (int*)(bsum + 32 * nblk);          // [32][64]
+    const int D = p.n_heads * kHeadDim;
+    const int64_t pl = p.kv.plane(p.seq, p.layer, g);
+    const int8_t* kp = p.kv.k + pl;
+    const int8_t* vp = p.kv.v + pl;
+    const float sk = p.kv_sk[p.layer * p.n_kv + g], sv = p.kv_sv[p.layer * p.n_kv + g];
+
+    // Q fragments (rows past the tile's last read a stand-in, never stored)
+    const int8_t* qrow = p.q8 + (int64_t)(r0 + min(col, nr - 1)) * D + h * kHeadDim + hi * 16;
+    const v4i qa0 = ld16(qrow), qa1 = ld16(qrow + 32);
+    if (tid < 32) scl[tid] = (float)((p.q_scale[r0 + min(tid, nr - 1)] * (double)sk) * p.attn_scale);
+    for (int e = tid; e < 32 * 64; e += 256) accs[e] = 0;
+    __syncthreads();
+    float rs[16];
+    int rpos[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int r = 8 * (i >> 2) + 4 * hi + (i & 3);
+        rs[i] = scl[r];
+        rpos[i] = pos_first + r;
+    }
+    auto scores = [&](int kt) {
+        const int t = kt * 32 + col;
+        const int8_t* kb = kp + (int64_t)(t >> 6) * 4096 + hi * 1024 + (t & 63) * 16;
+        const v4i k0 = ld16(kb), k1 = ld16(kb + 2048);
+        v16i acc = {};
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa0, k0, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa1, k1, acc, 0, 0, 0);
+        return acc;
+    };
+
+    // pass A: row maxima
+    float mx[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) mx[i] = -INFINITY;
+    for (int b = wave; b < nblk; b += 4) {
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+            const int kt = 2 * b + half, t = kt * 32 + col;
+            const v16i S = scores(kt);
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                if (t <= rpos[i]) mx[i] = fmaxf(mx[i], (float)S[i] * rs[i]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        float v = mx[i];
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+        if (col == 0) wmax[wave][8 * (i >> 2) + 4 * hi + (i & 3)] = v;
+    }
+    __syncthreads();
+    if (tid < 32) mrow[tid] = fmaxf(fmaxf(wmax[0][tid], wmax[1][tid]), fmaxf(wmax[2][tid], wmax[3][tid]));
+    __syncthreads();
+    float m[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) m[i] = mrow[8 * (i >> 2) + 4 * hi + (i & 3)];
+
+    // pass B: block sums
+    for (int b = wave; b < nblk; b += 4) {
+        const v16i S0 = scores(2 * b), S1 = scores(2 * b + 1);
+        const int t0 = 64 * b + col, t1 = t0 + 32;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float e0 = t0 <= rpos[i] ? tl_expf((float)S0[i] * rs[i] - m[i]) : 0.0f;
+            const float e1 = t1 <= rpos[i] ? tl_expf((float)S1[i] * rs[i] - m[i]) : 0.0f;
+            float v = e0 + e1;
+#pragma unroll
+            for (int off = 16; off >= 1; off >>= 1) v = v + __shfl_xor(v, off);
+            if (col == 0) bsum[(8 * (i >> 2) + 4 * hi + (i & 3)) * nblk + b] = v;
+        }
+    }
+    __syncthreads();
+    if (tid < 32) {
+        float total = 0.0f;
+        for (int b = 0; b < nblk; b++) total = total + bsum[tid * nblk + b];
+        tot[tid] = total;
+    }
+    __syncthreads();
+
+    // pass C: INT8 probabilities (zero past each row's last key)
+    for (int b = wave; b < nblk; b += 4) {
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+            const int kt = 2 * b + half, t = kt * 32 + col;
+            const v16i S = scores(kt);
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int r = 8 * (i >> 2) + 4 * hi + (i & 3);
+                int8_t pq = 0;
+                if (t <= rpos[i]) {
+                    const float e = tl_expf((float)S[i] * rs[i] - m[i]);
+                    float pr = __builtin_rintf(__fdiv_rn(e, tot[r]) * 127.0f);
+                    pr = pr < 0.0f ? 0.0f : (pr > 127.0f ? 127.0f : pr);
+                    pq = (int8_t)(int)pr;
+                }
+                p8[r * tpad + t] = pq;
+            }
+        }
+    }
+    __syncthreads();
+
+    // pass D: O = P8 . V
+    v16i o0 = {}, o1 = {};
+    for (int kc = wave; kc < tpad / 32; kc += 4) {
+        const v4i a = *(const v4i*)(p8 + col * tpad + kc * 32 + hi * 16);
+        const int8_t* vb = vp + (int64_t)(kc * 2 + hi) * 1024 + col * 16;
+        const v4i b0 = ld16(vb), b1 = ld16(vb + 512);
+        o0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b0, o0, 0, 0, 0);
+        o1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b1, o1, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int r = 8 * (i >> 2) + 4 * hi + (i & 3);
+        atomicAdd(&accs[r * 64 + col], o0[i]);
+        atomicAdd(&accs[r * 64 + 32 + col], o1[i]);
+    }
+    __syncthreads();
+    const float pv_mult = deq_mult(1.0 / 127.0, sv);
+    for (int e = tid; e < 32 * 64; e += 256) {
+        const int r = e >> 6, d = e & 63;
+        if (r < nr) p.out[(int64_t)(r0 + r) * D + (int64_t)h * kHeadDim + d] = (float)accs[e] * pv_mult;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // standalone element-wise ops (operator surface of TL)
 // ---------------------------------------------------------------------------
@@ -933,6 +1104,29 @@ hipError_t launch_qkv_post(hipStream_t s, const float* qkv, int32_t rows, int32_
     const size_t lds = sizeof(float) * ((size_t)(D + 2 * KVD) + D + KVD);
     TL_KLAUNCH(qkv_post_kernel, dim3(rows), dim3(256), lds, s, qkv, n_heads, n_kv_heads, rm,
                        cos, sin, kv, layer, kv_sk, kv_sv, q8, q_scale, q_rot_out);
+    return hipGetLastError();
+}
+
+// INT8 probabilities of 32 rows x tpad keys, block sums, partial sums
+static size_t tile_lds_bytes(int tpad) { return (size_t)32 * tpad + (size_t)32 * (tpad / 64) * sizeof(float) + 32 * 64 * sizeof(int); }
+
+hipError_t init_prefill_kernels() {
+    return hipFuncSetAttribute((const void*)attention_tile_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)tile_lds_bytes(kTileMaxKeys));
+}
+
+// rows of one sequence at positions pos0 .. pos0 + rows - 1
+hipError_t launch_attention_tiles(hipStream_t s, const int8_t* q8, const double* q_scale, int32_t rows,
+                                  int32_t n_heads, int32_t n_kv_heads, int32_t seq, int32_t pos0, KvGeom kv,
+                                  int32_t layer, const float* kv_sk, const float* kv_sv, float* out) {
+    if (rows <= 0) return hipSuccess;
+    if (n_heads % n_kv_heads || pos0 < 0 || pos0 + rows > kv.max_pos || pos0 + rows > kTileMaxKeys)
+        return hipErrorInvalidValue;
+    const int tpad = (pos0 + rows + 63) & ~63;
+    const size_t lds = tile_lds_bytes(tpad);
+    AttnTileArgs a{q8, q_scale, n_heads, n_kv_heads, rows, seq, pos0, layer, kv, kv_sk, kv_sv,
+                   1.0 / sqrt((double)kHeadDim), out};
+    TL_KLAUNCH(attention_tile_kernel, dim3(n_heads, (rows + 31) / 32), dim3(256), lds, s, a);
     return hipGetLastError();
 }
 

@@ -107,6 +107,9 @@ struct tl_handle {
 
     // persistent decode (tl_persist.hip)
     bool use_persist = false;             // TL_PERSIST=1 turns on the single-kernel decode
+    int batch_hpw = 1;                    // query heads per workgroup of multi-row decode attention (TL_BATCH_HPW)
+    bool rows_one_seq = false;            // the uploaded rows are one sequence at rows_pos0 + r
+    int32_t rows_seq = 0, rows_pos0 = 0;
     bool persist_ok = false;              // geometry and occupancy allow it
     int32_t persist_grid = 0;             // one workgroup per CU
     size_t persist_lds = 0;
@@ -333,6 +336,18 @@ int32_t linear(tl_handle* h, int epi, int rows, const int8_t* x8, const double* 
 
 RowMap rowmap(tl_handle* h) { return RowMap{h->row_seq, h->row_pos}; }
 
+// causal attention of the uploaded rows: MFMA tiles when the rows are one
+// sequence (prefill), else one workgroup per (row, KV head)
+hipError_t rows_attention(tl_handle* h, const int8_t* q8, const double* q_scale, int32_t rows, int32_t layer,
+                          float* out, int32_t max_t) {
+    const tl_config& c = h->cfg;
+    if (h->rows_one_seq && h->rows_pos0 + rows <= kTileMaxKeys)
+        return launch_attention_tiles(h->stream, q8, q_scale, rows, c.n_heads, c.n_kv_heads, h->rows_seq, h->rows_pos0,
+                                      h->kv, layer, h->kv_sk, h->kv_sv, out);
+    return launch_attention(h->stream, q8, q_scale, rows, c.n_heads, c.n_kv_heads, rowmap(h), h->kv, layer, h->kv_sk,
+                            h->kv_sv, out, max_t);
+}
+
 GemvArgs gemv_args(const tl_handle* h) {
     GemvArgs g{};
     g.eps = h->cfg.rms_eps;
@@ -402,7 +417,7 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
         Prof p(h, TL_K_ATTN, (double)rows * c.n_kv_heads * (double)max_t * 128.0 + rows * QKV * 4.0);
         TL_LAUNCH(h, launch_attention_decode(h->stream, h->qkv, rows, c.n_heads, c.n_kv_heads, rowmap(h), h->rope_cos,
                                              h->rope_sin, h->kv, layer, h->kv_sk, h->kv_sv, h->att, max_t,
-                                             G == 8 ? 8 : 1));
+                                             G == 8 && h->batch_hpw == 8 ? 8 : 1));
     } else {
         {
             Prof p(h, TL_K_ATTN, (double)rows * (QKV * 4.0 + D) + (double)rows * KVD * 2.0);
@@ -410,8 +425,7 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
                                          h->rope_sin, h->kv, layer, h->kv_sk, h->kv_sv, h->q8, h->qs, nullptr));
         }
         Prof p(h, TL_K_ATTN, (double)rows * c.n_kv_heads * (double)max_t * 128.0 + rows * D * 5.0);
-        TL_LAUNCH(h, launch_attention(h->stream, h->q8, h->qs, rows, c.n_heads, c.n_kv_heads, rowmap(h), h->kv,
-                                      layer, h->kv_sk, h->kv_sv, h->att, max_t));
+        TL_LAUNCH(h, rows_attention(h, h->q8, h->qs, rows, layer, h->att, max_t));
     }
     {
         Prof p(h, TL_K_NORM, (double)rows * D * 5.0);
@@ -470,6 +484,9 @@ int32_t upload_rows(tl_handle* h, int32_t rows, int32_t seq_first, bool seq_per_
         s[i] = seq_per_row ? seq_first + i : seq_first;
         p[i] = pos0 + i;
     }
+    h->rows_one_seq = !seq_per_row;
+    h->rows_seq = seq_first;
+    h->rows_pos0 = pos0;
     TL_HIP(h, hipMemcpyAsync(h->row_seq, s.data(), rows * sizeof(int32_t), hipMemcpyHostToDevice, h->stream));
     TL_HIP(h, hipMemcpyAsync(h->row_pos, p.data(), rows * sizeof(int32_t), hipMemcpyHostToDevice, h->stream));
     // the host vectors must outlive the async copies
@@ -688,8 +705,10 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
     h->rope_n = c.max_pos;
     if ((e = init_kernels())) return bad(e);
     if ((e = init_decode_kernels())) return bad(e);
+    if ((e = init_prefill_kernels())) return bad(e);
     if (const char* env = std::getenv("TL_NO_GRAPHS")) h->use_graphs = env[0] == '0';
     if (const char* env = std::getenv("TL_PERSIST")) h->use_persist = env[0] == '1';
+    if (const char* env = std::getenv("TL_BATCH_HPW")) h->batch_hpw = std::atoi(env) == 8 ? 8 : 1;
     if (const char* env = std::getenv("TL_GEMM_CFG")) h->gemm_cfg = std::atoi(env);
     if ((e = hipStreamSynchronize(h->stream))) return bad(e);
     *out = h;
@@ -974,8 +993,7 @@ int32_t tl_attention(tl_handle* h, int32_t seq, int32_t layer, int32_t pos0, int
     if (r) return r;
     {
         Prof p(h, TL_K_ATTN, 0.0);
-        TL_LAUNCH(h, launch_attention(h->stream, q8, q_scale, rows, c.n_heads, c.n_kv_heads, rowmap(h), h->kv, layer,
-                                      h->kv_sk, h->kv_sv, out, pos0 + rows));
+        TL_LAUNCH(h, rows_attention(h, q8, q_scale, rows, layer, out, pos0 + rows));
     }
     return finish(h);
 }

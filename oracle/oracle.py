@@ -212,6 +212,18 @@ def apply_rope(v, n_heads, hd, cos_p, sin_p):
     return v
 
 
+def attention_row(cfg: dict, layer, pos, q8, q_scale, kc, vc, sk, sv):
+    """or_attention_row: GQA attention of one INT8 query row (all heads, at
+    position pos, keys 0..pos of the logical cache kc / vc) -> float32 [D]."""
+    c = OrConfig(cfg["hidden"], cfg["intermediate"], cfg["n_layers"], cfg["n_heads"], cfg["n_kv_heads"],
+                 cfg["head_dim"], cfg["vocab"], cfg["max_pos"], cfg["rms_eps"], cfg["rope_theta"])
+    att = np.empty(cfg["n_heads"] * cfg["head_dim"], np.float32)
+    lib().or_attention_row(C.byref(c), layer, pos, ptr(i8(q8), C.c_int8), float(q_scale),
+                           ptr(kc, C.c_int8), ptr(vc, C.c_int8), ptr(f32(sk), C.c_float), ptr(f32(sv), C.c_float),
+                           ptr(att, C.c_float), None, None, None)
+    return att
+
+
 def expf(x):
     return np.array([lib().or_expf(float(v)) for v in np.asarray(x, np.float32).ravel()],
                     np.float32).reshape(np.shape(x))

@@ -271,3 +271,41 @@ def test_generate_tinyllama_shape_matches_oracle(persist, monkeypatch):
             assert_bits_equal(k, kc[layer, g, :n], f"K layer {layer} head {g}")
             assert_bits_equal(v, vc[layer, g, :n], f"V layer {layer} head {g}")
     eng.close()
+
+
+# ---- causal attention of a block of rows (prefill tiles) ----------------------------
+
+@pytest.mark.parametrize("shape,pos0,rows", [
+    ("tinyllama", 0, 1), ("tinyllama", 0, 77), ("tinyllama", 130, 64), ("tinyllama", 1900, 100),
+    ("small", 5, 33), ("small", 0, 256), ("small", 96, 160)])
+def test_attention_rows_match_oracle(shape, pos0, rows):
+    """tl_attention over rows at positions pos0 .. pos0 + rows - 1 of one
+    sequence (the prefill path: INT8 MFMA tiles of 32 rows, partial last
+    tiles, tiles that start mid-context) equals the oracle's per-row GQA
+    attention over the same INT8 cache, bit for bit."""
+    base = oracle.TINYLLAMA_CFG if shape == "tinyllama" else oracle.SMALL_CFG
+    cfg = dict(base, n_layers=1, vocab=64)
+    from lpta.engine import Engine
+    eng = Engine(cfg, max_seqs=1)
+    rng = np.random.default_rng(pos0 * 1000 + rows)
+    Hkv, H = cfg["n_kv_heads"], cfg["n_heads"]
+    D = H * 64
+    sk = rng.uniform(0.01, 0.08, (1, Hkv)).astype(F32)
+    sv = rng.uniform(0.01, 0.08, (1, Hkv)).astype(F32)
+    eng.set_kv_scales(sk, sv)
+    kc = np.zeros((1, Hkv, cfg["max_pos"], 64), np.int8)
+    vc = np.zeros_like(kc)
+    n = pos0 + rows
+    for g in range(Hkv):
+        kc[0, g, :n] = rng.integers(-127, 128, (n, 64))
+        vc[0, g, :n] = rng.integers(-127, 128, (n, 64))
+        eng.kv_write(0, 0, g, 0, kc[0, g, :n], vc[0, g, :n])
+    q8 = rng.integers(-127, 128, (rows, D)).astype(np.int8)
+    qs = rng.uniform(0.005, 0.05, rows)
+    out = dev(np.zeros((rows, D), F32))
+    eng.rt.call("tl_attention", 0, 0, pos0, rows, dev(q8), dev(qs), out)
+    got = host(out)
+    for r in range(rows):
+        want = oracle.attention_row(cfg, 0, pos0 + r, q8[r], qs[r], kc, vc, sk, sv)
+        assert_bits_equal(got[r], want, f"row {r} (position {pos0 + r})")
+    eng.close()
