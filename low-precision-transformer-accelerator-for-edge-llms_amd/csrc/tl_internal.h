@@ -113,6 +113,11 @@ hipError_t launch_quantize_tensor(hipStream_t s, const float* x, int64_t n, int8
 hipError_t launch_quantize_weight_rows(hipStream_t s, const float* w, int32_t rows, int32_t n,
                                        int8_t* q, float* scales);
 hipError_t launch_gemv(hipStream_t s, int epi, const GemvArgs& a);
+constexpr int kSkinnyTiles = 4096;
+constexpr int kSkinnyMaxSlices = 8;   // K slices of the small-M GEMM (LDS holds the other 7 partial tiles)   // output tiles of 32 columns the split small-M GEMM counts
+hipError_t launch_gemm_rows32(hipStream_t s, int epi, const GemmArgs& a);
+hipError_t launch_gemm_skinny(hipStream_t s, int epi, const GemmArgs& a, int32_t slices, int32_t* part,
+                              unsigned* counters);
 hipError_t launch_gemm(hipStream_t s, int epi, const GemmArgs& a, int32_t splits);
 hipError_t launch_gemm_reduce(hipStream_t s, int epi, const GemmArgs& a, int32_t splits);
 hipError_t launch_qkv_post(hipStream_t s, const float* qkv, int32_t rows, int32_t n_heads,
@@ -144,6 +149,7 @@ hipError_t launch_argmax_rows(hipStream_t s, const float* logits, int32_t rows, 
 hipError_t init_kernels();
 hipError_t init_decode_kernels();
 hipError_t init_prefill_kernels();
+hipError_t init_skinny_kernels();
 // persistent batch-1 decode (tl_persist.hip)
 struct PLayer {
     const int8_t* wqkv;

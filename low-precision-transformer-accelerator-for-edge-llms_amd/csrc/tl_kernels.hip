@@ -417,6 +417,149 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmArgs a, int32_t sp
 }
 
 // ---------------------------------------------------------------------------
+// small-M GEMM (M <= 32: batched decode rows) on i8 MFMA with the split-K
+// reduction inside the kernel.  Workgroup (t, s) computes the 32 x 32 output
+// tile t (all M rows, columns 32 t .. 32 t + 31) over K slice s of `slices`;
+// its 4 wavefronts split the slice again and add their tiles in LDS.  With
+// more than one slice the workgroup stores its partial tile (device-coherent
+// stores), and the last of the tile's workgroups to arrive (per-tile counter)
+// adds every partial -- exact integers, any order -- runs the epilogue of
+// gemm_reduce_kernel and sets the counter back to zero for the next launch.
+// A operand: lane l holds row l % 32, 16 bytes at K offset 16 (l / 32) of a
+// 32-byte chunk; B operand: column (weight row) l % 32, same bytes.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(1))) void GlobalVoid;
+typedef __attribute__((address_space(3))) void LdsVoid;
+constexpr int kCoherentLoad = 16;   // cache policy of a device-scope coherent load (sc1)
+
+// Operands reach LDS by device-to-LDS loads in rounds of up to 8 chunks
+// (256 K bytes): one load instruction moves 4 full rows x 256 bytes, and the
+// 16-byte column s of row r is stored at slot s ^ (r & 15), so the fragment
+// reads (lane l: row l % 32, one 16-byte column) spread over the banks.
+constexpr int kSkinnyRound = 8;   // 32-byte K chunks per round
+
+TL_DEV void skinny_stage(const int8_t* base, int64_t stride, int rows_valid, int kbyte0, int K, int8_t* lds) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int row = 4 * i + (lane >> 4), slot = lane & 15;
+        const int col = slot ^ (row & 15);
+        const int8_t* src = base + (int64_t)min(row, rows_valid - 1) * stride + min(kbyte0 + col * 16, K - 16);
+        __builtin_amdgcn_global_load_lds((GlobalVoid*)src, (LdsVoid*)(lds + i * 1024), 16, 0, 0);
+    }
+}
+
+TL_DEV v4i skinny_frag(const int8_t* lds, int row, int col16) {
+    return *(const v4i*)(lds + row * 256 + ((col16 ^ (row & 15)) << 4));
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs a, int32_t slices, int32_t* __restrict__ part,
+                                                          unsigned* __restrict__ counters) {
+    constexpr int NB = EPI == EPI_GLU ? 2 : 1;
+    extern __shared__ __align__(16) int8_t skinny_lds[];   // per wavefront: A + NB weight tiles of 32 x 256 bytes
+    const int tid = threadIdx.x, lane = tid & 63, col = lane & 31, hi = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: LDS load bases go to a scalar register
+    const int tile = blockIdx.x / slices, sl = blockIdx.x % slices;
+    const int n0 = tile * 32;
+    const int kch = a.k >> 5;
+    const int per = (kch + slices * 4 - 1) / (slices * 4);
+    const int c0 = (sl * 4 + wave) * per, c1 = min(c0 + per, kch);
+    int8_t* lds_a = skinny_lds + wave * (1 + NB) * 8192;
+    v16i acc[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) acc[b] = (v16i){};
+    for (int c = c0; c < c1; c += kSkinnyRound) {
+        const int nch = min(kSkinnyRound, c1 - c);
+        skinny_stage(a.a, a.k, a.m, c * 32, a.k, lds_a);
+        skinny_stage(a.w + (int64_t)n0 * a.k, a.k, a.n - n0, c * 32, a.k, lds_a + 8192);
+        if (NB == 2) skinny_stage(a.w2 + (int64_t)n0 * a.k, a.k, a.n - n0, c * 32, a.k, lds_a + 16384);
+        __builtin_amdgcn_s_waitcnt(0);   // this wavefront's tiles are in LDS
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+        for (int j = 0; j < kSkinnyRound; j++) {
+            if (j < nch) {
+                const v4i af = skinny_frag(lds_a, col, 2 * j + hi);
+#pragma unroll
+                for (int b = 0; b < NB; b++)
+                    acc[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, skinny_frag(lds_a + 8192 * (1 + b), col, 2 * j + hi),
+                                                                   acc[b], 0, 0, 0);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");   // reads done before the next round's loads land
+    }
+    // wavefront partials -> LDS (the staging area is free once every wavefront is past its last round)
+    __syncthreads();
+    int* red = (int*)skinny_lds;   // [slices <= 8][NB][16][64]
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) red[((wave * NB + b) * 16 + i) * 64 + lane] = acc[b][i];
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int o = (b * 16 + i) * 64 + lane, w = NB * 1024;
+            acc[b][i] = red[o] + red[w + o] + red[2 * w + o] + red[3 * w + o];
+        }
+    if (slices > 1) {
+        int32_t* mine = part + ((int64_t)tile * slices + sl) * NB * 1024;
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                __hip_atomic_store(mine + b * 1024 + i * 64 + lane, acc[b][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);   // the partial tile has reached the coherence point
+        unsigned before = 0;
+        if (lane == 0) before = __hip_atomic_fetch_add(counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        before = __shfl(before, 0);
+        if ((int)before != slices - 1) return;   // not the last: the last one finishes the tile
+        // every other slice's tile straight into LDS (device-coherent loads,
+        // 1 KiB per instruction, all in flight at once), then the sums
+        for (int z = 0, q = 0; z < slices; z++) {
+            if (z == sl) continue;
+            const int32_t* other = part + ((int64_t)tile * slices + z) * NB * 1024;
+#pragma unroll
+            for (int c = 0; c < NB * 4; c++)
+                __builtin_amdgcn_global_load_lds((GlobalVoid*)(other + c * 256 + lane * 4),
+                                                 (LdsVoid*)(red + (q * NB * 4 + c) * 256), 16, 0, kCoherentLoad);
+            q++;
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        for (int q = 0; q < slices - 1; q++)
+#pragma unroll
+            for (int b = 0; b < NB; b++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) acc[b][i] += red[((q * NB + b) * 16 + i) * 64 + lane];
+        if (lane == 0) __hip_atomic_store(counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const int n = n0 + col;
+    if (n >= a.n) return;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int m = 8 * (i >> 2) + 4 * hi + (i & 3);
+        if (m >= a.m) continue;
+        const int64_t idx = (int64_t)m * a.n + n;
+        if (EPI == EPI_RAW) {
+            a.acc[idx] = acc[0][i];
+            continue;
+        }
+        const double sx = a.as[m];
+        const float v0 = (float)acc[0][i] * deq_mult(sx, a.ws[n]);
+        if (EPI == EPI_GLU) {
+            const float up = (float)acc[NB - 1][i] * deq_mult(sx, a.ws2[n]);
+            a.y[idx] = tl_silu(v0) * up;
+        } else if (EPI == EPI_DEQUANT_RES) {
+            a.y[idx] = a.residual[idx] + v0;
+        } else {
+            a.y[idx] = v0;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Q/K/V post-processing per row (GI:150-156, design_decisions A7/B2):
 // RoPE on Q and K (TL:69-80), Q quantized at the row's own scale, K (post
 // RoPE) and V quantized at the static per-layer/per-KV-head scales and
@@ -1083,6 +1226,143 @@ hipError_t launch_gemm(hipStream_t s, int epi, const GemmArgs& a, int32_t splits
     return hipGetLastError();
 }
 
+// small-M GEMM without a cross-workgroup reduction: one workgroup of 16
+// wavefronts per 32-column output tile; wavefront w multiplies the 32 A rows
+// by the tile's weight rows over its own run of consecutive 32-byte K chunks
+// (register loads, all issued before the first MFMA) and the 16 partial
+// tiles are added in LDS (exact integers) by the epilogue threads, one
+// output element each.  Used for K <= 2048; the split-K kernel covers the
+// long-K down projection with more workgroups.
+constexpr int kRowsWaves = 16;
+constexpr int kRowsChunks = 12;   // most 32-byte K chunks per wavefront (K <= 16 x 12 x 32 = 6144)
+
+template <int EPI, int CH>
+__global__ __launch_bounds__(1024) void gemm_rows32_kernel(GemmArgs a) {
+    constexpr int NB = EPI == EPI_GLU ? 2 : 1;
+    extern __shared__ __align__(16) int rows32_lds[];   // [16 waves][NB][16][64]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, col = lane & 31, hi = lane >> 5;
+    const int n0 = blockIdx.x * 32;
+    const int kch = a.k >> 5;
+    const int8_t* arow = a.a + (int64_t)min(col, a.m - 1) * a.k + hi * 16;
+    const int8_t* wrow[NB];
+    wrow[0] = a.w + (int64_t)min(n0 + col, a.n - 1) * a.k + hi * 16;
+    if (NB == 2) wrow[NB - 1] = a.w2 + (int64_t)min(n0 + col, a.n - 1) * a.k + hi * 16;
+    const int per = (kch + kRowsWaves - 1) / kRowsWaves;   // consecutive chunks of this wavefront: 4 loads cover a 128-byte line
+    v4i af[CH], bf[NB][CH];
+#pragma unroll
+    for (int j = 0; j < CH; j++) {
+        const int cc = min(wave * per + min(j, per - 1), kch - 1);
+        af[j] = ld16(arow + (int64_t)cc * 32);
+#pragma unroll
+        for (int b = 0; b < NB; b++) bf[b][j] = ld_nt16(wrow[b] + (int64_t)cc * 32);
+    }
+    v16i acc[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) acc[b] = (v16i){};
+#pragma unroll
+    for (int j = 0; j < CH; j++)
+        if (j < per && wave * per + j < kch)
+#pragma unroll
+            for (int b = 0; b < NB; b++) acc[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[j], bf[b][j], acc[b], 0, 0, 0);
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) rows32_lds[((wave * NB + b) * 16 + i) * 64 + lane] = acc[b][i];
+    __syncthreads();
+    // thread t finishes element (register i, lane l) of the 32 x 32 tile
+    const int l = tid & 63, i = tid >> 6;
+    const int m = 8 * (i >> 2) + 4 * (l >> 5) + (i & 3), n = n0 + (l & 31);
+    if (m >= a.m || n >= a.n) return;
+    int sum[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        int v = 0;
+#pragma unroll
+        for (int w = 0; w < kRowsWaves; w++) v += rows32_lds[((w * NB + b) * 16 + i) * 64 + l];
+        sum[b] = v;
+    }
+    const int64_t idx = (int64_t)m * a.n + n;
+    if (EPI == EPI_RAW) {
+        a.acc[idx] = sum[0];
+        return;
+    }
+    const double sx = a.as[m];
+    const float v0 = (float)sum[0] * deq_mult(sx, a.ws[n]);
+    if (EPI == EPI_GLU) {
+        const float up = (float)sum[NB - 1] * deq_mult(sx, a.ws2[n]);
+        a.y[idx] = tl_silu(v0) * up;
+    } else if (EPI == EPI_DEQUANT_RES) {
+        a.y[idx] = a.residual[idx] + v0;
+    } else {
+        a.y[idx] = v0;
+    }
+}
+
+static size_t rows32_lds_bytes(int nb) { return (size_t)kRowsWaves * nb * 16 * 64 * sizeof(int); }
+
+// M <= 32, K a multiple of 64 and at most 6144
+hipError_t launch_gemm_rows32(hipStream_t s, int epi, const GemmArgs& a) {
+    if (a.m < 1 || a.m > 32 || a.n <= 0 || a.k <= 0 || a.k % 64 || a.k > kRowsWaves * kRowsChunks * 32)
+        return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((a.n + 31) / 32)), block(1024);
+    const size_t lds1 = rows32_lds_bytes(1), lds2 = rows32_lds_bytes(2);
+    const bool shortk = a.k <= kRowsWaves * 4 * 32;
+#define TL_R32(E, L)                                                                        \
+    do {                                                                                    \
+        if (shortk) TL_KLAUNCH((gemm_rows32_kernel<E, 4>), grid, block, L, s, a);           \
+        else TL_KLAUNCH((gemm_rows32_kernel<E, kRowsChunks>), grid, block, L, s, a);        \
+    } while (0)
+    switch (epi) {
+        case EPI_DEQUANT: TL_R32(EPI_DEQUANT, lds1); break;
+        case EPI_DEQUANT_RES: TL_R32(EPI_DEQUANT_RES, lds1); break;
+        case EPI_GLU:
+            if (!shortk) return hipErrorInvalidValue;   // both weight sets of 12 chunks exceed the registers
+            TL_KLAUNCH((gemm_rows32_kernel<EPI_GLU, 4>), grid, block, lds2, s, a);
+            break;
+        case EPI_RAW: TL_R32(EPI_RAW, lds1); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef TL_R32
+    return hipGetLastError();
+}
+
+// staging of 4 wavefronts (A + NB weight tiles of 32 x 256 bytes); also
+// holds the wavefront partials and the other slices' tiles (8 x NB x 4 KiB)
+static size_t skinny_lds_bytes(int nb) { return (size_t)4 * (1 + nb) * 8192; }
+
+hipError_t init_skinny_kernels() {
+    hipError_t e = hipSuccess;
+    const void* fns[4] = {(const void*)gemm_skinny_kernel<EPI_DEQUANT>, (const void*)gemm_skinny_kernel<EPI_DEQUANT_RES>,
+                          (const void*)gemm_skinny_kernel<EPI_GLU>, (const void*)gemm_skinny_kernel<EPI_RAW>};
+    for (int i = 0; i < 4 && e == hipSuccess; i++)
+        e = hipFuncSetAttribute(fns[i], hipFuncAttributeMaxDynamicSharedMemorySize, (int)skinny_lds_bytes(i == 2 ? 2 : 1));
+    const void* rfns[7] = {(const void*)gemm_rows32_kernel<EPI_DEQUANT, 4>, (const void*)gemm_rows32_kernel<EPI_DEQUANT_RES, 4>,
+                           (const void*)gemm_rows32_kernel<EPI_RAW, 4>, (const void*)gemm_rows32_kernel<EPI_DEQUANT, kRowsChunks>,
+                           (const void*)gemm_rows32_kernel<EPI_DEQUANT_RES, kRowsChunks>,
+                           (const void*)gemm_rows32_kernel<EPI_RAW, kRowsChunks>, (const void*)gemm_rows32_kernel<EPI_GLU, 4>};
+    for (int i = 0; i < 7 && e == hipSuccess; i++)
+        e = hipFuncSetAttribute(rfns[i], hipFuncAttributeMaxDynamicSharedMemorySize, (int)rows32_lds_bytes(i == 6 ? 2 : 1));
+    return e;
+}
+
+// M <= 32, K a multiple of 64; `part` holds tiles x slices x NB x 1024
+// int32 when slices > 1, `counters` one zeroed word per output tile
+hipError_t launch_gemm_skinny(hipStream_t s, int epi, const GemmArgs& a, int32_t slices, int32_t* part,
+                              unsigned* counters) {
+    if (a.m < 1 || a.m > 32 || a.n <= 0 || a.k <= 0 || a.k % 64 || slices < 1 || slices > kSkinnyMaxSlices)
+        return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(((a.n + 31) / 32) * slices)), block(256);
+    const size_t lds1 = skinny_lds_bytes(1), lds2 = skinny_lds_bytes(2);
+    switch (epi) {
+        case EPI_DEQUANT: TL_KLAUNCH(gemm_skinny_kernel<EPI_DEQUANT>, grid, block, lds1, s, a, slices, part, counters); break;
+        case EPI_DEQUANT_RES: TL_KLAUNCH(gemm_skinny_kernel<EPI_DEQUANT_RES>, grid, block, lds1, s, a, slices, part, counters); break;
+        case EPI_GLU: TL_KLAUNCH(gemm_skinny_kernel<EPI_GLU>, grid, block, lds2, s, a, slices, part, counters); break;
+        case EPI_RAW: TL_KLAUNCH(gemm_skinny_kernel<EPI_RAW>, grid, block, lds1, s, a, slices, part, counters); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_gemm_reduce(hipStream_t s, int epi, const GemmArgs& a, int32_t splits) {
     const int blocks = (int)std::min<int64_t>(2048, ((int64_t)a.m * a.n + 255) / 256);
     switch (epi) {
@@ -1115,6 +1395,174 @@ hipError_t init_prefill_kernels() {
                                (int)tile_lds_bytes(kTileMaxKeys));
 }
 
+// the same computation for contexts of at most 128 NB keys per wavefront
+// (NB blocks of 64 each, i.e. tpad <= 256 NB): every K and V fragment of the
+// wavefront is requested at the start, scores and exponentials stay in
+// registers across the passes
+template <int NB>
+__global__ __launch_bounds__(256) void attention_tile_reg_kernel(AttnTileArgs p) {
+    extern __shared__ __align__(16) int8_t tile_lds[];
+    __shared__ float scl[32], mrow[32], tot[32];
+    __shared__ float wmax[4][32];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 31, hi = lane >> 5;
+    const int h = blockIdx.x, r0 = blockIdx.y * 32;
+    const int G = p.n_heads / p.n_kv, g = h / G;
+    const int nr = min(32, p.rows - r0);
+    const int pos_first = p.pos0 + r0;
+    const int T = pos_first + nr;
+    const int tpad = (T + 63) & ~63, nblk = tpad >> 6;
+    int8_t* p8 = tile_lds;                         // [32][tpad]
+    float* bsum = (float*)(tile_lds + 32 * tpad);  // [32][nblk]
+    int* accs = (int*)(bsum + 32 * nblk);          // [32][64]
+    const int D = p.n_heads * kHeadDim;
+    const int64_t pl = p.kv.plane(p.seq, p.layer, g);
+    const int8_t* kp = p.kv.k + pl;
+    const int8_t* vp = p.kv.v + pl;
+    const float sk = p.kv_sk[p.layer * p.n_kv + g], sv = p.kv_sv[p.layer * p.n_kv + g];
+
+    // every load first: Q, then K of this wavefront's blocks b = wave + 4 j
+    // (two 32-key tiles each), then V of its 32-key chunks c = wave + 4 j
+    // (block indices clamped inside the plane; surplus copies unused)
+    const int8_t* qrow = p.q8 + (int64_t)(r0 + min(col, nr - 1)) * D + h * kHeadDim + hi * 16;
+    const v4i qa0 = ld16(qrow), qa1 = ld16(qrow + 32);
+    v4i kf[NB][2][2], vf[2 * NB][2];
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+            const int t = min(64 * (wave + 4 * j), tpad - 64) + 32 * half + col;
+            const int8_t* kb = kp + (int64_t)(t >> 6) * 4096 + hi * 1024 + (t & 63) * 16;
+            kf[j][half][0] = ld16(kb);
+            kf[j][half][1] = ld16(kb + 2048);
+        }
+#pragma unroll
+    for (int j = 0; j < 2 * NB; j++) {
+        const int kc = min(wave + 4 * j, tpad / 32 - 1);
+        const int8_t* vb = vp + (int64_t)(kc * 2 + hi) * 1024 + col * 16;
+        vf[j][0] = ld16(vb);
+        vf[j][1] = ld16(vb + 512);
+    }
+    if (tid < 32) scl[tid] = (float)((p.q_scale[r0 + min(tid, nr - 1)] * (double)sk) * p.attn_scale);
+    for (int e = tid; e < 32 * 64; e += 256) accs[e] = 0;
+    __syncthreads();
+    float rs[16];
+    int rpos[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int r = 8 * (i >> 2) + 4 * hi + (i & 3);
+        rs[i] = scl[r];
+        rpos[i] = pos_first + r;
+    }
+
+    // pass A: scores (kept) and row maxima
+    float sc[NB][2][16];
+    float mx[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) mx[i] = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+            v16i acc = {};
+            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa0, kf[j][half][0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa1, kf[j][half][1], acc, 0, 0, 0);
+            const int t = 64 * (wave + 4 * j) + 32 * half + col;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const float v = (float)acc[i] * rs[i];
+                const bool live = wave + 4 * j < nblk && t <= rpos[i];
+                sc[j][half][i] = v;
+                if (live) mx[i] = fmaxf(mx[i], v);
+            }
+        }
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        float v = mx[i];
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+        if (col == 0) wmax[wave][8 * (i >> 2) + 4 * hi + (i & 3)] = v;
+    }
+    __syncthreads();
+    if (tid < 32) mrow[tid] = fmaxf(fmaxf(wmax[0][tid], wmax[1][tid]), fmaxf(wmax[2][tid], wmax[3][tid]));
+    __syncthreads();
+
+    // pass B: exponentials (kept) and block sums
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+        const int b = wave + 4 * j;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int r = 8 * (i >> 2) + 4 * hi + (i & 3);
+            const float m = mrow[r];
+            const int t0 = 64 * b + col;
+            const float e0 = t0 <= rpos[i] ? tl_expf(sc[j][0][i] - m) : 0.0f;
+            const float e1 = t0 + 32 <= rpos[i] ? tl_expf(sc[j][1][i] - m) : 0.0f;
+            sc[j][0][i] = e0;
+            sc[j][1][i] = e1;
+            float v = e0 + e1;
+#pragma unroll
+            for (int off = 16; off >= 1; off >>= 1) v = v + __shfl_xor(v, off);
+            if (col == 0 && b < nblk) bsum[r * nblk + b] = v;
+        }
+    }
+    __syncthreads();
+    if (tid < 32) {
+        float total = 0.0f;
+        for (int b = 0; b < nblk; b++) total = total + bsum[tid * nblk + b];
+        tot[tid] = total;
+    }
+    __syncthreads();
+
+    // pass C: INT8 probabilities
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+        const int b = wave + 4 * j;
+        if (b < nblk) {
+#pragma unroll
+            for (int half = 0; half < 2; half++) {
+                const int t = 64 * b + 32 * half + col;
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int r = 8 * (i >> 2) + 4 * hi + (i & 3);
+                    int8_t pq = 0;
+                    if (t <= rpos[i]) {
+                        float pr = __builtin_rintf(__fdiv_rn(sc[j][half][i], tot[r]) * 127.0f);
+                        pr = pr < 0.0f ? 0.0f : (pr > 127.0f ? 127.0f : pr);
+                        pq = (int8_t)(int)pr;
+                    }
+                    p8[r * tpad + t] = pq;
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // pass D: O = P8 . V
+    v16i o0 = {}, o1 = {};
+#pragma unroll
+    for (int j = 0; j < 2 * NB; j++) {
+        const int kc = wave + 4 * j;
+        if (kc < tpad / 32) {
+            const v4i a = *(const v4i*)(p8 + col * tpad + kc * 32 + hi * 16);
+            o0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, vf[j][0], o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, vf[j][1], o1, 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int r = 8 * (i >> 2) + 4 * hi + (i & 3);
+        atomicAdd(&accs[r * 64 + col], o0[i]);
+        atomicAdd(&accs[r * 64 + 32 + col], o1[i]);
+    }
+    __syncthreads();
+    const float pv_mult = deq_mult(1.0 / 127.0, sv);
+    for (int e = tid; e < 32 * 64; e += 256) {
+        const int r = e >> 6, d = e & 63;
+        if (r < nr) p.out[(int64_t)(r0 + r) * D + (int64_t)h * kHeadDim + d] = (float)accs[e] * pv_mult;
+    }
+}
+
 // rows of one sequence at positions pos0 .. pos0 + rows - 1
 hipError_t launch_attention_tiles(hipStream_t s, const int8_t* q8, const double* q_scale, int32_t rows,
                                   int32_t n_heads, int32_t n_kv_heads, int32_t seq, int32_t pos0, KvGeom kv,
@@ -1126,7 +1574,10 @@ hipError_t launch_attention_tiles(hipStream_t s, const int8_t* q8, const double*
     const size_t lds = tile_lds_bytes(tpad);
     AttnTileArgs a{q8, q_scale, n_heads, n_kv_heads, rows, seq, pos0, layer, kv, kv_sk, kv_sv,
                    1.0 / sqrt((double)kHeadDim), out};
-    TL_KLAUNCH(attention_tile_kernel, dim3(n_heads, (rows + 31) / 32), dim3(256), lds, s, a);
+    const dim3 grid(n_heads, (rows + 31) / 32), block(256);
+    if (tpad <= 256) TL_KLAUNCH(attention_tile_reg_kernel<1>, grid, block, lds, s, a);
+    else if (tpad <= 512) TL_KLAUNCH(attention_tile_reg_kernel<2>, grid, block, lds, s, a);
+    else TL_KLAUNCH(attention_tile_kernel, grid, block, lds, s, a);
     return hipGetLastError();
 }
 

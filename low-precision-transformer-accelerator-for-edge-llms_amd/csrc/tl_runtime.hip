@@ -88,6 +88,7 @@ struct tl_handle {
     float* fscratch = nullptr;    // small scratch
     unsigned long long* op_key = nullptr;  // argmax slot of the standalone LM-head operator
     int32_t* partials = nullptr;
+    unsigned* tile_ctr = nullptr;         // [kSkinnyTiles] arrival counters of the small-M GEMM, zero between launches
     size_t partial_cap = 0;       // int32 elements
 
     // per-sequence generation state
@@ -108,6 +109,7 @@ struct tl_handle {
     // persistent decode (tl_persist.hip)
     bool use_persist = false;             // TL_PERSIST=1 turns on the single-kernel decode
     int batch_hpw = 1;                    // query heads per workgroup of multi-row decode attention (TL_BATCH_HPW)
+    int gemm_small = 0;                   // M <= 32 GEMM: 0 one workgroup per tile, 1 split K, 2 16x16x64 tiles (TL_GEMM_SMALL)
     bool rows_one_seq = false;            // the uploaded rows are one sequence at rows_pos0 + r
     int32_t rows_seq = 0, rows_pos0 = 0;
     bool persist_ok = false;              // geometry and occupancy allow it
@@ -296,7 +298,24 @@ int32_t run_gemm(tl_handle* h, int epi, GemmArgs a, int kclass) {
         TL_LAUNCH(h, launch_gemm32(h->stream, epi, a, 1, cfg));
         return TL_OK;
     }
-    // small M (batched decode): 16x16x64 tiles, split K until the output tiles
+    if (a.m <= 32 && a.k % 64 == 0 && a.k <= 6144 && h->gemm_small != 2) {
+        // batched decode: one 32-row MFMA tile per 32 output columns, K split
+        // over enough workgroups to cover the chip, reduced in the kernel
+        const int tiles = (a.n + 31) / 32, kch = a.k / 32;
+        int slices = 1;
+        while (tiles * slices < 256 && kch / (4 * slices * 2) >= 2 && slices < kSkinnyMaxSlices) slices *= 2;
+        if (tiles > kSkinnyTiles) slices = 1;
+        if (slices > 1) {
+            int32_t r = ensure_partials(h, (size_t)tiles * slices * nb * 1024);
+            if (r) return r;
+        }
+        Prof p(h, kclass, bytes);
+        if (h->gemm_small == 1 || a.k > 2048)
+            TL_LAUNCH(h, launch_gemm_skinny(h->stream, epi, a, slices, h->partials, h->tile_ctr));
+        else TL_LAUNCH(h, launch_gemm_rows32(h->stream, epi, a));
+        return TL_OK;
+    }
+    // small M (33..63 rows): 16x16x64 tiles, split K until the output tiles
     // plus K splits cover the chip
     const int bm = a.m <= 32 ? 32 : 64;
     const int64_t tiles = (int64_t)((a.m + bm - 1) / bm) * ((a.n + 63) / 64);
@@ -655,7 +674,7 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
         (e = dalloc(h, &h->a8, (size_t)R * KF)) || (e = dalloc(h, &h->as, (size_t)R)) ||
         (e = dalloc(h, &h->q8, (size_t)R * D)) || (e = dalloc(h, &h->qs, (size_t)R)) ||
         (e = dalloc(h, &h->att, (size_t)R * D)) || (e = dalloc(h, &h->hid, (size_t)R * F)) ||
-        (e = dalloc(h, &h->logits, (size_t)max_seqs * c.vocab)) || (e = dalloc(h, &h->row_seq, (size_t)R)) ||
+        (e = dalloc(h, &h->logits, (size_t)max_seqs * c.vocab)) || (e = dalloc(h, &h->row_seq, (size_t)R)) || (e = dalloc(h, &h->tile_ctr, (size_t)kSkinnyTiles)) ||
         (e = dalloc(h, &h->row_pos, (size_t)R)) || (e = dalloc(h, &h->tokens, (size_t)R)) ||
         (e = dalloc(h, &h->fscratch, 64)) || (e = dalloc(h, &h->op_key, 1)) || (e = dalloc(h, &h->keys, (size_t)max_seqs)) ||
         (e = dalloc(h, &h->token_cur, (size_t)max_seqs)) || (e = dalloc(h, &h->cursor, (size_t)max_seqs)) ||
@@ -695,7 +714,8 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
     if ((e = hipMemsetAsync(h->kv.k, 0, kv_bytes, h->stream)) || (e = hipMemsetAsync(h->kv.v, 0, kv_bytes, h->stream)) ||
         (e = hipMemsetAsync(h->keys, 0, sizeof(unsigned long long) * max_seqs, h->stream)) ||
         (e = hipMemsetAsync(h->cursor, 0, sizeof(int32_t) * max_seqs, h->stream)) ||
-        (e = hipMemsetAsync(h->n_gen, 0, sizeof(int32_t) * max_seqs, h->stream)))
+        (e = hipMemsetAsync(h->n_gen, 0, sizeof(int32_t) * max_seqs, h->stream)) ||
+        (e = hipMemsetAsync(h->tile_ctr, 0, sizeof(unsigned) * kSkinnyTiles, h->stream)))
         return bad(e);
     std::vector<float> cs, sn;
     default_rope(c.max_pos, c.rope_theta, cs, sn);
@@ -706,9 +726,11 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
     if ((e = init_kernels())) return bad(e);
     if ((e = init_decode_kernels())) return bad(e);
     if ((e = init_prefill_kernels())) return bad(e);
+    if ((e = init_skinny_kernels())) return bad(e);
     if (const char* env = std::getenv("TL_NO_GRAPHS")) h->use_graphs = env[0] == '0';
     if (const char* env = std::getenv("TL_PERSIST")) h->use_persist = env[0] == '1';
     if (const char* env = std::getenv("TL_BATCH_HPW")) h->batch_hpw = std::atoi(env) == 8 ? 8 : 1;
+    if (const char* env = std::getenv("TL_GEMM_SMALL")) h->gemm_small = std::atoi(env);
     if (const char* env = std::getenv("TL_GEMM_CFG")) h->gemm_cfg = std::atoi(env);
     if ((e = hipStreamSynchronize(h->stream))) return bad(e);
     *out = h;

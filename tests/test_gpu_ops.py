@@ -55,7 +55,7 @@ def test_gemv_rejects_bad_k(rt):
 
 # ---- MFMA GEMM ---------------------------------------------------------------------
 
-@pytest.mark.parametrize("m,n,k", [(2, 64, 64), (5, 128, 2048), (32, 2048, 2048), (33, 256, 5632),
+@pytest.mark.parametrize("m,n,k", [(2, 64, 64), (5, 128, 2048), (32, 2048, 2048), (20, 160, 5632), (33, 256, 5632),
                                    (64, 192, 128), (130, 320, 1024), (512, 2560, 2048), (7, 32000, 64)])
 def test_gemm_i8_exact(rt, m, n, k):
     rng = np.random.default_rng(m * 1000 + n + k)
