@@ -44,6 +44,30 @@ TL_DEV float tl_expf(float x) {
     return p * __int_as_float((k + 127) << 23);
 }
 
+// tl_expf without branches, the same value for every input: the argument is
+// clamped to [-80, 80] before the reduction and the result is 0 below -80
+// (and for NaN), as in tl_expf
+TL_DEV float tl_expf_sel(float x) {
+    const float xc = fminf(fmaxf(x, -80.0f), 80.0f);
+    const float log2e = 0x1.715476p+0f;
+    const float c1 = 0x1.63p-1f;
+    const float c2 = -0x1.bd0106p-13f;
+    float kf = __builtin_rintf(xc * log2e);
+    float r = __builtin_fmaf(-kf, c1, xc);
+    r = __builtin_fmaf(-kf, c2, r);
+    float p = 0x1.a01a02p-13f;
+    p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+    p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const int k = (int)kf;
+    const float e = p * __int_as_float((k + 127) << 23);
+    return x >= -80.0f ? e : 0.0f;
+}
+
 // SiLU, TL:159-161: x / (1 + exp(-clip(x, -60, 60)))
 TL_DEV float tl_silu(float x) {
     float c = x < -60.0f ? -60.0f : (x > 60.0f ? 60.0f : x);

@@ -797,7 +797,7 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(AttnTileArgs p) {
     __shared__ float wmax[4][32];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, hi = lane >> 5;
-    const int h = blockIdx.x, r0 = blockIdx.y * 32;
+    const int h = blockIdx.x, r0 = (gridDim.y - 1 - blockIdx.y) * 32;   // the longest (last) tiles dispatch first
     const int G = p.n_heads / p.n_kv, g = h / G;
     const int nr = min(32, p.rows - r0);
     const int pos_first = p.pos0 + r0;
@@ -1396,17 +1396,23 @@ hipError_t init_prefill_kernels() {
 }
 
 // the same computation for contexts of at most 128 NB keys per wavefront
-// (NB blocks of 64 each, i.e. tpad <= 256 NB): every K and V fragment of the
-// wavefront is requested at the start, scores and exponentials stay in
-// registers across the passes
+// (NB blocks of 64 each, i.e. tpad <= 256 NB), in the transposed layout
+// S^T = K Q^T: lane l owns query row l % 32 and register i key
+// 8 (i / 4) + 4 (l / 32) + i % 4 of a 32-key tile.  A row's maximum is then
+// an in-lane maximum and one exchange with lane l ^ 32; of the block-64
+// butterfly (token distances 32, 16, 8, 4, 2, 1) only distance 4 (lane
+// l ^ 32) crosses lanes, the others add registers of one lane; four
+// probabilities of a lane are consecutive keys and leave as one 32-bit LDS
+// store.  Every K and V fragment of the wavefront is requested at the start;
+// scores and exponentials stay in registers across the passes.
 template <int NB>
 __global__ __launch_bounds__(256) void attention_tile_reg_kernel(AttnTileArgs p) {
     extern __shared__ __align__(16) int8_t tile_lds[];
-    __shared__ float scl[32], mrow[32], tot[32];
+    __shared__ float scl[32], tot[32];
     __shared__ float wmax[4][32];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, hi = lane >> 5;
-    const int h = blockIdx.x, r0 = blockIdx.y * 32;
+    const int h = blockIdx.x, r0 = (gridDim.y - 1 - blockIdx.y) * 32;   // the longest (last) tiles dispatch first
     const int G = p.n_heads / p.n_kv, g = h / G;
     const int nr = min(32, p.rows - r0);
     const int pos_first = p.pos0 + r0;
@@ -1446,65 +1452,60 @@ __global__ __launch_bounds__(256) void attention_tile_reg_kernel(AttnTileArgs p)
     if (tid < 32) scl[tid] = (float)((p.q_scale[r0 + min(tid, nr - 1)] * (double)sk) * p.attn_scale);
     for (int e = tid; e < 32 * 64; e += 256) accs[e] = 0;
     __syncthreads();
-    float rs[16];
-    int rpos[16];
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const int r = 8 * (i >> 2) + 4 * hi + (i & 3);
-        rs[i] = scl[r];
-        rpos[i] = pos_first + r;
-    }
+    const float rs = scl[col];
+    const int rpos = pos_first + col;
 
-    // pass A: scores (kept) and row maxima
+    // pass A: scores (kept) and the row maximum
     float sc[NB][2][16];
-    float mx[16];
-#pragma unroll
-    for (int i = 0; i < 16; i++) mx[i] = -INFINITY;
+    float mx = -INFINITY;
 #pragma unroll
     for (int j = 0; j < NB; j++)
 #pragma unroll
         for (int half = 0; half < 2; half++) {
             v16i acc = {};
-            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa0, kf[j][half][0], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(qa1, kf[j][half][1], acc, 0, 0, 0);
-            const int t = 64 * (wave + 4 * j) + 32 * half + col;
+            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[j][half][0], qa0, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[j][half][1], qa1, acc, 0, 0, 0);
+            const int t0 = 64 * (wave + 4 * j) + 32 * half + 4 * hi;
+            const bool blk = wave + 4 * j < nblk;
 #pragma unroll
             for (int i = 0; i < 16; i++) {
-                const float v = (float)acc[i] * rs[i];
-                const bool live = wave + 4 * j < nblk && t <= rpos[i];
+                const float v = (float)acc[i] * rs;
                 sc[j][half][i] = v;
-                if (live) mx[i] = fmaxf(mx[i], v);
+                const int t = t0 + 8 * (i >> 2) + (i & 3);
+                mx = (blk && t <= rpos) ? fmaxf(mx, v) : mx;
             }
         }
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        float v = mx[i];
-#pragma unroll
-        for (int off = 16; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-        if (col == 0) wmax[wave][8 * (i >> 2) + 4 * hi + (i & 3)] = v;
-    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    if (hi == 0) wmax[wave][col] = mx;
     __syncthreads();
-    if (tid < 32) mrow[tid] = fmaxf(fmaxf(wmax[0][tid], wmax[1][tid]), fmaxf(wmax[2][tid], wmax[3][tid]));
-    __syncthreads();
+    const float m = fmaxf(fmaxf(wmax[0][col], wmax[1][col]), fmaxf(wmax[2][col], wmax[3][col]));
 
-    // pass B: exponentials (kept) and block sums
+    // pass B: exponentials (kept) and block sums in the butterfly order
 #pragma unroll
     for (int j = 0; j < NB; j++) {
         const int b = wave + 4 * j;
+        const int t0 = 64 * b + 4 * hi;
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int r = 8 * (i >> 2) + 4 * hi + (i & 3);
-            const float m = mrow[r];
-            const int t0 = 64 * b + col;
-            const float e0 = t0 <= rpos[i] ? tl_expf(sc[j][0][i] - m) : 0.0f;
-            const float e1 = t0 + 32 <= rpos[i] ? tl_expf(sc[j][1][i] - m) : 0.0f;
-            sc[j][0][i] = e0;
-            sc[j][1][i] = e1;
-            float v = e0 + e1;
+        for (int half = 0; half < 2; half++)
 #pragma unroll
-            for (int off = 16; off >= 1; off >>= 1) v = v + __shfl_xor(v, off);
-            if (col == 0 && b < nblk) bsum[r * nblk + b] = v;
+            for (int i = 0; i < 16; i++) {
+                const int t = t0 + 32 * half + 8 * (i >> 2) + (i & 3);
+                sc[j][half][i] = t <= rpos ? tl_expf_sel(sc[j][half][i] - m) : 0.0f;
+            }
+        float a[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) a[i] = sc[j][0][i] + sc[j][1][i];      // distance 32
+        float c[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float b0 = a[r] + a[r + 8], b1 = a[r + 4] + a[r + 12];      // distance 16
+            c[r] = b0 + b1;                                                   // distance 8
         }
+        float d[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) d[r] = c[r] + __shfl_xor(c[r], 32);      // distance 4
+        const float f = (d[0] + d[2]) + (d[1] + d[3]);                        // distances 2, 1
+        if (hi == 0 && b < nblk) bsum[col * nblk + b] = f;
     }
     __syncthreads();
     if (tid < 32) {
@@ -1514,26 +1515,25 @@ __global__ __launch_bounds__(256) void attention_tile_reg_kernel(AttnTileArgs p)
     }
     __syncthreads();
 
-    // pass C: INT8 probabilities
+    // pass C: INT8 probabilities, four consecutive keys per 32-bit store
+    const float tr = tot[col];
 #pragma unroll
     for (int j = 0; j < NB; j++) {
         const int b = wave + 4 * j;
         if (b < nblk) {
 #pragma unroll
-            for (int half = 0; half < 2; half++) {
-                const int t = 64 * b + 32 * half + col;
+            for (int half = 0; half < 2; half++)
 #pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const int r = 8 * (i >> 2) + 4 * hi + (i & 3);
-                    int8_t pq = 0;
-                    if (t <= rpos[i]) {
-                        float pr = __builtin_rintf(__fdiv_rn(sc[j][half][i], tot[r]) * 127.0f);
+                for (int q = 0; q < 4; q++) {
+                    unsigned word = 0;
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        float pr = __builtin_rintf(__fdiv_rn(sc[j][half][4 * q + r], tr) * 127.0f);
                         pr = pr < 0.0f ? 0.0f : (pr > 127.0f ? 127.0f : pr);
-                        pq = (int8_t)(int)pr;
+                        word |= (unsigned)(uint8_t)(int)pr << (8 * r);
                     }
-                    p8[r * tpad + t] = pq;
+                    *(unsigned*)(p8 + col * tpad + 64 * b + 32 * half + 8 * q + 4 * hi) = word;
                 }
-            }
         }
     }
     __syncthreads();
