@@ -659,12 +659,14 @@ hipError_t launch_gemv_fused(hipStream_t s, int pro, int epi, const GemvArgs& a)
     if (pro == PRO_RMSNORM && (a.plan.n_leaves > 64 || a.plan.leaf_len * a.plan.n_leaves != a.k)) return hipErrorInvalidValue;
     const int kch = cdiv(a.k, 1024);
 #define TL_GO(P, E, R) return gemv_fused_r<P, E, R>(s, a)
+    // rows per wavefront measured fastest (graph replay over rotating weights) for the
+    // TinyLlama shapes: Q|K|V 3, gate/up 3, LM head 12, O 2, down 2
     if (pro == PRO_RMSNORM) {
-        if (epi == EPI_DEQUANT) { if (kch <= 2) TL_GO(PRO_RMSNORM, EPI_DEQUANT, 2); TL_GO(PRO_RMSNORM, EPI_DEQUANT, 1); }
+        if (epi == EPI_DEQUANT) { if (kch <= 2) TL_GO(PRO_RMSNORM, EPI_DEQUANT, 3); TL_GO(PRO_RMSNORM, EPI_DEQUANT, 1); }
         if (epi == EPI_GLU) { if (kch <= 2) TL_GO(PRO_RMSNORM, EPI_GLU, 3); TL_GO(PRO_RMSNORM, EPI_GLU, 1); }
-        if (epi == EPI_ARGMAX) { if (kch <= 2) TL_GO(PRO_RMSNORM, EPI_ARGMAX, 8); TL_GO(PRO_RMSNORM, EPI_ARGMAX, 2); }
+        if (epi == EPI_ARGMAX) { if (kch <= 2) TL_GO(PRO_RMSNORM, EPI_ARGMAX, 12); TL_GO(PRO_RMSNORM, EPI_ARGMAX, 2); }
     } else if (pro == PRO_QUANT) {
-        if (epi == EPI_DEQUANT_RES) { if (kch <= 2) TL_GO(PRO_QUANT, EPI_DEQUANT_RES, 2); TL_GO(PRO_QUANT, EPI_DEQUANT_RES, 1); }
+        if (epi == EPI_DEQUANT_RES) TL_GO(PRO_QUANT, EPI_DEQUANT_RES, 2);
         if (epi == EPI_DEQUANT) { if (kch <= 2) TL_GO(PRO_QUANT, EPI_DEQUANT, 2); TL_GO(PRO_QUANT, EPI_DEQUANT, 1); }
     }
 #undef TL_GO
