@@ -189,6 +189,52 @@ int32_t tl_generate(tl_handle *h, int32_t seq, const int32_t *prompt, int32_t n_
 int32_t tl_decode_batch(tl_handle *h, int32_t n_seqs, const int32_t *tokens, const int32_t *start_pos,
                         int32_t n_steps, int32_t *tokens_out);
 
+/* ---- debug capture -------------------------------------------------------------- */
+
+/* Tensors of one decode step, captured for one decoder layer (the capture
+ * list of docs/design_decisions.txt:366-392, B8; the per-layer debug dict of
+ * GI:136-181 and GI:313-327 for one token).  All array pointers are host
+ * memory and may be NULL (not captured).  D = hidden, KVD = n_kv_heads * 64,
+ * Hq = n_heads, W = n_keys. */
+#define TL_CAPTURE_TOPK 16
+typedef struct tl_capture {
+    /* in */
+    int32_t layer;         /* decoder layer whose tensors are captured */
+    int32_t key0;          /* attention window: keys key0 .. key0 + n_keys - 1 */
+    int32_t n_keys;        /* key0 + n_keys <= pos + 1; < 0: through pos (set on return) */
+    /* out: scalars */
+    int32_t pos;           /* position of the step's input token */
+    int32_t token_in;      /* token consumed by the step */
+    int32_t token;         /* chosen token id (greedy argmax, lower id wins ties) */
+    float   logit;         /* its logit */
+    double  attn_in_scale; /* scale of the INT8 attention input (RMSNorm output) */
+    double  q_scale;       /* scale of the INT8 query row */
+    /* out: arrays */
+    float   *layer_in;     /* [D]   residual stream entering the layer */
+    int8_t  *attn_in_q;    /* [D]   RMSNorm output quantized for Q/K/V */
+    float   *qkv;          /* [D + 2 KVD] Q|K|V projections, dequantized, before RoPE */
+    int8_t  *q8;           /* [D]   quantized query after RoPE */
+    int8_t  *k_row;        /* [KVD] K cache row written at pos (post RoPE) */
+    int8_t  *v_row;        /* [KVD] V cache row written at pos */
+    float   *kv_scales;    /* [2 Hkv] static K scales then V scales of the layer */
+    float   *score_scale;  /* [Hq]  f32((s_q s_k) / sqrt(head_dim)) per query head */
+    int32_t *scores;       /* [Hq][W] INT32 Q.K scores of the window */
+    int8_t  *probs;        /* [Hq][W] INT8 probabilities (scale 1/127) of the window */
+    float   *attended;     /* [D]   attention output before the O projection */
+    float   *layer_out;    /* [D]   residual stream leaving the layer */
+    float   *final_hidden; /* [D]   residual stream after the last layer (before the final RMSNorm) */
+    int32_t *top_ids;      /* [TL_CAPTURE_TOPK] highest logits, descending (lower id first on ties) */
+    float   *top_logits;   /* [TL_CAPTURE_TOPK] */
+} tl_capture;
+/* One greedy decode step of sequence seq (exactly one step of tl_decode: the
+ * token fed is the last one predicted, the step's K/V rows are appended and
+ * its token recorded), run eagerly with the tensors of cap->layer copied out.
+ * The step's kernels are the decode path's own; the query quantization and
+ * the score/probability window are recomputed from the step's Q|K|V by the
+ * per-row prefill kernels (same arithmetic).  Debug use only: it allocates and
+ * synchronizes. */
+int32_t tl_capture_step(tl_handle *h, int32_t seq, tl_capture *cap);
+
 /* ---- profiling ---------------------------------------------------------------- */
 
 /* Kernel classes timed with HIP events on the handle's stream while profiling

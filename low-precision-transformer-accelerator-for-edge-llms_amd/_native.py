@@ -36,6 +36,22 @@ class TlConfig(C.Structure):
                    float(d["rms_eps"]), float(d["rope_theta"]))
 
 
+CAPTURE_TOPK = 16   # TL_CAPTURE_TOPK
+
+
+class TlCapture(C.Structure):
+    """struct tl_capture: one decode step's tensors of one layer."""
+    _fields_ = [
+        ("layer", C.c_int32), ("key0", C.c_int32), ("n_keys", C.c_int32),
+        ("pos", C.c_int32), ("token_in", C.c_int32), ("token", C.c_int32), ("logit", C.c_float),
+        ("attn_in_scale", C.c_double), ("q_scale", C.c_double),
+        ("layer_in", C.c_void_p), ("attn_in_q", C.c_void_p), ("qkv", C.c_void_p), ("q8", C.c_void_p),
+        ("k_row", C.c_void_p), ("v_row", C.c_void_p), ("kv_scales", C.c_void_p), ("score_scale", C.c_void_p),
+        ("scores", C.c_void_p), ("probs", C.c_void_p), ("attended", C.c_void_p), ("layer_out", C.c_void_p),
+        ("final_hidden", C.c_void_p), ("top_ids", C.c_void_p), ("top_logits", C.c_void_p),
+    ]
+
+
 class TlError(RuntimeError):
     def __init__(self, status: int, message: str):
         super().__init__(f"{message} (status {status})")
@@ -89,6 +105,7 @@ SIGNATURES = {
     "tl_decode": (_i32, [_vp, _i32, _i32, _i32, _vp, _vp, _i32p, _i32p]),
     "tl_generate": (_i32, [_vp, _i32, _vp, _i32, _i32, _i32, _vp, _vp, _i32p, _i32p]),
     "tl_decode_batch": (_i32, [_vp, _i32, _vp, _vp, _i32, _vp]),
+    "tl_capture_step": (_i32, [_vp, _i32, C.POINTER(TlCapture)]),
     "tl_set_profiling": (_i32, [_vp, _i32]),
     "tl_get_profile": (_i32, [_vp, _i32, C.POINTER(C.c_int64), _f64p, _f64p]),
 }

@@ -113,8 +113,8 @@ hipError_t launch_quantize_tensor(hipStream_t s, const float* x, int64_t n, int8
 hipError_t launch_quantize_weight_rows(hipStream_t s, const float* w, int32_t rows, int32_t n,
                                        int8_t* q, float* scales);
 hipError_t launch_gemv(hipStream_t s, int epi, const GemvArgs& a);
-constexpr int kSkinnyTiles = 4096;
-constexpr int kSkinnyMaxSlices = 8;   // K slices of the small-M GEMM (LDS holds the other 7 partial tiles)   // output tiles of 32 columns the split small-M GEMM counts
+constexpr int kSkinnyTiles = 4096;     // output tiles of 32 columns the split small-M GEMM counts
+constexpr int kSkinnyMaxSlices = 8;   // K slices of the small-M GEMM (LDS holds the other 7 partial tiles)
 hipError_t launch_gemm_rows32(hipStream_t s, int epi, const GemmArgs& a);
 hipError_t launch_gemm_skinny(hipStream_t s, int epi, const GemmArgs& a, int32_t slices, int32_t* part,
                               unsigned* counters);
@@ -123,15 +123,25 @@ hipError_t launch_gemm_reduce(hipStream_t s, int epi, const GemmArgs& a, int32_t
 hipError_t launch_qkv_post(hipStream_t s, const float* qkv, int32_t rows, int32_t n_heads,
                            int32_t n_kv_heads, RowMap rm, const float* cos, const float* sin,
                            KvGeom kv, int32_t layer, const float* kv_sk, const float* kv_sv,
-                           int8_t* q8, double* q_scale, float* q_rot_out);
+                           int8_t* q8, double* q_scale, float* q_rot_out, bool append_kv = true);
 constexpr int kTileMaxKeys = 4096;   // context limit of launch_attention_tiles (LDS)
 hipError_t launch_attention_tiles(hipStream_t s, const int8_t* q8, const double* q_scale, int32_t rows,
                                   int32_t n_heads, int32_t n_kv_heads, int32_t seq, int32_t pos0, KvGeom kv,
                                   int32_t layer, const float* kv_sk, const float* kv_sv, float* out);
+// Optional debug outputs of row 0 (the decode-step capture): INT32 scores and
+// INT8 probabilities of keys key0 .. key0 + n_keys - 1 per query head
+// ([n_heads][n_keys]) and the f32 score scale per query head.
+struct AttnDebug {
+    int32_t* scores = nullptr;
+    int8_t* probs = nullptr;
+    float* score_scale = nullptr;
+    int32_t key0 = 0;
+    int32_t n_keys = 0;
+};
 hipError_t launch_attention(hipStream_t s, const int8_t* q8, const double* q_scale, int32_t rows,
                             int32_t n_heads, int32_t n_kv_heads, RowMap rm, KvGeom kv,
                             int32_t layer, const float* kv_sk, const float* kv_sv, float* out,
-                            int32_t max_t);
+                            int32_t max_t, AttnDebug dbg = AttnDebug());
 hipError_t launch_rope(hipStream_t s, float* v, int32_t rows, int32_t n_heads, const int32_t* pos,
                        const float* cos, const float* sin);
 hipError_t launch_softmax_rows(hipStream_t s, const float* x, int32_t rows, int32_t n, float* p);

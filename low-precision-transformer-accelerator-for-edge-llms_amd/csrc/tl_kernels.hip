@@ -573,7 +573,7 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(const float* __restrict__
                                                        const float* __restrict__ kv_sv,
                                                        int8_t* __restrict__ q8,
                                                        double* __restrict__ q_scale,
-                                                       float* __restrict__ q_rot_out) {
+                                                       float* __restrict__ q_rot_out, int32_t append_kv) {
     extern __shared__ float lds[];
     __shared__ float red[16];
     const int row = blockIdx.x, tid = threadIdx.x;
@@ -602,6 +602,7 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(const float* __restrict__
         if (q_rot_out) q_rot_out[(int64_t)row * D + i] = o[i];
     }
     if (tid == 0) q_scale[row] = s;
+    if (!append_kv) return;
     for (int i = tid; i < KVD; i += blockDim.x) {
         const int g = i >> 6, d = i & 63;
         const int64_t pl = kv.plane(seq, layer, g);
@@ -626,7 +627,8 @@ __global__ __launch_bounds__(256) void attention_kernel(const int8_t* __restrict
                                                         KvGeom kv, int32_t layer,
                                                         const float* __restrict__ kv_sk,
                                                         const float* __restrict__ kv_sv,
-                                                        double attn_scale, float* __restrict__ out) {
+                                                        double attn_scale, float* __restrict__ out,
+                                                        AttnDebug dbg) {
     extern __shared__ float s_buf[];            // [G][tpad] scores then exps
     __shared__ int4 qs[kMaxGroup][4];           // q8 of the group's heads
     __shared__ float wmax[4][kMaxGroup];
@@ -649,7 +651,9 @@ __global__ __launch_bounds__(256) void attention_kernel(const int8_t* __restrict
     if (tid < G) {
         const float sk = kv_sk[layer * n_kv + g];
         scl[tid] = (float)((q_scale[row] * (double)sk) * attn_scale);
+        if (dbg.score_scale && row == 0) dbg.score_scale[g * G + tid] = scl[tid];
     }
+    const bool dbg_row = row == 0 && dbg.n_keys > 0;
     __syncthreads();
 
     const int64_t pl = kv.plane(seq, layer, g);
@@ -677,6 +681,8 @@ __global__ __launch_bounds__(256) void attention_kernel(const int8_t* __restrict
                     S = sdot4x4(k3, qs[h][3], S);
                     const float sv = (float)S * scl[h];
                     s_buf[h * tpad + t] = sv;
+                    if (dbg_row && dbg.scores && t >= dbg.key0 && t < dbg.key0 + dbg.n_keys)
+                        dbg.scores[(int64_t)(g * G + h) * dbg.n_keys + (t - dbg.key0)] = S;
                     lmax[h] = fmaxf(lmax[h], sv);
                 }
             }
@@ -731,6 +737,8 @@ __global__ __launch_bounds__(256) void attention_kernel(const int8_t* __restrict
                 pq = (int8_t)(int)pr;
             }
             p8[h * tpad + t] = pq;
+            if (dbg_row && dbg.probs && t >= dbg.key0 && t < dbg.key0 + dbg.n_keys)
+                dbg.probs[(int64_t)(g * G + h) * dbg.n_keys + (t - dbg.key0)] = pq;
         }
     }
     __syncthreads();
@@ -1378,12 +1386,12 @@ hipError_t launch_gemm_reduce(hipStream_t s, int epi, const GemmArgs& a, int32_t
 hipError_t launch_qkv_post(hipStream_t s, const float* qkv, int32_t rows, int32_t n_heads,
                            int32_t n_kv_heads, RowMap rm, const float* cos, const float* sin,
                            KvGeom kv, int32_t layer, const float* kv_sk, const float* kv_sv,
-                           int8_t* q8, double* q_scale, float* q_rot_out) {
+                           int8_t* q8, double* q_scale, float* q_rot_out, bool append_kv) {
     if (rows <= 0) return hipSuccess;
     const int D = n_heads * kHeadDim, KVD = n_kv_heads * kHeadDim;
     const size_t lds = sizeof(float) * ((size_t)(D + 2 * KVD) + D + KVD);
     TL_KLAUNCH(qkv_post_kernel, dim3(rows), dim3(256), lds, s, qkv, n_heads, n_kv_heads, rm,
-                       cos, sin, kv, layer, kv_sk, kv_sv, q8, q_scale, q_rot_out);
+                       cos, sin, kv, layer, kv_sk, kv_sv, q8, q_scale, q_rot_out, (int32_t)append_kv);
     return hipGetLastError();
 }
 
@@ -1584,7 +1592,7 @@ hipError_t launch_attention_tiles(hipStream_t s, const int8_t* q8, const double*
 hipError_t launch_attention(hipStream_t s, const int8_t* q8, const double* q_scale, int32_t rows,
                             int32_t n_heads, int32_t n_kv_heads, RowMap rm, KvGeom kv,
                             int32_t layer, const float* kv_sk, const float* kv_sv, float* out,
-                            int32_t max_t) {
+                            int32_t max_t, AttnDebug dbg) {
     if (rows <= 0) return hipSuccess;
     const int G = n_heads / n_kv_heads;
     if (G < 1 || G > kMaxGroup || n_heads % n_kv_heads) return hipErrorInvalidValue;
@@ -1592,7 +1600,7 @@ hipError_t launch_attention(hipStream_t s, const int8_t* q8, const double* q_sca
     const size_t lds = (size_t)G * tpad * sizeof(float) + (size_t)G * tpad + (size_t)G * (tpad / 64) * sizeof(float) + 16;
     const double attn_scale = 1.0 / sqrt((double)kHeadDim);
     TL_KLAUNCH(attention_kernel, dim3(n_kv_heads, rows), dim3(256), lds, s, q8, q_scale, n_heads,
-                       n_kv_heads, rm, kv, layer, kv_sk, kv_sv, attn_scale, out);
+                       n_kv_heads, rm, kv, layer, kv_sk, kv_sv, attn_scale, out, dbg);
     return hipGetLastError();
 }
 

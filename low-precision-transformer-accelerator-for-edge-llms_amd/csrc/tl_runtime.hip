@@ -1311,6 +1311,157 @@ int32_t tl_decode_batch(tl_handle* h, int32_t n_seqs, const int32_t* tokens, con
     return TL_OK;
 }
 
+// ---- debug capture -------------------------------------------------------------------
+
+}  // extern "C"
+
+namespace {
+
+// device buffers of one capture, freed after the stream has drained
+struct CaptureScratch {
+    hipStream_t stream;
+    std::vector<void*> ptrs;
+    explicit CaptureScratch(hipStream_t s) : stream(s) {}
+    ~CaptureScratch() {
+        hipStreamSynchronize(stream);
+        for (void* p : ptrs) hipFree(p);
+    }
+    template <class T>
+    T* get(size_t n) {
+        void* p = nullptr;
+        if (hipMalloc(&p, std::max<size_t>(n, 1) * sizeof(T)) != hipSuccess) return nullptr;
+        ptrs.push_back(p);
+        return (T*)p;
+    }
+};
+
+// device -> host copy on the handle's stream when the destination is wanted
+hipError_t copy_out(tl_handle* h, void* dst, const void* src, size_t bytes) {
+    if (!dst || !bytes) return hipSuccess;
+    return hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, h->stream);
+}
+
+// the capture layer's tensors once its decode kernels have run: the layer's
+// input was saved in xin; the attention input and the query are quantized
+// again, and the window's scores and probabilities are recomputed, by the
+// per-row kernels of the prefill path from the layer's Q|K|V (h->qkv)
+int32_t capture_layer(tl_handle* h, int32_t layer, int32_t pos, const float* xin, tl_capture* cap, CaptureScratch& sc) {
+    const tl_config& c = h->cfg;
+    const int D = h->D, KVD = h->KVD, Hq = c.n_heads, Hkv = c.n_kv_heads;
+    const LayerDev& L = h->layers[layer];
+    int8_t* a8 = sc.get<int8_t>(D);
+    double* as = sc.get<double>(1);
+    int8_t* kv_rows = sc.get<int8_t>(2 * (size_t)KVD);
+    const size_t win = (size_t)Hq * cap->n_keys;
+    int32_t* scores = sc.get<int32_t>(win);
+    int8_t* probs = sc.get<int8_t>(win);
+    float* scl = sc.get<float>(Hq);
+    if (!a8 || !as || !kv_rows || !scores || !probs || !scl) return fail(h, TL_ERR_INTERNAL, "hipMalloc");
+    TL_HIP(h, copy_out(h, cap->qkv, h->qkv, sizeof(float) * h->QKV));
+    TL_HIP(h, copy_out(h, cap->attended, h->att, sizeof(float) * D));
+    TL_HIP(h, copy_out(h, cap->layer_out, h->x, sizeof(float) * D));
+    TL_LAUNCH(h, launch_rmsnorm_quant(h->stream, xin, L.g_in, 1, D, c.rms_eps, h->plan, nullptr, a8, as));
+    TL_HIP(h, copy_out(h, cap->attn_in_q, a8, D));
+    TL_HIP(h, copy_out(h, &cap->attn_in_scale, as, sizeof(double)));
+    for (int g = 0; g < Hkv; g++)
+        TL_LAUNCH(h, launch_kv_gather(h->stream, h->kv, h->rows_seq, layer, g, pos, 1, kv_rows + g * kHeadDim,
+                                      kv_rows + KVD + g * kHeadDim));
+    TL_HIP(h, copy_out(h, cap->k_row, kv_rows, KVD));
+    TL_HIP(h, copy_out(h, cap->v_row, kv_rows + KVD, KVD));
+    if (cap->kv_scales) {
+        TL_HIP(h, copy_out(h, cap->kv_scales, h->kv_sk + (size_t)layer * Hkv, sizeof(float) * Hkv));
+        TL_HIP(h, copy_out(h, cap->kv_scales + Hkv, h->kv_sv + (size_t)layer * Hkv, sizeof(float) * Hkv));
+    }
+    TL_LAUNCH(h, launch_qkv_post(h->stream, h->qkv, 1, Hq, Hkv, rowmap(h), h->rope_cos, h->rope_sin, h->kv, layer,
+                                 h->kv_sk, h->kv_sv, h->q8, h->qs, nullptr, false));
+    TL_HIP(h, copy_out(h, cap->q8, h->q8, D));
+    TL_HIP(h, copy_out(h, &cap->q_scale, h->qs, sizeof(double)));
+    AttnDebug dbg;
+    dbg.scores = scores;
+    dbg.probs = probs;
+    dbg.score_scale = scl;
+    dbg.key0 = cap->key0;
+    dbg.n_keys = cap->n_keys;
+    // the recomputed attention output goes to h->att, whose copy is queued above
+    TL_LAUNCH(h, launch_attention(h->stream, h->q8, h->qs, 1, Hq, Hkv, rowmap(h), h->kv, layer, h->kv_sk, h->kv_sv,
+                                  h->att, pos + 1, dbg));
+    TL_HIP(h, copy_out(h, cap->score_scale, scl, sizeof(float) * Hq));
+    TL_HIP(h, copy_out(h, cap->scores, scores, sizeof(int32_t) * win));
+    TL_HIP(h, copy_out(h, cap->probs, probs, win));
+    return TL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t tl_capture_step(tl_handle* h, int32_t seq, tl_capture* cap) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    const tl_config& c = h->cfg;
+    TL_REQ(h, cap, "null pointer");
+    TL_REQ(h, seq >= 0 && seq < h->max_seqs, "sequence out of range");
+    TL_REQ(h, cap->layer >= 0 && cap->layer < c.n_layers, "capture layer out of range");
+    TL_REQ(h, h->host_ngen[seq] >= 1, "tl_capture_step needs a prefilled sequence");
+    const int32_t pos = h->host_cursor[seq];
+    TL_REQ(h, pos + 1 <= c.max_pos, "Sequence length exceeds max_position_embeddings");
+    TL_REQ(h, cap->key0 >= 0 && cap->key0 <= pos + 1, "attention window outside keys 0..pos");
+    if (cap->n_keys < 0) cap->n_keys = pos + 1 - cap->key0;
+    TL_REQ(h, cap->key0 + cap->n_keys <= pos + 1, "attention window outside keys 0..pos");
+    int32_t r = check_model_loaded(h);
+    if (r) return r;
+    const int D = h->D, V = c.vocab;
+    const int32_t first = h->host_ngen[seq];
+    CaptureScratch sc(h->stream);
+    float* xin = sc.get<float>(D);
+    if (!xin) return fail(h, TL_ERR_INTERNAL, "hipMalloc");
+    if ((r = upload_rows(h, 1, seq, false, pos))) return r;
+    cap->pos = pos;
+    TL_HIP(h, hipMemcpyAsync(&cap->token_in, h->token_cur + seq, sizeof(int32_t), hipMemcpyDeviceToHost, h->stream));
+    // one step of decode_step1, eagerly
+    TL_LAUNCH(h, launch_embed_step(h->stream, h->token_cur, h->row_seq, 1, h->cursor, h->row_pos, h->D, c.vocab,
+                                   h->emb, h->emb_s, h->x));
+    for (int l = 0; l < c.n_layers; l++) {
+        if (l == cap->layer) {
+            TL_HIP(h, hipMemcpyAsync(xin, h->x, sizeof(float) * D, hipMemcpyDeviceToDevice, h->stream));
+            TL_HIP(h, copy_out(h, cap->layer_in, h->x, sizeof(float) * D));
+        }
+        if ((r = layer_row1(h, l, pos + 1))) return r;
+        if (l == cap->layer && (r = capture_layer(h, l, pos, xin, cap, sc))) return r;
+    }
+    TL_HIP(h, copy_out(h, cap->final_hidden, h->x, sizeof(float) * D));
+    std::vector<float> logits;
+    if (cap->top_ids || cap->top_logits) {
+        // the step's logits through the standalone LM-head operator's kernels
+        logits.resize(V);
+        TL_LAUNCH(h, launch_reset_keys(h->stream, h->op_key, 1));
+        TL_LAUNCH(h, launch_rmsnorm_quant(h->stream, h->x, h->g_final, 1, D, c.rms_eps, h->plan, nullptr, h->a8, h->as));
+        GemvArgs g{};
+        g.w = h->lm_w; g.ws = h->lm_s; g.x = h->a8; g.xs = h->as; g.key = h->op_key; g.y = h->logits; g.n = V; g.k = D;
+        TL_LAUNCH(h, launch_gemv(h->stream, EPI_ARGMAX, g));
+        TL_HIP(h, copy_out(h, logits.data(), h->logits, sizeof(float) * V));
+    }
+    if ((r = lm_head_rows(h, h->x, 1, seq, 1))) return r;
+    const size_t slot = (size_t)seq * c.max_pos + first;
+    TL_HIP(h, hipMemcpyAsync(&cap->token, h->tokens_out + slot, sizeof(int32_t), hipMemcpyDeviceToHost, h->stream));
+    TL_HIP(h, hipMemcpyAsync(&cap->logit, h->logit_out + slot, sizeof(float), hipMemcpyDeviceToHost, h->stream));
+    if ((r = finish(h))) return r;
+    h->host_cursor[seq] += 1;
+    h->host_ngen[seq] += 1;
+    if (!logits.empty()) {
+        const int k = std::min(TL_CAPTURE_TOPK, V);
+        std::vector<int32_t> idx(V);
+        for (int i = 0; i < V; i++) idx[i] = i;
+        std::partial_sort(idx.begin(), idx.begin() + k, idx.end(), [&](int32_t a, int32_t b) {
+            return logits[a] > logits[b] || (logits[a] == logits[b] && a < b);
+        });
+        for (int i = 0; i < k; i++) {
+            if (cap->top_ids) cap->top_ids[i] = idx[i];
+            if (cap->top_logits) cap->top_logits[i] = logits[idx[i]];
+        }
+    }
+    return TL_OK;
+}
+
 // ---- profiling -----------------------------------------------------------------------
 
 int32_t tl_set_profiling(tl_handle* h, int32_t on) {

@@ -137,6 +137,12 @@ class Engine:
         self.rt.call("tl_decode_batch", int(t.size), t, p, int(n_steps), out)
         return out
 
+    def capture_step(self, layer: int, seq: int = 0, key0: int = 0, n_keys: int = -1) -> dict:
+        """One greedy decode step (as one step of ``decode``) with the tensors
+        of decoder layer ``layer`` copied out (golden_trace.capture_step)."""
+        from .golden_trace import capture_step
+        return capture_step(self.rt, seq, layer, key0, n_keys)
+
     def decode_layer(self, x_dev, layer: int, pos: int, seq: int = 0) -> None:
         """One decoder layer on a device row x_dev (torch float32 [D]) in place."""
         self.rt.call("tl_decode_layer", int(seq), int(layer), int(pos), x_dev)

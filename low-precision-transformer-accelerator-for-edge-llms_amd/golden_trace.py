@@ -1,0 +1,430 @@
+"""Golden-trace I/O and decode-step debug capture.
+
+- memh files in the reference's text format: one hexadecimal word per line,
+  lower case, zero padded to ceil(bits / 4) digits, two's complement for
+  negative values (EX:199-217 write_hex_memh); packed-lane rows with lane 0 in
+  the least significant (right-most) position (EX:220-244
+  write_packed_lane_memh); readers with the sign extension of
+  hls/common/test_memh.hpp:14-76.
+- The canonical case format of docs/golden_trace_plan.md (section 5): one
+  manifest.json listing the cases, one .npz of numeric arrays per case, and
+  packed RTL fixtures under <phase>/rtl/ (EX:292-415 build_gemm_case).
+- capture_step: one greedy decode step with the tensors of one decoder layer
+  copied out (the capture list of docs/design_decisions.txt:366-392, B8),
+  through tl_capture_step.
+- replay_gemm_case / replay_gemm_fixture: run an exported shared_gemm_engine
+  case (EX:292-415) through the library's INT8 GEMM and compare the INT32
+  accumulators.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import json
+import os
+from pathlib import Path
+
+import numpy as np
+
+from ._native import CAPTURE_TOPK, Runtime, TlCapture
+
+_HEX = np.frombuffer(b"0123456789abcdef", dtype=np.uint8)
+
+
+def _ceil_div(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+def _as_words(values, bits: int) -> np.ndarray:
+    """Integer values -> uint64 words masked to `bits` (two's complement).
+    For integers, the signed branch of EX:210-214 ((v + 2**bits) & mask for
+    v < 0) and the unsigned one (v & mask) give the same word."""
+    a = np.asarray(values)
+    if a.dtype.kind == "u":
+        u = a.astype(np.uint64)
+    elif a.dtype.kind in "ib":
+        u = a.astype(np.int64).view(np.uint64)
+    elif a.dtype.kind == "f":   # int(raw_value) truncates toward zero
+        u = np.trunc(a).astype(np.int64).view(np.uint64)
+    else:
+        raise TypeError(f"memh values must be numeric, got {a.dtype}")
+    if bits < 64:
+        u = u & np.uint64((1 << bits) - 1)
+    return u
+
+
+def _hex_digits(words: np.ndarray, width: int) -> np.ndarray:
+    """[n] uint64 -> [n][width] ASCII hex digits, most significant first."""
+    shifts = np.arange(width - 1, -1, -1, dtype=np.uint64) * np.uint64(4)
+    nib = (words.reshape(-1, 1) >> shifts) & np.uint64(0xF)
+    return _HEX[nib.astype(np.intp)]
+
+
+def _write_rows(path, digits: np.ndarray) -> None:
+    path = Path(path)
+    path.parent.mkdir(parents=True, exist_ok=True)
+    rows = np.concatenate([digits, np.full((digits.shape[0], 1), ord("\n"), np.uint8)], axis=1)
+    path.write_bytes(rows.tobytes())
+
+
+def write_hex_memh(path, values, *, bits: int, signed: bool) -> None:
+    """EX:199-217: one word of `bits` per line, every value of the flattened
+    array in order.  `signed` is kept for the reference's signature: the
+    masked word does not depend on it."""
+    del signed
+    flat = np.asarray(values).reshape(-1)
+    _write_rows(path, _hex_digits(_as_words(flat, bits), _ceil_div(bits, 4)))
+
+
+def write_packed_lane_memh(path, values, *, bits_per_lane: int, signed: bool) -> None:
+    """EX:220-244: one line per row (a 1-D array is one row), lanes written
+    from the last to the first so lane 0 is the right-most word."""
+    del signed
+    arr = np.asarray(values)
+    if arr.ndim == 1:
+        arr = arr.reshape(1, -1)
+    rows, lanes = arr.shape[0], int(np.prod(arr.shape[1:]))
+    width = _ceil_div(bits_per_lane, 4)
+    words = _as_words(arr.reshape(rows, lanes)[:, ::-1].reshape(-1), bits_per_lane)
+    _write_rows(path, _hex_digits(words, width).reshape(rows, lanes * width))
+
+
+def read_memh_lines(path) -> list[str]:
+    """test_memh.hpp:14-28: the non-empty lines of the file."""
+    p = Path(path)
+    if not p.is_file():
+        raise FileNotFoundError(f"Failed to open memh file: {path}")
+    return [ln for ln in p.read_text().split("\n") if ln]
+
+
+def _hex_prefix(token: str) -> int:
+    """Leading hexadecimal digits of a token as an unsigned integer (what
+    `stream >> std::hex` extracts; 0 when there are none), wrapped to 64 bits."""
+    t = token.strip()
+    if t[:2].lower() == "0x":
+        t = t[2:]
+    n = 0
+    while n < len(t) and t[n] in "0123456789abcdefABCDEF":
+        n += 1
+    return int(t[:n], 16) & ((1 << 64) - 1) if n else 0
+
+
+def parse_hex_unsigned(token: str) -> int:
+    """test_memh.hpp:46-52."""
+    return _hex_prefix(token)
+
+
+def parse_hex_signed(token: str, bits: int) -> int:
+    """test_memh.hpp:30-44: sign-extend from bit bits-1 (only that bit is
+    tested; digits above it are kept), as a signed 64-bit value."""
+    v = _hex_prefix(token)
+    if bits < 64 and v & (1 << (bits - 1)):
+        v |= ((1 << 64) - 1) & ~((1 << bits) - 1)
+    return v - (1 << 64) if v >> 63 else v
+
+
+_NIBBLE = np.full(256, 255, np.uint8)
+_NIBBLE[np.frombuffer(b"0123456789abcdef", np.uint8)] = np.arange(16, dtype=np.uint8)
+_NIBBLE[np.frombuffer(b"ABCDEF", np.uint8)] = np.arange(10, 16, dtype=np.uint8)
+
+
+def _nibbles_to_words(nib: np.ndarray) -> np.ndarray:
+    """[..., width] nibbles, most significant first -> [...] uint64."""
+    words = np.zeros(nib.shape[:-1], np.uint64)
+    for i in range(nib.shape[-1]):
+        words = (words << np.uint64(4)) | nib[..., i].astype(np.uint64)
+    return words
+
+
+def _read_words(path) -> np.ndarray:
+    """The unsigned word of every line (parse_hex_unsigned), vectorized when
+    every line is 1..16 plain hex digits."""
+    lines = read_memh_lines(path)
+    if not lines:
+        return np.zeros(0, np.uint64)
+    if max(len(ln) for ln in lines) <= 16:
+        try:
+            b = np.char.rjust(np.char.encode(np.array(lines), "ascii"), 16, b"0")
+        except UnicodeEncodeError:
+            b = None
+        if b is not None:
+            nib = _NIBBLE[np.frombuffer(b.astype("S16").tobytes(), np.uint8).reshape(-1, 16)]
+            if not (nib == 255).any():
+                return _nibbles_to_words(nib)
+    return np.array([_hex_prefix(ln) for ln in lines], np.uint64)
+
+
+# The casts of test_memh.hpp:54-76 keep the low bits of the parsed value, which
+# the sign extension of parse_hex_signed leaves unchanged.
+def read_scalar_memh_i32(path) -> np.ndarray:
+    """test_memh.hpp:54-60."""
+    return (_read_words(path) & np.uint64(0xFFFFFFFF)).astype(np.uint32).view(np.int32)
+
+
+def read_scalar_memh_u32(path) -> np.ndarray:
+    """test_memh.hpp:62-68."""
+    return (_read_words(path) & np.uint64(0xFFFFFFFF)).astype(np.uint32)
+
+
+def read_scalar_memh_i8(path) -> np.ndarray:
+    """test_memh.hpp:70-76."""
+    return (_read_words(path) & np.uint64(0xFF)).astype(np.uint8).view(np.int8)
+
+
+def read_packed_lane_memh(path, *, bits_per_lane: int, signed: bool, lanes: int | None = None) -> np.ndarray:
+    """Inverse of write_packed_lane_memh: [rows][lanes] (int64 when signed,
+    uint64 otherwise).  Every line must hold lanes * ceil(bits / 4) digits."""
+    width = _ceil_div(bits_per_lane, 4)
+    lines = read_memh_lines(path)
+    if not lines:
+        return np.zeros((0, lanes or 0), np.int64 if signed else np.uint64)
+    n_chars = len(lines[0])
+    if lanes is None:
+        if n_chars % width:
+            raise ValueError(f"{path}: line of {n_chars} digits is not a whole number of {width}-digit lanes")
+        lanes = n_chars // width
+    if any(len(ln) != lanes * width for ln in lines):
+        raise ValueError(f"{path}: every line must hold {lanes} lanes of {width} hex digits")
+    raw = np.frombuffer("".join(lines).encode("ascii"), dtype=np.uint8).reshape(len(lines), lanes, width)
+    nib = _NIBBLE[raw]
+    if (nib == 255).any():
+        raise ValueError(f"{path}: non-hexadecimal character")
+    words = _nibbles_to_words(nib)[:, ::-1]
+    if not signed:
+        return np.ascontiguousarray(words)
+    if bits_per_lane >= 64:
+        return np.ascontiguousarray(words.view(np.int64))
+    sign = np.uint64(1 << (bits_per_lane - 1))
+    ext = np.uint64(((1 << 64) - 1) & ~((1 << bits_per_lane) - 1))
+    return np.ascontiguousarray(np.where(words & sign, words | ext, words).view(np.int64))
+
+
+# ---------------------------------------------------------------------------
+# canonical case format: manifest.json + one .npz per case
+# ---------------------------------------------------------------------------
+TRACE_FORMAT_VERSION = 1
+
+
+def _manifest_path(root) -> Path:
+    return Path(root) / "manifest.json"
+
+
+def read_manifest(root) -> dict:
+    p = _manifest_path(root)
+    if not p.is_file():
+        return {"trace_format_version": TRACE_FORMAT_VERSION, "cases": []}
+    return json.loads(p.read_text())
+
+
+def write_case(root, case_id: str, phase: str, block: str, arrays: dict, meta: dict | None = None) -> Path:
+    """Write <root>/<phase>/<case_id>.npz and add (or replace) its manifest
+    entry: case id, phase, block, path (relative to root), dtype and shape
+    summaries and the caller's metadata."""
+    root = Path(root)
+    case_path = root / phase / f"{case_id}.npz"
+    case_path.parent.mkdir(parents=True, exist_ok=True)
+    arrays = {k: np.asarray(v) for k, v in arrays.items()}
+    np.savez(case_path, **arrays)
+    entry = {
+        "case_id": case_id,
+        "phase": phase,
+        "block": block,
+        "path": case_path.relative_to(root).as_posix(),
+        "dtype_summary": {k: str(v.dtype) for k, v in arrays.items()},
+        "shape_summary": {k: list(v.shape) for k, v in arrays.items()},
+    }
+    entry.update(meta or {})
+    man = read_manifest(root)
+    man["cases"] = [c for c in man.get("cases", []) if c.get("case_id") != case_id] + [entry]
+    _manifest_path(root).write_text(json.dumps(man, indent=2) + "\n")
+    return case_path
+
+
+def _resolve(root: Path, path: str) -> Path:
+    p = Path(path)
+    if p.is_absolute() and p.exists():
+        return p
+    for base in (root, root.parent):
+        if (base / p).exists():
+            return base / p
+    # the reference exporter records paths under its own output root
+    for parent in [p] + list(p.parents):
+        if parent.name == root.name:
+            cand = root / p.relative_to(parent)
+            if cand.exists():
+                return cand
+    raise FileNotFoundError(f"case file {path} not found under {root}")
+
+
+def load_case(root, case_id: str) -> tuple[dict, dict[str, np.ndarray]]:
+    """(manifest entry, arrays) of one case; arrays load without pickle."""
+    root = Path(root)
+    for entry in read_manifest(root).get("cases", []):
+        if entry.get("case_id") == case_id:
+            with np.load(_resolve(root, entry["path"]), allow_pickle=False) as z:
+                return entry, {k: z[k] for k in z.files}
+    raise KeyError(f"case {case_id} not in {_manifest_path(root)}")
+
+
+# ---------------------------------------------------------------------------
+# decode-step capture (design_decisions.txt:366-392)
+# ---------------------------------------------------------------------------
+def capture_step(rt: Runtime, seq: int, layer: int, key0: int = 0, n_keys: int = -1) -> dict:
+    """One greedy decode step of sequence `seq` (as one step of tl_decode)
+    with the tensors of decoder layer `layer` copied out.  The attention
+    window holds keys key0 .. key0 + n_keys - 1 (n_keys < 0: through the
+    step's position).  Returns a dict of NumPy arrays and scalars."""
+    cfg = rt.cfg
+    D, Hq, Hkv = cfg["hidden"], cfg["n_heads"], cfg["n_kv_heads"]
+    KVD = Hkv * cfg["head_dim"]
+    W = cfg["max_pos"] if n_keys < 0 else int(n_keys)
+    out = {
+        "layer_in": np.zeros(D, np.float32),
+        "attn_in_q": np.zeros(D, np.int8),
+        "qkv": np.zeros(D + 2 * KVD, np.float32),
+        "q8": np.zeros(D, np.int8),
+        "k_row": np.zeros(KVD, np.int8),
+        "v_row": np.zeros(KVD, np.int8),
+        "kv_scales": np.zeros(2 * Hkv, np.float32),
+        "score_scale": np.zeros(Hq, np.float32),
+        "scores": np.zeros(Hq * max(W, 1), np.int32),
+        "probs": np.zeros(Hq * max(W, 1), np.int8),
+        "attended": np.zeros(D, np.float32),
+        "layer_out": np.zeros(D, np.float32),
+        "final_hidden": np.zeros(D, np.float32),
+        "top_ids": np.zeros(CAPTURE_TOPK, np.int32),
+        "top_logits": np.zeros(CAPTURE_TOPK, np.float32),
+    }
+    cap = TlCapture()
+    cap.layer, cap.key0, cap.n_keys = int(layer), int(key0), int(n_keys)
+    for k, v in out.items():
+        setattr(cap, k, v.ctypes.data)
+    rt.check(rt.lib.tl_capture_step(rt.h, int(seq), C.byref(cap)), "tl_capture_step")
+    W = cap.n_keys
+    out["scores"] = out["scores"][:Hq * W].reshape(Hq, W)
+    out["probs"] = out["probs"][:Hq * W].reshape(Hq, W)
+    out["kv_scales"] = out["kv_scales"].reshape(2, Hkv)
+    out.update(layer=int(layer), pos=cap.pos, key0=cap.key0, n_keys=W, token_in=cap.token_in, token=cap.token,
+               logit=np.float32(cap.logit), attn_in_scale=cap.attn_in_scale, q_scale=cap.q_scale)
+    return out
+
+
+_SCALARS = ("layer", "pos", "key0", "n_keys", "token_in", "token")
+
+
+def export_capture(capture: dict, root, case_id: str | None = None, memh: bool = True) -> str:
+    """Write a capture as a decode-step case (phase7, block "decode_step"):
+    the .npz holds every array and scalar, the manifest entry its layer,
+    position and window, and with memh=True the integer tensors are also
+    written as packed RTL fixtures under phase7/rtl/ (one 64-lane row per
+    head for q8 / K / V, one row per head of the score and probability
+    windows).  Returns the case id."""
+    layer, pos = int(capture["layer"]), int(capture["pos"])
+    case_id = case_id or f"phase7_decode_layer{layer}_pos{pos}"
+    arrays = {k: v for k, v in capture.items() if isinstance(v, np.ndarray)}
+    for k in _SCALARS:
+        arrays[k] = np.asarray([capture[k]], np.int32)
+    arrays["logit"] = np.asarray([capture["logit"]], np.float32)
+    arrays["attn_in_scale"] = np.asarray([capture["attn_in_scale"]], np.float64)
+    arrays["q_scale"] = np.asarray([capture["q_scale"]], np.float64)
+    meta = {"layer_id": layer, "token_start": pos, "token_count": 1, "key0": int(capture["key0"]),
+            "n_keys": int(capture["n_keys"])}
+    if memh:
+        base = Path(root) / "phase7" / "rtl" / case_id
+        hd = 64
+        write_hex_memh(base.with_suffix(".meta.memh"),
+                       np.asarray([layer, pos, capture["key0"], capture["n_keys"], capture["token_in"],
+                                   capture["token"]], np.uint32), bits=32, signed=False)
+        write_packed_lane_memh(base.with_suffix(".q8_packed.memh"), capture["q8"].reshape(-1, hd), bits_per_lane=8,
+                               signed=True)
+        write_packed_lane_memh(base.with_suffix(".k_row_packed.memh"), capture["k_row"].reshape(-1, hd),
+                               bits_per_lane=8, signed=True)
+        write_packed_lane_memh(base.with_suffix(".v_row_packed.memh"), capture["v_row"].reshape(-1, hd),
+                               bits_per_lane=8, signed=True)
+        if capture["n_keys"] > 0:
+            write_packed_lane_memh(base.with_suffix(".scores_packed.memh"), capture["scores"], bits_per_lane=32,
+                                   signed=True)
+            write_packed_lane_memh(base.with_suffix(".probs_packed.memh"), capture["probs"], bits_per_lane=8,
+                                   signed=True)
+        write_hex_memh(base.with_suffix(".top_ids.memh"), capture["top_ids"], bits=32, signed=False)
+        meta["rtl_fixture_base"] = base.relative_to(Path(root)).as_posix()
+    write_case(root, case_id, "phase7", "decode_step", arrays, meta)
+    return case_id
+
+
+# ---------------------------------------------------------------------------
+# replay of exported shared_gemm_engine cases (EX:259-415)
+# ---------------------------------------------------------------------------
+GEMM_N_TILE = 32      # EX:45 N_TILE: lane = m_local * N_TILE + n_local (EX:283-289)
+GEMM_LANES = 512      # EX:46
+
+
+def _gemm_i8(rt: Runtime, act: np.ndarray, wt: np.ndarray) -> np.ndarray:
+    """act [m][K] int8 . wt [K][n] int8 -> [m][n] int32 on the device (K is
+    zero-padded to the GEMM's multiple of 64, which leaves every sum as is)."""
+    from .tinyllama import dev, empty, host
+    m, k = act.shape
+    n = wt.shape[1]
+    kp = max(64, _ceil_div(k, 64) * 64)
+    a = np.zeros((m, kp), np.int8)
+    a[:, :k] = act
+    w = np.zeros((n, kp), np.int8)
+    w[:, :k] = wt.T
+    c = empty((m, n), np.int32)
+    rt.call("tl_gemm_i8", dev(a), dev(w), m, n, kp, c)
+    return host(c)
+
+
+def replay_gemm_case(rt: Runtime, arrays: dict) -> dict:
+    """A case .npz of EX:328-336 (act [m][K], wt [K][n], acc_expected [m][n]):
+    the library's accumulators and whether they equal the expected ones."""
+    act = np.asarray(arrays["act"], np.int8)
+    wt = np.asarray(arrays["wt"], np.int8)
+    acc = _gemm_i8(rt, act, wt)
+    exp = np.asarray(arrays["acc_expected"], np.int32)
+    return {"acc": acc, "match": bool(acc.shape == exp.shape and np.array_equal(acc, exp))}
+
+
+def replay_gemm_fixture(rt: Runtime, fixture_base) -> dict:
+    """The RTL fixture files of EX:338-386 (<base>.meta.memh = K, active
+    lanes, m, n; .act_steps.memh / .wt_steps.memh = [K][512] int8 lane
+    steps; .acc_expected_lane.memh = [512] int32): rebuild the operand tiles
+    from the lanes, run them through the library and compare lane by lane."""
+    base = str(fixture_base)
+    k_total, active, m, n = (int(v) for v in read_scalar_memh_u32(base + ".meta.memh")[:4])
+    if active != m * n or m * GEMM_N_TILE > GEMM_LANES or n > GEMM_N_TILE:
+        raise ValueError(f"{base}: meta {k_total, active, m, n} does not fit the lane packing")
+    act_steps = read_scalar_memh_i8(base + ".act_steps.memh").reshape(k_total, GEMM_LANES)
+    wt_steps = read_scalar_memh_i8(base + ".wt_steps.memh").reshape(k_total, GEMM_LANES)
+    acc_lane = read_scalar_memh_i32(base + ".acc_expected_lane.memh")
+    act = np.ascontiguousarray(act_steps[:, [mi * GEMM_N_TILE for mi in range(m)]].T)
+    wt = np.ascontiguousarray(wt_steps[:, :n])
+    acc = _gemm_i8(rt, act, wt)
+    lanes = np.zeros(GEMM_LANES, np.int32)
+    for mi in range(m):
+        lanes[mi * GEMM_N_TILE:mi * GEMM_N_TILE + n] = acc[mi]
+    return {"acc": acc, "acc_lane": lanes, "match": bool(np.array_equal(lanes, acc_lane))}
+
+
+def replay_manifest(rt: Runtime, root) -> list[dict]:
+    """Replay every shared_gemm_engine case a manifest lists; other blocks
+    are reported as not replayed."""
+    root = Path(root)
+    results = []
+    for entry in read_manifest(root).get("cases", []):
+        if entry.get("block") != "shared_gemm_engine":
+            results.append({"case_id": entry.get("case_id"), "replayed": False})
+            continue
+        _, arrays = load_case(root, entry["case_id"])
+        r = replay_gemm_case(rt, arrays)
+        results.append({"case_id": entry["case_id"], "replayed": True, "match": r["match"]})
+    return results
+
+
+def fixture_paths(root) -> list[str]:
+    """Sorted fixture bases (<...>/rtl/<case_id>) found under root."""
+    out = set()
+    for dirpath, _, files in os.walk(root):
+        for f in files:
+            if f.endswith(".meta.memh"):
+                out.add(os.path.join(dirpath, f[: -len(".meta.memh")]))
+    return sorted(out)

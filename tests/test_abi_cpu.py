@@ -107,3 +107,21 @@ def test_golden_surface_host_logic(tmp_path):
     assert w.embed([1, 3]).shape == (2, 64) and w.embed([1]).dtype == np.float32
     assert w.kv_scales() is None
     assert w._optional_array("layer0_k_b") is None and w._optional_array("layer0_q_b").dtype == np.float32
+
+
+def test_capture_layout_matches_header(tmp_path):
+    # offsets of struct tl_capture as the C compiler lays it out from the header
+    fields = [f for f, _ in _native.TlCapture._fields_]
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "tl_int8.h"\nint main(void) {\n'
+                   + "".join(f'    printf("%zu\\n", offsetof(tl_capture, {f}));\n' for f in fields)
+                   + '    printf("%zu\\n", sizeof(tl_capture));\n    printf("%d\\n", TL_CAPTURE_TOPK);\n'
+                   + "    return 0;\n}\n")
+    exe = tmp_path / "layout"
+    import subprocess
+    subprocess.run(["gcc", "-std=c11", "-I", os.path.join(os.path.dirname(_native.HEADER)), "-o", str(exe),
+                    str(src)], check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    want = [getattr(_native.TlCapture, f).offset for f in fields] + [ctypes.sizeof(_native.TlCapture),
+                                                                     _native.CAPTURE_TOPK]
+    assert got == want

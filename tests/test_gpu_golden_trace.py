@@ -1,0 +1,212 @@
+"""Decode-step debug capture (tl_capture_step) against the CPU oracle's trace
+of the same step, the capture's export in the canonical case format, and the
+replay of shared_gemm_engine cases written in the reference exporter's
+layout (EX:259-386).  Integer tensors, float tensors and token ids must be
+bit-identical to the oracle's."""
+import numpy as np
+import pytest
+
+import oracle
+from gpu_util import assert_bits_equal
+from lpta import golden_trace as gt
+
+pytestmark = pytest.mark.gpu
+
+
+def engine_for(model):
+    from lpta.engine import Engine
+    return Engine(model.cfg).load_model(model)
+
+
+def oracle_prefill(orc, m, prompt):
+    kc, vc = m.new_cache()
+    x = None
+    for i, t in enumerate(prompt):
+        x = orc.embed(int(t))
+        for layer in range(m.cfg["n_layers"]):
+            x = orc.decode_row(layer, i, x, kc, vc)
+    return orc.lm_head(x)[0], kc, vc
+
+
+def oracle_step(orc, m, tok, pos, kc, vc, layer):
+    """The oracle's decode step at pos with layer's trace and the top-16 logits."""
+    c = m.cfg
+    D, Hq, V = c["hidden"], c["n_heads"], c["vocab"]
+    KVD = c["n_kv_heads"] * 64
+    tr = {"attn_in_q": np.zeros(D, np.int8), "attn_in_s": np.zeros(1), "qkv": np.zeros(D + 2 * KVD, np.float32),
+          "q8": np.zeros(D, np.int8), "q_s": np.zeros(1), "scores": np.zeros(Hq * (pos + 1), np.int32),
+          "probs": np.zeros(Hq * (pos + 1), np.int8), "attended": np.zeros(D, np.float32),
+          "out": np.zeros(D, np.float32)}
+    x = orc.embed(int(tok))
+    x_in = None
+    for li in range(c["n_layers"]):
+        if li == layer:
+            x_in = x.copy()
+            x = orc.decode_row(li, pos, x, kc, vc, tr)
+        else:
+            x = orc.decode_row(li, pos, x, kc, vc)
+    nxt, logit, logits = orc.lm_head(x, want_logits=True)
+    top = np.lexsort((np.arange(V), -logits))[:16]
+    tr["scores"] = tr["scores"].reshape(Hq, pos + 1)
+    tr["probs"] = tr["probs"].reshape(Hq, pos + 1)
+    return dict(tr, x_in=x_in, final=x, token=nxt, logit=logit, top_ids=top, top_logits=logits[top])
+
+
+CASES = [
+    # (geometry, prompt length, captured layer, key0, n_keys)
+    ("small", 70, 1, 0, -1),
+    ("small", 9, 0, 3, 5),
+    ("tinyllama2", 33, 1, 0, -1),
+]
+
+
+def model_for(name):
+    if name == "small":
+        return oracle.synthetic_model(dict(oracle.SMALL_CFG), seed=11)
+    cfg = dict(oracle.TINYLLAMA_CFG, n_layers=2, vocab=512)
+    return oracle.synthetic_model(cfg, seed=12, kv_range=(0.01, 0.1))
+
+
+@pytest.mark.parametrize("name,n_prompt,layer,key0,n_keys", CASES)
+def test_capture_step_matches_oracle(name, n_prompt, layer, key0, n_keys, tmp_path):
+    print(f"capture case {name} prompt={n_prompt} layer={layer} window={key0},{n_keys}", flush=True)
+    m = model_for(name)
+    c = m.cfg
+    prompt = np.random.default_rng(n_prompt).integers(0, c["vocab"], n_prompt).astype(np.int32)
+    eng = engine_for(m)
+    first, _ = eng.prefill(prompt)
+    cap = eng.capture_step(layer, key0=key0, n_keys=n_keys)
+    orc = oracle.Oracle(m)
+    tok0, kc, vc = oracle_prefill(orc, m, prompt)
+    assert first == tok0
+    pos = n_prompt
+    want = oracle_step(orc, m, tok0, pos, kc, vc, layer)
+    W = pos + 1 - key0 if n_keys < 0 else n_keys
+
+    assert (cap["layer"], cap["pos"], cap["key0"], cap["n_keys"], cap["token_in"]) == (layer, pos, key0, W, tok0)
+    assert_bits_equal(cap["layer_in"], want["x_in"], "layer input")
+    assert_bits_equal(cap["attn_in_q"], want["attn_in_q"], "attention input (INT8)")
+    assert cap["attn_in_scale"] == want["attn_in_s"][0]
+    assert_bits_equal(cap["qkv"], want["qkv"], "Q|K|V projections")
+    assert_bits_equal(cap["q8"], want["q8"], "query (INT8)")
+    assert cap["q_scale"] == want["q_s"][0]
+    G = c["n_heads"] // c["n_kv_heads"]
+    for g in range(c["n_kv_heads"]):
+        assert_bits_equal(cap["k_row"][g * 64:(g + 1) * 64], kc[layer, g, pos], f"K row head {g}")
+        assert_bits_equal(cap["v_row"][g * 64:(g + 1) * 64], vc[layer, g, pos], f"V row head {g}")
+        assert_bits_equal(cap["kv_scales"][0, g], m.kv_sk[layer, g], "K scale")
+        assert_bits_equal(cap["kv_scales"][1, g], m.kv_sv[layer, g], "V scale")
+        # score scale f32((s_q s_k) / sqrt(64)) of each query head of the group
+        want_scl = np.float32((want["q_s"][0] * np.float64(m.kv_sk[layer, g])) * 0.125)
+        assert_bits_equal(cap["score_scale"][g * G:(g + 1) * G], np.full(G, want_scl, np.float32), "score scale")
+    assert_bits_equal(cap["scores"], want["scores"][:, key0:key0 + W], "INT32 score window")
+    assert_bits_equal(cap["probs"], want["probs"][:, key0:key0 + W], "INT8 probability window")
+    assert (cap["probs"] >= 0).all()
+    assert_bits_equal(cap["attended"], want["attended"], "attention output")
+    assert_bits_equal(cap["layer_out"], want["out"], "layer output")
+    assert_bits_equal(cap["final_hidden"], want["final"], "final hidden state")
+    assert cap["token"] == want["token"] and cap["top_ids"][0] == want["token"]
+    assert_bits_equal(cap["top_ids"], want["top_ids"].astype(np.int32), "top-16 ids")
+    assert_bits_equal(cap["top_logits"], want["top_logits"], "top-16 logits")
+    assert_bits_equal(np.float32(cap["logit"]), np.float32(want["logit"]), "chosen logit")
+
+    # the capture was one real decode step: the sequence continues as if
+    # tl_decode had run it
+    more, _ = eng.decode(3)
+    eng.close()
+    ref = engine_for(m)
+    plain, _ = ref.generate(prompt, 5)
+    ref.close()
+    assert [first, cap["token"], *more.tolist()] == plain.tolist()
+
+    # export in the canonical case format and read it back
+    case_id = gt.export_capture(cap, tmp_path)
+    entry, arrays = gt.load_case(tmp_path, case_id)
+    assert entry["block"] == "decode_step" and entry["layer_id"] == layer and entry["token_start"] == pos
+    for k in ("q8", "k_row", "scores", "probs", "attended", "top_ids"):
+        assert_bits_equal(arrays[k], cap[k], f"exported {k}")
+    assert int(arrays["token"][0]) == cap["token"]
+    base = tmp_path / entry["rtl_fixture_base"]
+    q8 = gt.read_packed_lane_memh(str(base) + ".q8_packed.memh", bits_per_lane=8, signed=True)
+    assert_bits_equal(q8.astype(np.int8), cap["q8"].reshape(-1, 64), "q8 fixture")
+    sc = gt.read_packed_lane_memh(str(base) + ".scores_packed.memh", bits_per_lane=32, signed=True)
+    assert_bits_equal(sc.astype(np.int32), cap["scores"], "score fixture")
+    meta = gt.read_scalar_memh_u32(str(base) + ".meta.memh")
+    assert meta.tolist() == [layer, pos, key0, W, tok0, cap["token"]]
+
+
+def test_capture_rejects_bad_windows():
+    m = model_for("small")
+    eng = engine_for(m)
+    from lpta import TlValueError
+    with pytest.raises(TlValueError, match="prefilled"):
+        eng.capture_step(0)
+    eng.prefill(np.arange(5, dtype=np.int32))
+    with pytest.raises(TlValueError, match="window"):
+        eng.capture_step(0, key0=2, n_keys=5)    # keys 2..6 but pos = 5
+    with pytest.raises(TlValueError, match="layer"):
+        eng.capture_step(2)
+    cap = eng.capture_step(1, key0=6, n_keys=-1)  # empty window at the step's own key
+    assert cap["n_keys"] == 0 and cap["scores"].shape == (m.cfg["n_heads"], 0)
+    eng.close()
+
+
+# ---- replay of exporter-format shared_gemm_engine cases ------------------------------
+
+N_TILE, LANES = 32, 512   # EX:45-46
+
+
+def write_ex_gemm_case(root, case_id, act, wt, acc):
+    """A shared_gemm_engine case laid out as EX:259-386 writes it."""
+    m, k = act.shape
+    n = wt.shape[1]
+    act_steps = np.zeros((k, LANES), np.int8)
+    wt_steps = np.zeros((k, LANES), np.int8)
+    acc_lane = np.zeros(LANES, np.int32)
+    for mi in range(m):
+        for ni in range(n):
+            lane = mi * N_TILE + ni
+            act_steps[:, lane] = act[mi]
+            wt_steps[:, lane] = wt[:, ni]
+            acc_lane[lane] = acc[mi, ni]
+    gt.write_case(root, case_id, "phase3", "shared_gemm_engine",
+                  dict(act=act, wt=wt, acc_expected=acc, act_steps=act_steps, wt_steps=wt_steps,
+                       acc_expected_lane=acc_lane, active_lane_count=np.asarray([m * n], np.int32)),
+                  {"k_total": k, "m_count": m, "n_count": n})
+    base = root / "phase3" / "rtl" / case_id
+    gt.write_hex_memh(str(base) + ".meta.memh", np.asarray([k, m * n, m, n], np.uint32), bits=32, signed=False)
+    gt.write_hex_memh(str(base) + ".act_steps.memh", act_steps, bits=8, signed=True)
+    gt.write_hex_memh(str(base) + ".wt_steps.memh", wt_steps, bits=8, signed=True)
+    gt.write_hex_memh(str(base) + ".acc_expected_lane.memh", acc_lane, bits=32, signed=True)
+    return base
+
+
+@pytest.mark.parametrize("m,n,k", [(16, 32, 2048), (3, 7, 40), (16, 32, 5632)])
+def test_replay_gemm_cases(m, n, k, tmp_path):
+    print(f"replay case m={m} n={n} k={k}", flush=True)
+    rng = np.random.default_rng(k + m)
+    act = rng.integers(-127, 128, (m, k)).astype(np.int8)
+    wt = rng.integers(-127, 128, (k, n)).astype(np.int8)
+    acc = oracle.gemm_i8(act, np.ascontiguousarray(wt.T))
+    base = write_ex_gemm_case(tmp_path, "phase3_decode_layer0_q_gemm_m0_n0", act, wt, acc)
+    bad = acc.copy()
+    bad[m - 1, n - 1] += 1
+    write_ex_gemm_case(tmp_path / "planted", "phase3_decode_layer0_q_gemm_m0_n0", act, wt, bad)
+    gt.write_case(tmp_path, "phase3_other", "phase3", "requantize_unit", {"acc": acc})
+    rt = gt.Runtime(dict(hidden=512, intermediate=1408, n_layers=1, n_heads=8, n_kv_heads=2, head_dim=64,
+                         vocab=64, max_pos=64, rms_eps=np.float32(1e-5), rope_theta=1e4))
+    _, arrays = gt.load_case(tmp_path, "phase3_decode_layer0_q_gemm_m0_n0")
+    r = gt.replay_gemm_case(rt, arrays)
+    assert r["match"]
+    assert_bits_equal(r["acc"], acc, "replayed accumulators")
+    f = gt.replay_gemm_fixture(rt, base)
+    assert f["match"]
+    assert gt.fixture_paths(tmp_path / "phase3") == [str(base)]
+    res = gt.replay_manifest(rt, tmp_path)
+    assert res == [{"case_id": "phase3_decode_layer0_q_gemm_m0_n0", "replayed": True, "match": True},
+                   {"case_id": "phase3_other", "replayed": False}]
+    # a planted wrong accumulator is reported as a mismatch
+    _, arrays = gt.load_case(tmp_path / "planted", "phase3_decode_layer0_q_gemm_m0_n0")
+    assert not gt.replay_gemm_case(rt, arrays)["match"]
+    assert not gt.replay_gemm_fixture(rt, gt.fixture_paths(tmp_path / "planted")[0])["match"]
+    rt.close()
