@@ -130,6 +130,19 @@ int32_t tl_gemm_i8_dequant(tl_handle *h, const int8_t *a, const double *a_scales
 int32_t tl_rope(tl_handle *h, float *v, int32_t rows, int32_t n_heads, const int32_t *pos);
 /* TL:100-103 softmax of each row. */
 int32_t tl_softmax_rows(tl_handle *h, const float *x, int32_t rows, int32_t n, float *p);
+/* TL:106-110 linear in float32: y[M][N] = residual + (x[M][K] . w[K][N] + b[N]),
+ * w in the reference's [K][N] layout; b and residual may be NULL.  The float
+ * model the analysis report compares the INT8 path against (GI:470-626). */
+int32_t tl_linear_f32(tl_handle *h, const float *x, const float *w, const float *b, const float *residual,
+                      int32_t m, int32_t n, int32_t k, float *y);
+/* TL:122-156 attention core in float32 over seq tokens: q [seq][Hq*64] and
+ * k [seq][Hkv*64] after RoPE, v [seq][Hkv*64]; scores = (q . k) * scale with
+ * the causal mask value -1e9 (TL:90-91), weights = softmax(scores)
+ * (TL:100-103), out [seq][Hq*64] = weights . v (query head h reads KV head
+ * h / (Hq / Hkv), TL:94-97).  scores and weights [Hq][seq][seq] may be NULL. */
+int32_t tl_attention_f32(tl_handle *h, const float *q, const float *k, const float *v, int32_t seq,
+                         int32_t n_heads, int32_t n_kv_heads, float scale, float *out, float *scores,
+                         float *weights);
 /* TL:159-161 silu (u == NULL) or the GLU product silu(g) * u (GI:212). */
 int32_t tl_silu_mul(tl_handle *h, const float *g, const float *u, int64_t n, float *y);
 /* GQA attention of query rows over sequence seq's INT8 cache at layer:

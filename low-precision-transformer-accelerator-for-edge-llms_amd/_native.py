@@ -91,6 +91,8 @@ SIGNATURES = {
     "tl_gemm_i8": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _vp]),
     "tl_gemm_i8_dequant": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp]),
     "tl_rope": (_i32, [_vp, _vp, _i32, _i32, _vp]),
+    "tl_linear_f32": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp]),
+    "tl_attention_f32": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, C.c_float, _vp, _vp, _vp]),
     "tl_softmax_rows": (_i32, [_vp, _vp, _i32, _i32, _vp]),
     "tl_silu_mul": (_i32, [_vp, _vp, _vp, _i64, _vp]),
     "tl_attention": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),

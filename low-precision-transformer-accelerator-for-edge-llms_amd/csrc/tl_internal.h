@@ -142,6 +142,12 @@ hipError_t launch_attention(hipStream_t s, const int8_t* q8, const double* q_sca
                             int32_t n_heads, int32_t n_kv_heads, RowMap rm, KvGeom kv,
                             int32_t layer, const float* kv_sk, const float* kv_sv, float* out,
                             int32_t max_t, AttnDebug dbg = AttnDebug());
+// float32 model of the analysis report (tl_float.hip)
+hipError_t launch_linear_f32(hipStream_t s, const float* x, const float* w, const float* b, const float* residual,
+                             int32_t m, int32_t n, int32_t k, float* y);
+hipError_t launch_attention_f32(hipStream_t s, const float* q, const float* k, const float* v, int32_t seq,
+                                int32_t n_heads, int32_t n_kv, float scale, float* out, float* scores,
+                                float* weights);
 hipError_t launch_rope(hipStream_t s, float* v, int32_t rows, int32_t n_heads, const int32_t* pos,
                        const float* cos, const float* sin);
 hipError_t launch_softmax_rows(hipStream_t s, const float* x, int32_t rows, int32_t n, float* p);

@@ -976,6 +976,24 @@ int32_t tl_rope(tl_handle* h, float* v, int32_t rows, int32_t n_heads, const int
     return finish(h);
 }
 
+int32_t tl_linear_f32(tl_handle* h, const float* x, const float* w, const float* b, const float* residual, int32_t m,
+                      int32_t n, int32_t k, float* y) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, x && w && y && m >= 0 && n >= 0 && k >= 0, "bad linear arguments");
+    TL_LAUNCH(h, launch_linear_f32(h->stream, x, w, b, residual, m, n, k, y));
+    return finish(h);
+}
+
+int32_t tl_attention_f32(tl_handle* h, const float* q, const float* k, const float* v, int32_t seq, int32_t n_heads,
+                         int32_t n_kv_heads, float scale, float* out, float* scores, float* weights) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, q && k && v && out, "null pointer");
+    TL_REQ(h, seq >= 0 && seq <= kTileMaxKeys, "sequence longer than 4096 tokens");
+    TL_REQ(h, n_heads >= 1 && n_kv_heads >= 1 && n_heads % n_kv_heads == 0, "heads must be a multiple of KV heads");
+    TL_LAUNCH(h, launch_attention_f32(h->stream, q, k, v, seq, n_heads, n_kv_heads, scale, out, scores, weights));
+    return finish(h);
+}
+
 int32_t tl_softmax_rows(tl_handle* h, const float* x, int32_t rows, int32_t n, float* p) {
     if (!h) return TL_ERR_BAD_DESCRIPTOR;
     TL_REQ(h, x && p && rows >= 0 && n > 0, "bad softmax arguments");

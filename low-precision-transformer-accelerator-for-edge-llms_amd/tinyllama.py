@@ -181,6 +181,139 @@ def silu(x: np.ndarray) -> np.ndarray:
 
 
 # ---------------------------------------------------------------------------
+# TL:106-197, 391-408: the float32 model, the baseline the analysis report
+# compares the INT8 path against (tl_linear_f32 / tl_attention_f32).  Sums
+# run in the kernels' order, so results agree with the reference to float32
+# rounding; the reference's scores and softmax are float64 (float32 scores
+# times a float64 scale), here they stay float32.
+# ---------------------------------------------------------------------------
+def _float_runtime(cfg: dict) -> Runtime:
+    return op_runtime(cfg["rms_norm_eps"], max_pos=cfg["max_position_embeddings"])
+
+
+def _bias(b, n: int):
+    return None if b is None else dev(np.broadcast_to(np.asarray(b, np.float32), (n,)))
+
+
+def linear_dev(rt: Runtime, x, w: np.ndarray, b, rows: int, residual=None):
+    """Device rows x [rows][K] @ w [K][N] (+ b) (+ residual) -> [rows][N]."""
+    w_fp = np.asarray(w, np.float32)
+    k, n = w_fp.shape
+    y = empty((rows, n), np.float32)
+    rt.call("tl_linear_f32", x, dev(w_fp), _bias(b, n), residual, rows, n, k, y)
+    return y
+
+
+def linear(x: np.ndarray, w: np.ndarray, b: np.ndarray | None = None) -> np.ndarray:
+    """TL:106-110: x @ w (+ b) in float32, w [K][N]."""
+    x_fp = np.asarray(x, dtype=np.float32)
+    w_fp = np.asarray(w, dtype=np.float32)
+    k, n = w_fp.shape
+    rows = int(np.prod(x_fp.shape[:-1], dtype=np.int64))
+    if rows == 0:
+        return np.empty(x_fp.shape[:-1] + (n,), np.float32)
+    y = linear_dev(op_runtime(), dev(x_fp.reshape(rows, k)), w_fp, b, rows)
+    return host(y).reshape(x_fp.shape[:-1] + (n,))
+
+
+def rms_norm_dev(rt: Runtime, x, w: np.ndarray, rows: int, n: int):
+    """TL:45-50 on device rows (the handle's epsilon)."""
+    y = empty((rows, n), np.float32)
+    q = empty((rows, n), np.int8)
+    s = empty((rows,), np.float64)
+    rt.call("tl_rmsnorm_quant", x, dev(np.asarray(w, np.float32)), rows, n, y, q, s)
+    return y
+
+
+def self_attention_dev(rt: Runtime, x, layer: dict, cfg: dict, cos, sin, rows: int, capture: bool = False):
+    """TL:122-156 on device rows x [rows][D]: (out, parts) where parts holds
+    the Q/K/V projections and, when capture is set, the scores, weights and
+    attended rows.  The attention output projection is not added to any
+    residual here."""
+    Hq, Hkv, hd = cfg["num_attention_heads"], cfg["num_key_value_heads"], cfg["head_dim"]
+    if hd != 64:
+        raise ValueError("head_dim must be 64")
+    set_rope_rows(rt, cos, sin, rows)
+    q = linear_dev(rt, x, layer["q_w"], layer.get("q_b"), rows)
+    k = linear_dev(rt, x, layer["k_w"], layer.get("k_b"), rows)
+    v = linear_dev(rt, x, layer["v_w"], layer.get("v_b"), rows)
+    parts = {"q": q, "k": k, "v": v}
+    qr, kr = q.clone(), k.clone()
+    pos = dev(np.arange(rows, dtype=np.int32))
+    rt.call("tl_rope", qr, rows, Hq, pos)
+    rt.call("tl_rope", kr, rows, Hkv, pos)
+    att = empty((rows, Hq * hd), np.float32)
+    scores = empty((Hq, rows, rows), np.float32) if capture else None
+    weights = empty((Hq, rows, rows), np.float32) if capture else None
+    rt.call("tl_attention_f32", qr, kr, v, rows, Hq, Hkv, float(np.float32(cfg["attn_scale"])), att, scores, weights)
+    parts.update(attended=att, scores=scores, weights=weights)
+    return att, parts
+
+
+def self_attention(x: np.ndarray, layer: dict, cfg: dict, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
+    """TL:122-156: GQA self-attention of x [seq][D] at positions 0..seq-1."""
+    rt = _float_runtime(cfg)
+    x_fp = np.asarray(x, np.float32)
+    rows = x_fp.shape[0]
+    att, _ = self_attention_dev(rt, dev(x_fp), layer, cfg, cos, sin, rows)
+    return host(linear_dev(rt, att, layer["o_w"], layer.get("o_b"), rows))
+
+
+def feed_forward_dev(rt: Runtime, x, layer: dict, rows: int, residual=None):
+    """TL:164-169 on device rows: (out, gate, up, hidden)."""
+    gate = linear_dev(rt, x, layer["gate_w"], layer.get("gate_b"), rows)
+    up = linear_dev(rt, x, layer["up_w"], layer.get("up_b"), rows)
+    F = gate.shape[1]
+    hid = empty((rows, F), np.float32)
+    rt.call("tl_silu_mul", gate, up, rows * F, hid)
+    out = linear_dev(rt, hid, layer["down_w"], layer.get("down_b"), rows, residual)
+    return out, gate, up, hid
+
+
+def feed_forward(x: np.ndarray, layer: dict) -> np.ndarray:
+    """TL:164-169: down(silu(gate(x)) * up(x))."""
+    x_fp = np.asarray(x, np.float32)
+    rows = int(np.prod(x_fp.shape[:-1], dtype=np.int64))
+    out, *_ = feed_forward_dev(op_runtime(), dev(x_fp.reshape(rows, -1)), layer, rows)
+    return host(out).reshape(x_fp.shape[:-1] + (out.shape[1],))
+
+
+def decoder_layer_dev(rt: Runtime, x, layer: dict, cfg: dict, cos, sin, rows: int):
+    """TL:177-189 on device rows; the residual adds run in the O and down
+    projections' epilogues (x + (a @ W + b), the reference's rounding)."""
+    D = cfg["hidden_size"]
+    a = rms_norm_dev(rt, x, layer["input_norm_w"], rows, D)
+    att, _ = self_attention_dev(rt, a, layer, cfg, cos, sin, rows)
+    x1 = linear_dev(rt, att, layer["o_w"], layer.get("o_b"), rows, residual=x)
+    f = rms_norm_dev(rt, x1, layer["post_norm_w"], rows, D)
+    out, *_ = feed_forward_dev(rt, f, layer, rows, residual=x1)
+    return out
+
+
+def decoder_layer(x: np.ndarray, layer: dict, cfg: dict, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
+    """TL:177-189: pre-norm attention and feed-forward with residuals."""
+    x_fp = np.asarray(x, np.float32)
+    rt = _float_runtime(cfg)
+    return host(decoder_layer_dev(rt, dev(x_fp), layer, cfg, cos, sin, x_fp.shape[0]))
+
+
+def forward(token_ids: list[int], weights: "TinyLlamaWeights", cos: np.ndarray, sin: np.ndarray,
+            layer_count: int | None = None) -> np.ndarray:
+    """TL:391-408: logits [seq][V] of the float32 model (all layers unless
+    layer_count is given)."""
+    cfg = weights.cfg
+    seq = len(token_ids)
+    if seq > cfg["max_position_embeddings"]:
+        raise ValueError(f"Sequence length {seq} exceeds max_position_embeddings={cfg['max_position_embeddings']}")
+    rt = _float_runtime(cfg)
+    x = dev(np.asarray(weights.embed(token_ids), np.float32))
+    for i in range(cfg["num_hidden_layers"] if layer_count is None else layer_count):
+        x = decoder_layer_dev(rt, x, weights.layer(i), cfg, cos, sin, seq)
+    x = rms_norm_dev(rt, x, weights.final_norm_w(), seq, cfg["hidden_size"])
+    return host(linear_dev(rt, x, weights.lm_head_w(), None, seq))
+
+
+# ---------------------------------------------------------------------------
 # TL:198-267: the weight archive
 # ---------------------------------------------------------------------------
 class TinyLlamaWeights:

@@ -27,11 +27,13 @@ LM head is one of the INT8 GEMM roles of the path.
 """
 from __future__ import annotations
 
+import os
 from typing import Any
 
 import numpy as np
 
 from ._native import Runtime
+from . import tinyllama as TL
 from .tinyllama import (TinyLlamaWeights, build_rope_cache, dev, empty, host, load_weights, op_runtime,
                         round_pos, set_rope_rows)
 
@@ -389,6 +391,77 @@ def mixed_precision_decoder_layer(x: np.ndarray, layer: dict, cfg: dict, cos: np
 
 
 # ---------------------------------------------------------------------------
+# GI:91-133, 185-203, 228-253, 408-434: the float32 reference the analysis
+# report compares against, on the library's float32 kernels (TL:106-197)
+# ---------------------------------------------------------------------------
+def _ref_attention_dev(rt: Runtime, a, layer: dict, cfg: dict, cos, sin, rows: int, capture: bool):
+    att, parts = TL.self_attention_dev(rt, a, layer, cfg, cos, sin, rows, capture)
+    out = TL.linear_dev(rt, att, layer["o_w"], layer.get("o_b"), rows)
+    debug: dict[str, Any] = {"q_proj_fp": host(parts["q"]), "k_proj_fp": host(parts["k"]),
+                             "v_proj_fp": host(parts["v"])}
+    if capture:
+        debug.update({"scores_fp": host(parts["scores"]), "weights_fp": host(parts["weights"]),
+                      "attended_fp": host(att), "out_fp": host(out)})
+    return att, out, debug
+
+
+def _ref_ffn_dev(rt: Runtime, f, layer: dict, rows: int, capture: bool):
+    out, gate, up, hid = TL.feed_forward_dev(rt, f, layer, rows)
+    debug: dict[str, Any] = {"gate_proj_fp": host(gate), "up_proj_fp": host(up), "hidden_fp": host(hid)}
+    if capture:
+        debug["out_fp"] = host(out)
+    return hid, out, debug
+
+
+def reference_self_attention(x: np.ndarray, layer: dict, cfg: dict, cos: np.ndarray, sin: np.ndarray,
+                             capture_arrays: bool = False) -> tuple[np.ndarray, dict[str, Any]]:
+    """GI:91-133: float32 self-attention of x [seq][D] with its debug dict."""
+    x_fp, rows = _rows_of(x, cfg["hidden_size"])
+    _, out, debug = _ref_attention_dev(TL._float_runtime(cfg), dev(x_fp), layer, cfg, cos, sin, rows,
+                                       capture_arrays)
+    return host(out), debug
+
+
+def reference_feed_forward(x: np.ndarray, layer: dict,
+                           capture_arrays: bool = False) -> tuple[np.ndarray, dict[str, Any]]:
+    """GI:185-202: float32 SwiGLU feed-forward with its debug dict."""
+    x_fp = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    x2 = x_fp.reshape(-1, x_fp.shape[-1])
+    _, out, debug = _ref_ffn_dev(op_runtime(), dev(x2), layer, x2.shape[0], capture_arrays)
+    lead = x_fp.shape[:-1]
+    debug = {k: v.reshape(lead + (-1,)) for k, v in debug.items()}
+    return host(out).reshape(lead + (-1,)), debug
+
+
+def reference_decoder_layer(x: np.ndarray, layer: dict, cfg: dict, cos: np.ndarray, sin: np.ndarray,
+                            capture_arrays: bool = False) -> tuple[np.ndarray, dict[str, Any]]:
+    """GI:228-253: the float32 decoder layer with its debug dict.  The
+    residual adds run in the projections' epilogues (x + (a @ W + b), the
+    reference's rounding); the projections are recomputed for that."""
+    rt = TL._float_runtime(cfg)
+    x_fp, rows = _rows_of(x, cfg["hidden_size"])
+    D = cfg["hidden_size"]
+    xd = dev(x_fp)
+    a = TL.rms_norm_dev(rt, xd, layer["input_norm_w"], rows, D)
+    att, _, attn_debug = _ref_attention_dev(rt, a, layer, cfg, cos, sin, rows, capture_arrays)
+    x1 = TL.linear_dev(rt, att, layer["o_w"], layer.get("o_b"), rows, residual=xd)
+    f = TL.rms_norm_dev(rt, x1, layer["post_norm_w"], rows, D)
+    hid, _, ffn_debug = _ref_ffn_dev(rt, f, layer, rows, capture_arrays)
+    out = host(TL.linear_dev(rt, hid, layer["down_w"], layer.get("down_b"), rows, residual=x1))
+    debug: dict[str, Any] = {"attn_input_fp": host(a), "x_after_attn_fp": host(x1), "ffn_input_fp": host(f),
+                             "attn": attn_debug, "ffn": ffn_debug}
+    if capture_arrays:
+        debug["layer_out_fp"] = out
+    return out, debug
+
+
+def forward_reference(token_ids, weights: TinyLlamaWeights, cos: np.ndarray, sin: np.ndarray,
+                      layer_count: int) -> np.ndarray:
+    """GI:408-434: float32 logits [seq][V] over the first layer_count layers."""
+    return TL.forward(list(token_ids), weights, cos, sin, layer_count=layer_count)
+
+
+# ---------------------------------------------------------------------------
 # whole model: one device-resident engine per weight archive
 # ---------------------------------------------------------------------------
 class _Engine(_Model):
@@ -552,3 +625,219 @@ def run_generate(prompt: str | None, token_ids_arg: str | None, weights_path, la
     print("")
     print(f"Output token ids: {generated}")
     return generated
+
+
+# ---------------------------------------------------------------------------
+# GI:284-338, 351-353, 401-405, 470-626: the analysis report and its
+# per-layer debug dump (the reporting itself is host-side formatting)
+# ---------------------------------------------------------------------------
+def decode_token(tokenizer, token_id: int) -> str:
+    """GI:284-287."""
+    return "" if tokenizer is None else tokenizer.decode([token_id])
+
+
+def safe_repr(text: str) -> str:
+    """GI:290-291."""
+    return text.encode("unicode_escape").decode("ascii")
+
+
+def top_tokens(logits: np.ndarray, tokenizer, k: int) -> list[tuple[int, float, str]]:
+    """GI:294-299: the k highest logits, highest first."""
+    indices = np.argsort(logits)[-k:][::-1]
+    return [(int(i), float(logits[i]), decode_token(tokenizer, int(i))) for i in indices]
+
+
+def flatten_named_arrays(prefix: str, obj: Any) -> dict[str, np.ndarray]:
+    """GI:302-310: nested debug dicts -> {"a_b_c": array}; non-array leaves
+    are dropped."""
+    flat: dict[str, np.ndarray] = {}
+    if isinstance(obj, dict):
+        for key, value in obj.items():
+            flat.update(flatten_named_arrays(f"{prefix}_{key}" if prefix else key, value))
+    elif isinstance(obj, np.ndarray):
+        flat[prefix] = obj
+    return flat
+
+
+def dump_debug(dump_dir: str, token_ids: list[int], reference_debug: dict[str, Any], mixed_debug: dict[str, Any],
+               summary_lines: list[str]) -> None:
+    """GI:313-327: debug_arrays.npz (token_ids, reference_*, mixed_*) and
+    summary.txt under dump_dir."""
+    os.makedirs(dump_dir, exist_ok=True)
+    arrays = {"token_ids": np.asarray(token_ids, dtype=np.int32)}
+    arrays.update(flatten_named_arrays("reference", reference_debug))
+    arrays.update(flatten_named_arrays("mixed", mixed_debug))
+    np.savez(os.path.join(dump_dir, "debug_arrays.npz"), **arrays)
+    with open(os.path.join(dump_dir, "summary.txt"), "w", encoding="utf-8") as handle:
+        handle.write("\n".join(summary_lines) + "\n")
+
+
+def maybe_load_tokenizer(model_id: str, local_files_only: bool):
+    """GI:330-337: a local tokenizer if one is cached, else None."""
+    try:
+        from transformers import AutoTokenizer
+        return AutoTokenizer.from_pretrained(model_id, local_files_only=local_files_only)
+    except Exception as exc:
+        print(f"Warning: could not load tokenizer for {model_id}: {exc}")
+        return None
+
+
+def projection_stats_line(name: str, ref_array: np.ndarray, mix_array: np.ndarray) -> str:
+    """GI:351-353."""
+    stats = diff_stats(ref_array, mix_array)
+    return f"{name}: mae={stats['mae']:.6f}, max_abs={stats['max_abs']:.6f}"
+
+
+def print_token_context(token_ids: list[int], tokenizer) -> None:
+    """GI:401-405."""
+    print(f"Token ids: {token_ids}")
+    if tokenizer is not None:
+        print(f"Decoded tokens: {[safe_repr(tokenizer.decode([tok])) for tok in token_ids]}")
+    print("")
+
+
+def run_analysis(prompt: str | None, token_ids_arg: str | None, weights_path, layer_count: int,
+                 dump_layer: int | None = None, dump_dir: str | None = None, local_files_only: bool = True,
+                 top_k: int = 5, quantize_lm_head: bool = False, cache_arrays: bool = False,
+                 tokenizer=None) -> dict:
+    """GI:470-626: one pass of the float32 model and of the INT8 path over the
+    prompt, layer by layer (isolated: both from the float32 input; cumulative:
+    the INT8 path from its own previous output), then the final logits of the
+    last position.  With dump_layer, that layer's debug dicts (and the LM
+    head's when quantized) are written by dump_debug to dump_dir.  The INT8
+    layers use the archive's static KV scales when it has them, else scales
+    calibrated on the prompt.  ``weights_path`` may also be a
+    TinyLlamaWeights.  Returns the summary lines and both tokens."""
+    weights = weights_path if isinstance(weights_path, TinyLlamaWeights) else load_weights(
+        weights_path, cache_arrays=cache_arrays)
+    cfg = weights.cfg
+    validate_layer_count(cfg, layer_count)
+    if tokenizer is None and prompt is not None and token_ids_arg is None:
+        tokenizer = maybe_load_tokenizer(cfg["model_id"], local_files_only=local_files_only)
+    token_ids = resolve_token_ids(prompt, token_ids_arg, tokenizer)
+    cos, sin = build_rope_cache(cfg["max_position_embeddings"], cfg["head_dim"], cfg["rope_theta"])
+    if dump_layer is not None and (dump_layer < 0 or dump_layer >= layer_count):
+        raise ValueError("--dump-layer must be within the executed layer range")
+    print_token_context(token_ids, tokenizer)
+
+    x_ref = np.asarray(weights.embed(token_ids), np.float32)
+    x_mix = x_ref.copy()
+    summary_lines = [f"Token ids: {token_ids}", f"Layers analyzed: {layer_count}", "Layer stats:"]
+    dump_reference: dict[str, Any] | None = None
+    dump_mixed: dict[str, Any] | None = None
+    scales = weights.kv_scales()
+    for layer_idx in range(layer_count):
+        layer = weights.layer(layer_idx)
+        capture = dump_layer == layer_idx
+        kv = None if scales is None else (scales[0][layer_idx], scales[1][layer_idx])
+        ref_out, ref_debug = reference_decoder_layer(x_ref, layer, cfg, cos, sin, capture_arrays=capture)
+        iso_mix_out, iso_mix_debug = mixed_precision_decoder_layer(x_ref, layer, cfg, cos, sin,
+                                                                   capture_arrays=capture, kv_scales=kv)
+        cum_mix_out, _ = mixed_precision_decoder_layer(x_mix, layer, cfg, cos, sin, capture_arrays=False,
+                                                       kv_scales=kv)
+        isolated = diff_stats(ref_out, iso_mix_out)
+        cumulative = diff_stats(ref_out, cum_mix_out)
+        line = (f"Layer {layer_idx}: "
+                f"isolated MAE={isolated['mae']:.6f}, isolated max={isolated['max_abs']:.6f}, "
+                f"cumulative MAE={cumulative['mae']:.6f}, cumulative max={cumulative['max_abs']:.6f}")
+        print(line)
+        summary_lines.append(line)
+        if capture:
+            dump_reference, dump_mixed = ref_debug, iso_mix_debug
+            ra, ma, rf, mf = ref_debug["attn"], iso_mix_debug["attn"], ref_debug["ffn"], iso_mix_debug["ffn"]
+            breakdown = [
+                projection_stats_line("  attn q_proj", ra["q_proj_fp"], ma["q_proj_fp"]),
+                projection_stats_line("  attn k_proj", ra["k_proj_fp"], ma["k_proj_fp"]),
+                projection_stats_line("  attn v_proj", ra["v_proj_fp"], ma["v_proj_fp"]),
+                projection_stats_line("  ffn gate_proj", rf["gate_proj_fp"], mf["gate_proj_fp"]),
+                projection_stats_line("  ffn up_proj", rf["up_proj_fp"], mf["up_proj_fp"]),
+            ]
+            if "out_fp" in ra and "out_fp" in ma:
+                breakdown.append(projection_stats_line("  attn o_proj", ra["out_fp"], ma["out_fp"]))
+            if "out_fp" in rf and "out_fp" in mf:
+                breakdown.append(projection_stats_line("  ffn down_proj", rf["out_fp"], mf["out_fp"]))
+            for b in breakdown:
+                print(b)
+                summary_lines.append(b)
+        x_ref, x_mix = ref_out, cum_mix_out
+
+    eps = cfg["rms_norm_eps"]
+    x_ref = TL.rms_norm(x_ref, weights.final_norm_w(), eps)
+    x_mix = TL.rms_norm(x_mix, weights.final_norm_w(), eps)
+    ref_logits = TL.linear(x_ref[-1:], weights.lm_head_w())
+    lm_debug: dict[str, Any] = {}
+    if quantize_lm_head:
+        mix_logits, lm_debug = quantized_linear(x_mix[-1:], weights.lm_head_w(), None,
+                                                capture_arrays=dump_dir is not None)
+    else:
+        mix_logits = TL.linear(x_mix[-1:], weights.lm_head_w())
+    logit_stats = diff_stats(ref_logits, mix_logits)
+    ref_token = int(np.argmax(ref_logits[0]))
+    mix_token = int(np.argmax(mix_logits[0]))
+
+    print("")
+    print(f"Final logits: MAE={logit_stats['mae']:.6f}, "
+          f"RMSE={logit_stats['rmse']:.6f}, max_abs={logit_stats['max_abs']:.6f}")
+    print(f"Float32 next token: {ref_token} -> '{safe_repr(decode_token(tokenizer, ref_token))}'")
+    print(f"INT8 path next token: {mix_token} -> '{safe_repr(decode_token(tokenizer, mix_token))}'")
+    print("")
+    print(f"Top {top_k} float32 tokens:")
+    for idx, value, decoded in top_tokens(ref_logits[0], tokenizer, top_k):
+        print(f"  {idx:6d}  {value:12.6f}  '{safe_repr(decoded)}'")
+    print("")
+    print(f"Top {top_k} INT8-path tokens:")
+    for idx, value, decoded in top_tokens(mix_logits[0], tokenizer, top_k):
+        print(f"  {idx:6d}  {value:12.6f}  '{safe_repr(decoded)}'")
+    summary_lines.extend([
+        "",
+        f"Final logits: mae={logit_stats['mae']:.6f}, rmse={logit_stats['rmse']:.6f}, "
+        f"max_abs={logit_stats['max_abs']:.6f}",
+        f"Float32 next token: {ref_token} -> '{safe_repr(decode_token(tokenizer, ref_token))}'",
+        f"INT8 path next token: {mix_token} -> '{safe_repr(decode_token(tokenizer, mix_token))}'",
+    ])
+    if dump_dir is not None:
+        arrays_mix = dict(dump_mixed or {})
+        if quantize_lm_head and lm_debug:
+            arrays_mix["lm_head"] = lm_debug
+        dump_debug(dump_dir, token_ids, dump_reference or {}, arrays_mix, summary_lines)
+        print("")
+        print(f"Saved debug dump to {dump_dir}")
+    return {"summary_lines": summary_lines, "ref_token": ref_token, "mix_token": mix_token,
+            "ref_logits": ref_logits, "mix_logits": mix_logits}
+
+
+def main(argv: list[str] | None = None) -> None:
+    """GI:688-745: --mode analysis | generate."""
+    import argparse
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--mode", choices=["analysis", "generate"], default="analysis",
+                        help="analysis = one-pass float32 vs INT8 comparison, generate = autoregressive INT8-path "
+                             "generation")
+    parser.add_argument("--prompt", type=str, default=None)
+    parser.add_argument("--token-ids", type=str, default=None)
+    parser.add_argument("--weights", type=str, required=True)
+    parser.add_argument("--layers", type=int, default=1)
+    parser.add_argument("--max-tokens", type=int, default=20)
+    parser.add_argument("--dump-layer", type=int, default=None)
+    parser.add_argument("--dump-dir", type=str, default=None)
+    parser.add_argument("--top-k", type=int, default=5)
+    parser.add_argument("--local-files-only", action="store_true")
+    parser.add_argument("--cache-arrays", action="store_true")
+    parser.add_argument("--quantize-lm-head", action="store_true",
+                        help="Also quantize the final vocab projection (always on in --mode generate).")
+    args = parser.parse_args(argv)
+    if not os.path.exists(args.weights):
+        raise FileNotFoundError(f"Weights not found at {args.weights}. Run model/tinyllama.py --save-weights first.")
+    if args.mode == "generate":
+        if args.dump_layer is not None or args.dump_dir is not None:
+            raise ValueError("--dump-layer and --dump-dir are only supported in --mode analysis")
+        tok = maybe_load_tokenizer(load_weights(args.weights).cfg["model_id"], args.local_files_only) \
+            if args.prompt is not None and args.token_ids is None else None
+        run_generate(args.prompt, args.token_ids, args.weights, args.layers, args.max_tokens,
+                     local_files_only=args.local_files_only, quantize_lm_head=True, cache_arrays=args.cache_arrays,
+                     tokenizer=tok)
+        return
+    run_analysis(args.prompt, args.token_ids, args.weights, args.layers, dump_layer=args.dump_layer,
+                 dump_dir=args.dump_dir, local_files_only=args.local_files_only, top_k=args.top_k,
+                 quantize_lm_head=args.quantize_lm_head, cache_arrays=args.cache_arrays)
+
