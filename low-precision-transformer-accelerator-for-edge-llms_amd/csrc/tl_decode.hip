@@ -554,8 +554,7 @@ __global__ __launch_bounds__(256) void attention_row_kernel(AttnDecodeArgs p) {
         if (lane == 0) bsum[b] = bs;
     }
     __syncthreads();
-    float tot = 0.0f;
-    for (int b = 0; b < nblk; b++) tot = tot + bsum[b];
+    const float tot = ordered_sum(bsum, nblk);
 
     // 5) INT8 probabilities of this wavefront's keys, then P . V over the
     //    same keys (lane <-> dimension; this row's V is v8 of lane d)
@@ -609,6 +608,231 @@ __global__ __launch_bounds__(256) void attention_row_kernel(AttnDecodeArgs p) {
         const int O = accs[0][tid] + accs[1][tid] + accs[2][tid] + accs[3][tid];
         p.out[(int64_t)row * D + (int64_t)h0 * kHeadDim + tid] = (float)O * deq_mult(1.0 / 127.0, sv);
     }
+}
+
+// Batched decode attention (many rows, long contexts): one workgroup of 16
+// wavefronts per (row, group of HPW query heads sharing a KV head).  Every
+// wavefront issues all of its key and value loads first (T <= 2048: two
+// 64-key blocks and eight 16-key value groups per wavefront), so each phase
+// costs about one memory latency, and the HPW heads share every loaded key
+// and value.  Same arithmetic as attention_row_kernel.
+constexpr int kGW = 16;                         // wavefronts
+constexpr int kGKB = 2;                         // key blocks per wavefront
+constexpr int kGVG = 8;                         // value groups per wavefront
+constexpr int kGroupMaxKeys = kGW * kGKB * 64;  // 2048
+
+template <int HPW>
+__global__ __launch_bounds__(kGW * 64) void attention_group_kernel(AttnDecodeArgs p) {
+    extern __shared__ __align__(16) float gdyn[];
+    __shared__ __align__(16) int8_t qs[HPW][64];
+    __shared__ __align__(16) int8_t kn[64];
+    __shared__ int8_t vn[64];
+    __shared__ float red[kGW];
+    __shared__ float wmax[kGW][HPW];
+    __shared__ float mh[HPW], toth[HPW];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int G = p.n_heads / p.n_kv;
+    const int h0 = blockIdx.x * HPW, g = h0 / G, row = blockIdx.y;
+    const int D = p.n_heads * kHeadDim, KVD = p.n_kv * kHeadDim, W = D + 2 * KVD;
+    const int pos = p.rm.pos[row], seq = p.rm.seq[row];
+    const int T = pos + 1, tpad = (T + 63) & ~63, nblk = tpad >> 6, ngrp = tpad >> 4;
+    const int64_t pl = p.kv.plane(seq, p.layer, g);
+    const int8_t* kp = p.kv.k + pl;
+    const int8_t* vp = p.kv.v + pl;
+    float* s_buf = gdyn;                                  // [HPW][tpad]
+    int8_t* p8 = (int8_t*)(gdyn + HPW * tpad);            // [HPW][tpad]
+    float* bsum = (float*)(p8 + HPW * tpad);              // [HPW][nblk]
+    int* accs = (int*)(bsum + HPW * nblk);                // [kGW][HPW][64]
+    const float* src = p.qkv + (int64_t)row * W;
+    const int d = lane;
+
+    // 0) loads in the order they are needed (loads complete in issue order):
+    //    the Q row, this group's Q heads and the row's own K and V, the RoPE
+    //    factors, then this wavefront's cached key blocks and value groups
+    //    (indices clamped inside the plane; rows 0..pos-1 are final, surplus
+    //    copies unused)
+    constexpr int kQPer = 4;   // Q elements per thread: D <= 4 x 1024
+    float qv[kQPer];
+#pragma unroll
+    for (int j = 0; j < kQPer; j++) qv[j] = src[min(tid + kGW * 64 * j, D - 1)];
+    float qh = 0.0f, kx = 0.0f, vx = 0.0f;
+    if (wave < HPW) qh = src[(h0 + wave) * kHeadDim + d];
+    if (wave == HPW) {
+        kx = src[D + g * kHeadDim + d];
+        vx = src[D + KVD + g * kHeadDim + d];
+    }
+    const float cs = p.cosb[(int64_t)pos * kHeadDim + d];
+    const float sn = p.sinb[(int64_t)pos * kHeadDim + d];
+    v4i kreg[kGKB][4], vreg[kGVG];
+#pragma unroll
+    for (int i = 0; i < kGKB; i++) {
+        const int b = min(wave + kGW * i, nblk - 1);
+#pragma unroll
+        for (int q = 0; q < 4; q++) kreg[i][q] = ld16(kp + (int64_t)b * 4096 + q * 1024 + lane * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < kGVG; i++) vreg[i] = ld16(vp + (int64_t)min(wave + kGW * i, ngrp - 1) * 1024 + lane * 16);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 1) RoPE of every Q element of the row -> the row's scale; this group's
+    //    rotated Q and the row's K (RoPE, static scale) and V
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kQPer; j++) {
+        const float o = __shfl_xor(qv[j], 32);
+        if (tid + kGW * 64 * j < D) mx = fmaxf(mx, fabsf((qv[j] * cs) + ((d < 32 ? -o : o) * sn)));
+    }
+    mx = wave_max_f32(mx);
+    if (lane == 0) red[wave] = mx;
+    const float sk = p.kv_sk[p.layer * p.n_kv + g], sv = p.kv_sv[p.layer * p.n_kv + g];
+    __syncthreads();
+    mx = red[0];
+#pragma unroll
+    for (int w = 1; w < kGW; w++) mx = fmaxf(mx, red[w]);
+    const double s_q = quant_scale(mx);
+    if (wave < HPW) {
+        const float qo = __shfl_xor(qh, 32);
+        const float qr = (qh * cs) + ((d < 32 ? -qo : qo) * sn);
+        qs[wave][d] = sat_i8(__builtin_rintf(__fdiv_rn(qr, (float)s_q)));
+    } else if (wave == HPW) {
+        const float ko = __shfl_xor(kx, 32);
+        const float kr = (kx * cs) + ((d < 32 ? -ko : ko) * sn);
+        const int8_t k8 = sat_i8(__builtin_rintf(__fdiv_rn(kr, sk)));
+        const int8_t v8 = sat_i8(__builtin_rintf(__fdiv_rn(vx, sv)));
+        kn[d] = k8;
+        vn[d] = v8;
+        if (h0 % G == 0) {   // the first head group of the KV head appends the row
+            p.kv.k[pl + KvGeom::k_off(pos, d)] = k8;
+            p.kv.v[pl + KvGeom::v_off(pos, d)] = v8;
+        }
+    }
+    const float scl = (float)((s_q * (double)sk) * p.attn_scale);
+    __syncthreads();
+
+    // 2) scores (lane <-> key) of this wavefront's blocks for the HPW heads
+    float lmax[HPW];
+#pragma unroll
+    for (int h = 0; h < HPW; h++) lmax[h] = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kGKB; i++) {
+        const int b = wave + kGW * i;
+        const int t = b * 64 + lane;
+        if (b < nblk && t < T) {
+            v4i k0 = kreg[i][0], k1 = kreg[i][1], k2 = kreg[i][2], k3 = kreg[i][3];
+            if (t == pos) {
+                const v4i* kn4 = (const v4i*)kn;
+                k0 = kn4[0];
+                k1 = kn4[1];
+                k2 = kn4[2];
+                k3 = kn4[3];
+            }
+#pragma unroll
+            for (int h = 0; h < HPW; h++) {
+                const v4i* q4 = (const v4i*)qs[h];
+                int S = sdot4v(k0, q4[0], 0);
+                S = sdot4v(k1, q4[1], S);
+                S = sdot4v(k2, q4[2], S);
+                S = sdot4v(k3, q4[3], S);
+                const float sc = (float)S * scl;
+                s_buf[h * tpad + t] = sc;
+                lmax[h] = fmaxf(lmax[h], sc);
+            }
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < HPW; h++) {
+        const float m = wave_max_f32(lmax[h]);
+        if (lane == 0) wmax[wave][h] = m;
+    }
+    __syncthreads();
+    if (tid < HPW) {
+        float m = wmax[0][tid];
+        for (int w = 1; w < kGW; w++) m = fmaxf(m, wmax[w][tid]);
+        mh[tid] = m;
+    }
+    __syncthreads();
+
+    // 3) exponentials and block-64 butterfly sums, then each head's total
+    //    (block sums added in key order)
+#pragma unroll
+    for (int i = 0; i < kGKB; i++) {
+        const int b = wave + kGW * i;
+        if (b < nblk) {
+            const int t = b * 64 + lane;
+#pragma unroll
+            for (int h = 0; h < HPW; h++) {
+                float e = 0.0f;
+                if (t < T) {
+                    e = tl_expf(s_buf[h * tpad + t] - mh[h]);
+                    s_buf[h * tpad + t] = e;
+                }
+                const float bs = wave_butterfly_sum(e);
+                if (lane == 0) bsum[h * nblk + b] = bs;
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < HPW) {
+        toth[tid] = ordered_sum(bsum + tid * nblk, nblk);
+    }
+    __syncthreads();
+
+    // 4) INT8 probabilities (zero past the last key)
+#pragma unroll
+    for (int i = 0; i < kGKB; i++) {
+        const int b = wave + kGW * i;
+        if (b < nblk) {
+            const int t = b * 64 + lane;
+#pragma unroll
+            for (int h = 0; h < HPW; h++) {
+                int8_t pq = 0;
+                if (t < T) {
+                    float pr = __builtin_rintf(__fdiv_rn(s_buf[h * tpad + t], toth[h]) * 127.0f);
+                    pr = pr < 0.0f ? 0.0f : (pr > 127.0f ? 127.0f : pr);
+                    pq = (int8_t)(int)pr;
+                }
+                p8[h * tpad + t] = pq;
+            }
+        }
+    }
+    __syncthreads();
+
+    // 5) P . V (lane <-> dimension) over this wavefront's value groups; the
+    //    row's own V comes from vn
+    int o[HPW];
+#pragma unroll
+    for (int h = 0; h < HPW; h++) o[h] = 0;
+    const int cpos = pos >> 4, bpos = pos & 15;
+#pragma unroll
+    for (int i = 0; i < kGVG; i++) {
+        const int c = wave + kGW * i;
+        if (c < ngrp) {
+            v4i vv = vreg[i];
+            if (c == cpos) {
+                const unsigned nb = (uint8_t)vn[d];
+                const int sh = (bpos & 3) * 8;
+                const unsigned keep = ~(0xFFu << sh);
+                const int q = bpos >> 2;
+                vv[q] = (int)(((unsigned)vv[q] & keep) | (nb << sh));
+            }
+#pragma unroll
+            for (int h = 0; h < HPW; h++) o[h] = sdot4v(vv, *(const v4i*)(p8 + h * tpad + c * 16), o[h]);
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < HPW; h++) accs[(wave * HPW + h) * 64 + lane] = o[h];
+    __syncthreads();
+    if (tid < HPW * 64) {
+        const int h = tid >> 6, dd = tid & 63;
+        int O = 0;
+        for (int w = 0; w < kGW; w++) O += accs[(w * HPW + h) * 64 + dd];
+        p.out[(int64_t)row * D + (int64_t)(h0 + h) * kHeadDim + dd] = (float)O * deq_mult(1.0 / 127.0, sv);
+    }
+}
+
+static size_t group_lds_bytes(int hpw, int tpad) {
+    return (size_t)hpw * tpad * 5 + (size_t)hpw * (tpad / 64) * 4 + (size_t)kGW * hpw * 64 * 4 + 16;
 }
 
 // embedding of each row's current token and the row's position (= its
@@ -682,15 +906,20 @@ hipError_t launch_attention_decode(hipStream_t s, const float* qkv, int32_t rows
     const int D = n_heads * kHeadDim, W = D + 2 * n_kv * kHeadDim;
     const int tpad = (max_t + 63) & ~63;
     AttnDecodeArgs p{qkv, n_heads, n_kv, rm, cos, sin, kv, layer, kv_sk, kv_sv, 1.0 / sqrt((double)kHeadDim), out};
-    if (hpw == 1 && n_heads % 4 == 0 && D <= kRowQPerThread * kNT) {
+    if (rows > 1 && G % 4 == 0 && max_t <= kGroupMaxKeys && D <= 4 * kGW * 64 && (hpw == 1 || (hpw == 8 && G == 8))) {
+        // many rows: the grouped kernel, 4 (or 8) query heads per workgroup
+        if (hpw == 8)
+            TL_KLAUNCH((attention_group_kernel<8>), dim3(n_heads / 8, rows), dim3(kGW * 64), group_lds_bytes(8, tpad),
+                       s, p);
+        else
+            TL_KLAUNCH((attention_group_kernel<4>), dim3(n_heads / 4, rows), dim3(kGW * 64), group_lds_bytes(4, tpad),
+                       s, p);
+    } else if (hpw == 1 && n_heads % 4 == 0 && D <= kRowQPerThread * kNT) {
         const size_t lds = (size_t)tpad * 5 + (tpad / 64) * 4 + 16;
         TL_KLAUNCH((attention_row_kernel<2>), dim3(n_heads, rows), dim3(256), lds, s, p);
     } else if (hpw == 1) {
         const size_t lds = sizeof(float) * W + (size_t)tpad * 4 + tpad + (tpad / 64) * 4 + 64;
         TL_KLAUNCH((attention_decode_kernel<1, 2, 8, 4>), dim3(n_heads, rows), dim3(256), lds, s, p);
-    } else if (hpw == 8 && G == 8) {
-        const size_t lds = sizeof(float) * W + (size_t)8 * tpad * 4 + 8 * tpad + 8 * (tpad / 64) * 4 + 64;
-        TL_KLAUNCH((attention_decode_kernel<8, 2, 4, 8>), dim3(n_heads / 8, rows), dim3(512), lds, s, p);
     } else {
         return hipErrorInvalidValue;
     }
@@ -707,11 +936,15 @@ hipError_t launch_embed_step(hipStream_t s, const int32_t* tok_by_seq, const int
 }
 
 hipError_t init_decode_kernels() {
-    hipError_t e = hipFuncSetAttribute((const void*)attention_decode_kernel<8, 2, 4, 8>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, 120 * 1024);
+    hipError_t e = hipFuncSetAttribute((const void*)attention_group_kernel<8>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)group_lds_bytes(8, kGroupMaxKeys));
     if (e != hipSuccess) return e;
     e = hipFuncSetAttribute((const void*)attention_row_kernel<2>, hipFuncAttributeMaxDynamicSharedMemorySize,
                             120 * 1024);
+    if (e != hipSuccess) return e;
+    e = hipFuncSetAttribute((const void*)attention_group_kernel<4>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)group_lds_bytes(4, kGroupMaxKeys));
     if (e != hipSuccess) return e;
     return hipFuncSetAttribute((const void*)attention_decode_kernel<1, 2, 8, 4>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);

@@ -155,6 +155,24 @@ TL_DEV int sdot4x4(int4 a, int4 b, int acc) {
     return acc;
 }
 
+// v[0] + v[1] + ... + v[n-1] added in index order, starting from 0 (the
+// softmax denominator over block sums); up to 32 values are read before the
+// first add, so the chain costs one LDS latency instead of n
+TL_DEV float ordered_sum(const float* v, int n) {
+    float t = 0.0f;
+    if (n <= 32) {
+        float r[32];
+#pragma unroll
+        for (int i = 0; i < 32; i++) r[i] = v[i < n ? i : 0];
+#pragma unroll
+        for (int i = 0; i < 32; i++)
+            if (i < n) t = t + r[i];
+        return t;
+    }
+    for (int i = 0; i < n; i++) t = t + v[i];
+    return t;
+}
+
 // block-wide max of a non-negative float (all threads get the result)
 TL_DEV float block_max(float v, float* red /* >= 16 floats */) {
     v = wave_max_f32(v);

@@ -100,6 +100,9 @@ struct GemmArgs {
     int32_t* acc;             // [M][N] raw (EPI_RAW) or [splits][M][N] partials
     int32_t m, n, k;
     int32_t k_split;          // K elements per split (multiple of 64)
+    const int8_t* wp;         // packed copy of w (MFMA operand blocks, pack_weights_kernel) or null
+    const int8_t* wp2;        // packed copy of w2
+    unsigned long long* key;  // EPI_ARGMAX: [N / 32 tiles][M] best key of each tile and row
 };
 
 // ---- launchers (tl_kernels.hip) ------------------------------------------
@@ -116,6 +119,8 @@ hipError_t launch_gemv(hipStream_t s, int epi, const GemvArgs& a);
 constexpr int kSkinnyTiles = 4096;     // output tiles of 32 columns the split small-M GEMM counts
 constexpr int kSkinnyMaxSlices = 8;   // K slices of the small-M GEMM (LDS holds the other 7 partial tiles)
 hipError_t launch_gemm_rows32(hipStream_t s, int epi, const GemmArgs& a);
+hipError_t launch_pack_weights(hipStream_t s, const int8_t* w, int32_t n, int32_t k, int8_t* wp);
+
 hipError_t launch_gemm_skinny(hipStream_t s, int epi, const GemmArgs& a, int32_t slices, int32_t* part,
                               unsigned* counters);
 hipError_t launch_gemm(hipStream_t s, int epi, const GemmArgs& a, int32_t splits);
@@ -162,6 +167,8 @@ hipError_t launch_finalize_tokens(hipStream_t s, unsigned long long* keys, int32
                                   int32_t* n_gen, int32_t* cursor, float* best_logit, int32_t advance);
 hipError_t launch_argmax_rows(hipStream_t s, const float* logits, int32_t rows, int32_t n,
                               unsigned long long* keys);
+hipError_t launch_argmax_tiles(hipStream_t s, const unsigned long long* part, int32_t tiles, int32_t rows,
+                               unsigned long long* keys);
 hipError_t init_kernels();
 hipError_t init_decode_kernels();
 hipError_t init_prefill_kernels();

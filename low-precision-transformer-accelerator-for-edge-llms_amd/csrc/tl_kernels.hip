@@ -721,8 +721,7 @@ __global__ __launch_bounds__(256) void attention_kernel(const int8_t* __restrict
     }
     __syncthreads();
     if (tid < G) {
-        float total = 0.0f;
-        for (int b = 0; b < nblk; b++) total = total + bsum[tid * nblk + b];
+        const float total = ordered_sum(bsum + tid * nblk, nblk);
         tot[tid] = total;
     }
     __syncthreads();
@@ -888,8 +887,7 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(AttnTileArgs p) {
     }
     __syncthreads();
     if (tid < 32) {
-        float total = 0.0f;
-        for (int b = 0; b < nblk; b++) total = total + bsum[tid * nblk + b];
+        const float total = ordered_sum(bsum + tid * nblk, nblk);
         tot[tid] = total;
     }
     __syncthreads();
@@ -994,8 +992,7 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(const float* __restri
     }
     __syncthreads();
     if (tid == 0) {
-        float total = 0.0f;
-        for (int b = 0; b < nblk; b++) total = total + bs[b];
+        const float total = ordered_sum(bs, nblk);
         mtot[1] = total;
     }
     __syncthreads();
@@ -1072,9 +1069,19 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const float* __restric
     const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float* lr = logits + (int64_t)row * n;
     unsigned long long best = 0;
-    for (int i = tid; i < n; i += blockDim.x) {
-        const unsigned long long k = argmax_key(lr[i], i);
-        best = k > best ? k : best;
+    // eight loads in flight per thread (the max of the keys is order-free)
+    for (int i0 = tid; i0 < n; i0 += 8 * blockDim.x) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = lr[min(i0 + j * (int)blockDim.x, n - 1)];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int i = i0 + j * (int)blockDim.x;
+            if (i < n) {
+                const unsigned long long k = argmax_key(v[j], i);
+                best = k > best ? k : best;
+            }
+        }
     }
     best = wave_max_u64(best);
     if (lane == 0) wbest[wave] = best;
@@ -1084,6 +1091,41 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const float* __restric
         for (int i = 1; i < 4; i++) b = wbest[i] > b ? wbest[i] : b;
         keys[row] = b;
     }
+}
+
+// the best of the per-tile keys [tiles][rows] of each row (one workgroup per
+// row; the max of the keys is order-free)
+__global__ __launch_bounds__(256) void argmax_tiles_kernel(const unsigned long long* __restrict__ part, int32_t tiles,
+                                                           int32_t rows, unsigned long long* __restrict__ keys) {
+    __shared__ unsigned long long wbest[4];
+    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    unsigned long long best = 0;
+    for (int t0 = tid; t0 < tiles; t0 += 8 * blockDim.x) {
+        unsigned long long v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int t = t0 + j * (int)blockDim.x;
+            v[j] = part[(int64_t)min(t, tiles - 1) * rows + row];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (t0 + j * (int)blockDim.x < tiles) best = v[j] > best ? v[j] : best;
+    }
+    best = wave_max_u64(best);
+    if (lane == 0) wbest[wave] = best;
+    __syncthreads();
+    if (tid == 0) {
+        unsigned long long b = wbest[0];
+        for (int i = 1; i < 4; i++) b = wbest[i] > b ? wbest[i] : b;
+        keys[row] = b;
+    }
+}
+
+hipError_t launch_argmax_tiles(hipStream_t s, const unsigned long long* part, int32_t tiles, int32_t rows,
+                               unsigned long long* keys) {
+    if (rows <= 0 || tiles <= 0) return hipErrorInvalidValue;
+    TL_KLAUNCH(argmax_tiles_kernel, dim3(rows), dim3(256), 0, s, part, tiles, rows, keys);
+    return hipGetLastError();
 }
 
 // batched decode: the position of each row is its sequence's cursor
@@ -1244,7 +1286,11 @@ hipError_t launch_gemm(hipStream_t s, int epi, const GemmArgs& a, int32_t splits
 constexpr int kRowsWaves = 16;
 constexpr int kRowsChunks = 12;   // most 32-byte K chunks per wavefront (K <= 16 x 12 x 32 = 6144)
 
-template <int EPI, int CH>
+// PK: the weights are read from their packed copy (a.wp / a.wp2, MFMA
+// operand order, one contiguous 1 KiB block per 32 rows x 32 K bytes), so
+// every weight load of a wavefront is one coalesced 1 KiB read; otherwise from
+// the row-major [N][K] matrix (32 rows x 32 bytes per load).
+template <int EPI, int CH, bool PK>
 __global__ __launch_bounds__(1024) void gemm_rows32_kernel(GemmArgs a) {
     constexpr int NB = EPI == EPI_GLU ? 2 : 1;
     extern __shared__ __align__(16) int rows32_lds[];   // [16 waves][NB][16][64]
@@ -1253,8 +1299,14 @@ __global__ __launch_bounds__(1024) void gemm_rows32_kernel(GemmArgs a) {
     const int kch = a.k >> 5;
     const int8_t* arow = a.a + (int64_t)min(col, a.m - 1) * a.k + hi * 16;
     const int8_t* wrow[NB];
-    wrow[0] = a.w + (int64_t)min(n0 + col, a.n - 1) * a.k + hi * 16;
-    if (NB == 2) wrow[NB - 1] = a.w2 + (int64_t)min(n0 + col, a.n - 1) * a.k + hi * 16;
+    if (PK) {
+        wrow[0] = a.wp + (int64_t)blockIdx.x * kch * 1024 + lane * 16;
+        if (NB == 2) wrow[NB - 1] = a.wp2 + (int64_t)blockIdx.x * kch * 1024 + lane * 16;
+    } else {
+        wrow[0] = a.w + (int64_t)min(n0 + col, a.n - 1) * a.k + hi * 16;
+        if (NB == 2) wrow[NB - 1] = a.w2 + (int64_t)min(n0 + col, a.n - 1) * a.k + hi * 16;
+    }
+    const int64_t wstep = PK ? 1024 : 32;   // bytes between consecutive K chunks
     const int per = (kch + kRowsWaves - 1) / kRowsWaves;   // consecutive chunks of this wavefront: 4 loads cover a 128-byte line
     v4i af[CH], bf[NB][CH];
 #pragma unroll
@@ -1262,7 +1314,7 @@ __global__ __launch_bounds__(1024) void gemm_rows32_kernel(GemmArgs a) {
         const int cc = min(wave * per + min(j, per - 1), kch - 1);
         af[j] = ld16(arow + (int64_t)cc * 32);
 #pragma unroll
-        for (int b = 0; b < NB; b++) bf[b][j] = ld_nt16(wrow[b] + (int64_t)cc * 32);
+        for (int b = 0; b < NB; b++) bf[b][j] = ld_nt16(wrow[b] + (int64_t)cc * wstep);
     }
     v16i acc[NB];
 #pragma unroll
@@ -1280,6 +1332,29 @@ __global__ __launch_bounds__(1024) void gemm_rows32_kernel(GemmArgs a) {
     // thread t finishes element (register i, lane l) of the 32 x 32 tile
     const int l = tid & 63, i = tid >> 6;
     const int m = 8 * (i >> 2) + 4 * (l >> 5) + (i & 3), n = n0 + (l & 31);
+    if (EPI == EPI_ARGMAX) {
+        // dequantized logit -> 64-bit key; the 32 columns of row m are the 32
+        // lanes of this half-wavefront, whose best key is this tile's key of
+        // row m (argmax_tiles_kernel folds the tiles)
+        unsigned long long k = 0;
+        if (m < a.m && n < a.n) {
+            int v = 0;
+#pragma unroll
+            for (int w = 0; w < kRowsWaves; w++) v += rows32_lds[(w * 16 + i) * 64 + l];
+            const float lg = (float)v * deq_mult(a.as[m], a.ws[n]);
+            if (a.y) a.y[(int64_t)m * a.n + n] = lg;
+            k = argmax_key(lg, n);
+        }
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) {
+            const unsigned lo = __shfl_xor((unsigned)(k & 0xFFFFFFFFull), off);
+            const unsigned hi2 = __shfl_xor((unsigned)(k >> 32), off);
+            const unsigned long long o = ((unsigned long long)hi2 << 32) | lo;
+            k = o > k ? o : k;
+        }
+        if ((l & 31) == 0 && m < a.m) a.key[(int64_t)blockIdx.x * a.m + m] = k;
+        return;
+    }
     if (m >= a.m || n >= a.n) return;
     int sum[NB];
 #pragma unroll
@@ -1308,29 +1383,67 @@ __global__ __launch_bounds__(1024) void gemm_rows32_kernel(GemmArgs a) {
 
 static size_t rows32_lds_bytes(int nb) { return (size_t)kRowsWaves * nb * 16 * 64 * sizeof(int); }
 
-// M <= 32, K a multiple of 64 and at most 6144
+// M <= 32, K a multiple of 64 and at most 6144; with packed weights (a.wp,
+// and a.wp2 for the GLU) N must be a multiple of 32
 hipError_t launch_gemm_rows32(hipStream_t s, int epi, const GemmArgs& a) {
     if (a.m < 1 || a.m > 32 || a.n <= 0 || a.k <= 0 || a.k % 64 || a.k > kRowsWaves * kRowsChunks * 32)
         return hipErrorInvalidValue;
+    const bool pk = a.wp != nullptr;
+    if (pk && (a.n % 32 || (epi == EPI_GLU && !a.wp2))) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((a.n + 31) / 32)), block(1024);
     const size_t lds1 = rows32_lds_bytes(1), lds2 = rows32_lds_bytes(2);
     const bool shortk = a.k <= kRowsWaves * 4 * 32;
+#define TL_R32P(E, C, L)                                                                    \
+    do {                                                                                    \
+        if (pk) TL_KLAUNCH((gemm_rows32_kernel<E, C, true>), grid, block, L, s, a);         \
+        else TL_KLAUNCH((gemm_rows32_kernel<E, C, false>), grid, block, L, s, a);           \
+    } while (0)
 #define TL_R32(E, L)                                                                        \
     do {                                                                                    \
-        if (shortk) TL_KLAUNCH((gemm_rows32_kernel<E, 4>), grid, block, L, s, a);           \
-        else TL_KLAUNCH((gemm_rows32_kernel<E, kRowsChunks>), grid, block, L, s, a);        \
+        if (shortk) TL_R32P(E, 4, L);                                                       \
+        else TL_R32P(E, kRowsChunks, L);                                                    \
     } while (0)
     switch (epi) {
         case EPI_DEQUANT: TL_R32(EPI_DEQUANT, lds1); break;
         case EPI_DEQUANT_RES: TL_R32(EPI_DEQUANT_RES, lds1); break;
         case EPI_GLU:
             if (!shortk) return hipErrorInvalidValue;   // both weight sets of 12 chunks exceed the registers
-            TL_KLAUNCH((gemm_rows32_kernel<EPI_GLU, 4>), grid, block, lds2, s, a);
+            TL_R32P(EPI_GLU, 4, lds2);
             break;
         case EPI_RAW: TL_R32(EPI_RAW, lds1); break;
+        case EPI_ARGMAX:
+            if (!a.key || !shortk) return hipErrorInvalidValue;
+            TL_R32P(EPI_ARGMAX, 4, lds1);
+            break;
         default: return hipErrorInvalidValue;
     }
 #undef TL_R32
+#undef TL_R32P
+    return hipGetLastError();
+}
+
+// packed copy of an int8 [N][K] matrix (N, K multiples of 32): block
+// (n / 32, k / 32) of 1 KiB at ((n / 32) (K / 32) + k / 32) * 1024, byte
+// (((k / 16) % 2) * 32 + n % 32) * 16 + k % 16 -- lane l of an MFMA B operand
+// (row l % 32, K bytes 16 (l / 32) .. +16) reads bytes 16 l .. 16 l + 15
+__global__ __launch_bounds__(256) void pack_weights_kernel(const int8_t* __restrict__ w, int32_t n, int32_t k,
+                                                           int8_t* __restrict__ wp) {
+    const int64_t units = (int64_t)n * k / 16;
+    const int kch = k >> 5;
+    for (int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; u < units; u += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t blk = u >> 6;
+        const int l = (int)(u & 63);
+        const int64_t nb = blk / kch, kc = blk % kch;
+        const int8_t* src = w + (nb * 32 + (l & 31)) * (int64_t)k + kc * 32 + (l >> 5) * 16;
+        *(v4i*)(wp + u * 16) = *(const v4i*)src;
+    }
+}
+
+hipError_t launch_pack_weights(hipStream_t s, const int8_t* w, int32_t n, int32_t k, int8_t* wp) {
+    if (n <= 0 || k <= 0 || n % 32 || k % 32) return hipErrorInvalidValue;
+    const int64_t units = (int64_t)n * k / 16;
+    const int blocks = (int)std::min<int64_t>(8192, (units + 255) / 256);
+    TL_KLAUNCH(pack_weights_kernel, dim3(blocks), dim3(256), 0, s, w, n, k, wp);
     return hipGetLastError();
 }
 
@@ -1344,12 +1457,18 @@ hipError_t init_skinny_kernels() {
                           (const void*)gemm_skinny_kernel<EPI_GLU>, (const void*)gemm_skinny_kernel<EPI_RAW>};
     for (int i = 0; i < 4 && e == hipSuccess; i++)
         e = hipFuncSetAttribute(fns[i], hipFuncAttributeMaxDynamicSharedMemorySize, (int)skinny_lds_bytes(i == 2 ? 2 : 1));
-    const void* rfns[7] = {(const void*)gemm_rows32_kernel<EPI_DEQUANT, 4>, (const void*)gemm_rows32_kernel<EPI_DEQUANT_RES, 4>,
-                           (const void*)gemm_rows32_kernel<EPI_RAW, 4>, (const void*)gemm_rows32_kernel<EPI_DEQUANT, kRowsChunks>,
-                           (const void*)gemm_rows32_kernel<EPI_DEQUANT_RES, kRowsChunks>,
-                           (const void*)gemm_rows32_kernel<EPI_RAW, kRowsChunks>, (const void*)gemm_rows32_kernel<EPI_GLU, 4>};
-    for (int i = 0; i < 7 && e == hipSuccess; i++)
-        e = hipFuncSetAttribute(rfns[i], hipFuncAttributeMaxDynamicSharedMemorySize, (int)rows32_lds_bytes(i == 6 ? 2 : 1));
+#define TL_R32FNS(PK)                                                                                    \
+    {(const void*)gemm_rows32_kernel<EPI_DEQUANT, 4, PK>, (const void*)gemm_rows32_kernel<EPI_DEQUANT_RES, 4, PK>, \
+     (const void*)gemm_rows32_kernel<EPI_RAW, 4, PK>, (const void*)gemm_rows32_kernel<EPI_DEQUANT, kRowsChunks, PK>, \
+     (const void*)gemm_rows32_kernel<EPI_DEQUANT_RES, kRowsChunks, PK>,                                  \
+     (const void*)gemm_rows32_kernel<EPI_RAW, kRowsChunks, PK>, (const void*)gemm_rows32_kernel<EPI_GLU, 4, PK>, \
+     (const void*)gemm_rows32_kernel<EPI_ARGMAX, 4, PK>}
+    const void* rfns[2][8] = {TL_R32FNS(false), TL_R32FNS(true)};
+#undef TL_R32FNS
+    for (int p = 0; p < 2; p++)
+        for (int i = 0; i < 8 && e == hipSuccess; i++)
+            e = hipFuncSetAttribute(rfns[p][i], hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)rows32_lds_bytes(i == 6 ? 2 : 1));
     return e;
 }
 
@@ -1517,8 +1636,7 @@ __global__ __launch_bounds__(256) void attention_tile_reg_kernel(AttnTileArgs p)
     }
     __syncthreads();
     if (tid < 32) {
-        float total = 0.0f;
-        for (int b = 0; b < nblk; b++) total = total + bsum[tid * nblk + b];
+        const float total = ordered_sum(bsum + tid * nblk, nblk);
         tot[tid] = total;
     }
     __syncthreads();

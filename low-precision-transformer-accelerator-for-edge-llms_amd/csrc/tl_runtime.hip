@@ -35,6 +35,13 @@ struct LayerDev {
     float* sd = nullptr;
     float* g_in = nullptr;
     float* g_post = nullptr;
+    // packed copies (MFMA operand blocks) read by the M <= 32 GEMMs of
+    // batched decode; null when the geometry has no 32-multiple shapes
+    int8_t* wqkv_p = nullptr;
+    int8_t* wo_p = nullptr;
+    int8_t* wg_p = nullptr;
+    int8_t* wu_p = nullptr;
+    int8_t* wd_p = nullptr;
 };
 
 constexpr int kPersistChunk = 64;   // decode steps per persistent launch at most
@@ -61,6 +68,7 @@ struct tl_handle {
 
     std::vector<LayerDev> layers;
     int8_t* lm_w = nullptr;
+    int8_t* lm_wp = nullptr;      // packed copy of lm_w (batched decode LM head), or null
     float* lm_s = nullptr;
     float* g_final = nullptr;
     int8_t* emb = nullptr;
@@ -298,6 +306,17 @@ int32_t run_gemm(tl_handle* h, int epi, GemmArgs a, int kclass) {
         TL_LAUNCH(h, launch_gemm32(h->stream, epi, a, 1, cfg));
         return TL_OK;
     }
+    if (a.m <= 32 && a.wp && (epi != EPI_GLU || (a.wp2 && a.k <= 2048)) && a.k % 64 == 0 && a.k <= 6144 &&
+        a.n % 32 == 0 && h->gemm_small == 0) {
+        // batched decode on the packed weight copies: one 16-wavefront
+        // workgroup per 32 output columns, every weight load a coalesced 1 KiB
+        // (measured faster than splitting K over workgroups: the cross-XCD
+        // reduction of the partial tiles costs more than the added bandwidth)
+        Prof p(h, kclass, bytes);
+        TL_LAUNCH(h, launch_gemm_rows32(h->stream, epi, a));
+        return TL_OK;
+    }
+    a.wp = a.wp2 = nullptr;
     if (a.m <= 32 && a.k % 64 == 0 && a.k <= 6144 && h->gemm_small != 2) {
         // batched decode: one 32-row MFMA tile per 32 output columns, K split
         // over enough workgroups to cover the chip, reduced in the kernel
@@ -337,7 +356,8 @@ int32_t run_gemm(tl_handle* h, int epi, GemmArgs a, int kclass) {
 
 int32_t linear(tl_handle* h, int epi, int rows, const int8_t* x8, const double* xs, const int8_t* w,
                const float* ws, const int8_t* w2, const float* ws2, int32_t n, int32_t k,
-               const float* residual, float* y, int kclass) {
+               const float* residual, float* y, int kclass, const int8_t* wp = nullptr,
+               const int8_t* wp2 = nullptr) {
     if (rows == 1) {
         GemvArgs g{};
         g.w = w; g.w2 = w2; g.ws = ws; g.ws2 = ws2; g.x = x8; g.xs = xs;
@@ -349,7 +369,7 @@ int32_t linear(tl_handle* h, int epi, int rows, const int8_t* x8, const double* 
     }
     GemmArgs a{};
     a.a = x8; a.w = w; a.w2 = w2; a.as = xs; a.ws = ws; a.ws2 = ws2;
-    a.residual = residual; a.y = y; a.m = rows; a.n = n; a.k = k;
+    a.residual = residual; a.y = y; a.m = rows; a.n = n; a.k = k; a.wp = wp; a.wp2 = wp2;
     return run_gemm(h, epi, a, kclass == TL_K_LMHEAD ? TL_K_LMHEAD : TL_K_GEMM_PREFILL);
 }
 
@@ -429,7 +449,8 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
         Prof p(h, TL_K_NORM, (double)rows * D * 9.0);
         TL_LAUNCH(h, launch_rmsnorm_quant(h->stream, h->x, L.g_in, rows, D, c.rms_eps, h->plan, nullptr, h->a8, h->as));
     }
-    if ((r = linear(h, EPI_DEQUANT, rows, h->a8, h->as, L.wqkv, L.sqkv, nullptr, nullptr, QKV, D, nullptr, h->qkv, TL_K_QKV)))
+    if ((r = linear(h, EPI_DEQUANT, rows, h->a8, h->as, L.wqkv, L.sqkv, nullptr, nullptr, QKV, D, nullptr, h->qkv, TL_K_QKV,
+                    L.wqkv_p)))
         return r;
     if (decode) {
         const int G = c.n_heads / c.n_kv_heads;
@@ -450,19 +471,22 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
         Prof p(h, TL_K_NORM, (double)rows * D * 5.0);
         TL_LAUNCH(h, launch_quantize_rows(h->stream, h->att, rows, D, h->a8, h->as));
     }
-    if ((r = linear(h, EPI_DEQUANT_RES, rows, h->a8, h->as, L.wo, L.so, nullptr, nullptr, D, D, h->x, h->x, TL_K_O)))
+    if ((r = linear(h, EPI_DEQUANT_RES, rows, h->a8, h->as, L.wo, L.so, nullptr, nullptr, D, D, h->x, h->x, TL_K_O,
+                    L.wo_p)))
         return r;
     {
         Prof p(h, TL_K_NORM, (double)rows * D * 9.0);
         TL_LAUNCH(h, launch_rmsnorm_quant(h->stream, h->x, L.g_post, rows, D, c.rms_eps, h->plan, nullptr, h->a8, h->as));
     }
-    if ((r = linear(h, EPI_GLU, rows, h->a8, h->as, L.wg, L.sg, L.wu, L.su, F, D, nullptr, h->hid, TL_K_GLU)))
+    if ((r = linear(h, EPI_GLU, rows, h->a8, h->as, L.wg, L.sg, L.wu, L.su, F, D, nullptr, h->hid, TL_K_GLU, L.wg_p,
+                    L.wu_p)))
         return r;
     {
         Prof p(h, TL_K_NORM, (double)rows * F * 5.0);
         TL_LAUNCH(h, launch_quantize_rows(h->stream, h->hid, rows, F, h->a8, h->as));
     }
-    if ((r = linear(h, EPI_DEQUANT_RES, rows, h->a8, h->as, L.wd, L.sd, nullptr, nullptr, D, F, h->x, h->x, TL_K_DOWN)))
+    if ((r = linear(h, EPI_DEQUANT_RES, rows, h->a8, h->as, L.wd, L.sd, nullptr, nullptr, D, F, h->x, h->x, TL_K_DOWN,
+                    L.wd_p)))
         return r;
     return TL_OK;
 }
@@ -483,12 +507,26 @@ int32_t lm_head_rows(tl_handle* h, const float* xrow, int32_t rows, int32_t seq,
             Prof p(h, TL_K_NORM, (double)rows * D * 9.0);
             TL_LAUNCH(h, launch_rmsnorm_quant(h->stream, xrow, h->g_final, rows, D, c.rms_eps, h->plan, nullptr, h->a8, h->as));
         }
-        // M > 1: MFMA GEMM writes logits, a row argmax folds them into keys
         GemmArgs a{};
         a.a = h->a8; a.w = h->lm_w; a.as = h->as; a.ws = h->lm_s; a.y = h->logits; a.m = rows; a.n = V; a.k = D;
-        int32_t r = run_gemm(h, EPI_DEQUANT, a, TL_K_LMHEAD);
-        if (r) return r;
-        TL_LAUNCH(h, launch_argmax_rows(h->stream, h->logits, rows, V, keys));
+        if (rows <= 32 && h->lm_wp && h->gemm_small == 0 && D % 64 == 0 && D <= 2048) {
+            // packed-weight MFMA GEMM with the argmax in its epilogue (one key
+            // per 32-column tile and row), then the tiles' keys folded per row
+            const int tiles = V / 32;
+            int32_t r = ensure_partials(h, (size_t)tiles * rows * 2);
+            if (r) return r;
+            a.wp = h->lm_wp;
+            a.key = (unsigned long long*)h->partials;
+            a.y = nullptr;
+            Prof p(h, TL_K_LMHEAD, (double)V * D + V * 4.0 + (double)rows * D);
+            TL_LAUNCH(h, launch_gemm_rows32(h->stream, EPI_ARGMAX, a));
+            TL_LAUNCH(h, launch_argmax_tiles(h->stream, a.key, tiles, rows, keys));
+        } else {
+            // MFMA GEMM writes logits, a row argmax folds them into keys
+            int32_t r = run_gemm(h, EPI_DEQUANT, a, TL_K_LMHEAD);
+            if (r) return r;
+            TL_LAUNCH(h, launch_argmax_rows(h->stream, h->logits, rows, V, keys));
+        }
     }
     TL_LAUNCH(h, launch_finalize_tokens(h->stream, keys, rows, h->token_cur + (rows == 1 ? seq : 0),
                                         h->tokens_out + (int64_t)(rows == 1 ? seq : 0) * c.max_pos, c.max_pos,
@@ -801,6 +839,20 @@ int32_t tl_load_layer(tl_handle* h, int32_t layer, const int8_t* const w[7], con
     TL_HIP(h, copy_in(h, L.sd, s[6], sizeof(float) * D, src));
     TL_HIP(h, copy_in(h, L.g_in, g_in, sizeof(float) * D, src));
     TL_HIP(h, copy_in(h, L.g_post, g_post, sizeof(float) * D, src));
+    if (D % 32 == 0 && F % 32 == 0 && KVD % 32 == 0) {
+        if (!L.wqkv_p) {
+            TL_HIP(h, dalloc(h, &L.wqkv_p, (size_t)h->QKV * D));
+            TL_HIP(h, dalloc(h, &L.wo_p, (size_t)D * D));
+            TL_HIP(h, dalloc(h, &L.wg_p, (size_t)F * D));
+            TL_HIP(h, dalloc(h, &L.wu_p, (size_t)F * D));
+            TL_HIP(h, dalloc(h, &L.wd_p, (size_t)D * F));
+        }
+        TL_LAUNCH(h, launch_pack_weights(h->stream, L.wqkv, h->QKV, D, L.wqkv_p));
+        TL_LAUNCH(h, launch_pack_weights(h->stream, L.wo, D, D, L.wo_p));
+        TL_LAUNCH(h, launch_pack_weights(h->stream, L.wg, F, D, L.wg_p));
+        TL_LAUNCH(h, launch_pack_weights(h->stream, L.wu, F, D, L.wu_p));
+        TL_LAUNCH(h, launch_pack_weights(h->stream, L.wd, D, F, L.wd_p));
+    }
     h->players_dirty = true;
     return finish(h);
 }
@@ -811,6 +863,10 @@ int32_t tl_load_lm_head(tl_handle* h, const int8_t* w, const float* s, const flo
     TL_HIP(h, copy_in(h, h->lm_w, w, (size_t)h->cfg.vocab * h->D, src));
     TL_HIP(h, copy_in(h, h->lm_s, s, sizeof(float) * h->cfg.vocab, src));
     TL_HIP(h, copy_in(h, h->g_final, g_final, sizeof(float) * h->D, src));
+    if (h->cfg.vocab % 32 == 0 && h->D % 32 == 0) {
+        if (!h->lm_wp) TL_HIP(h, dalloc(h, &h->lm_wp, (size_t)h->cfg.vocab * h->D));
+        TL_LAUNCH(h, launch_pack_weights(h->stream, h->lm_w, h->cfg.vocab, h->D, h->lm_wp));
+    }
     return finish(h);
 }
 
