@@ -128,6 +128,50 @@ def test_quantize_rows_and_tensor(rt):
     assert host(st)[0] == ws
 
 
+def near_half_integer_rows(rows, n, seed):
+    """Rows whose quotients x / s sit on and within a few ulps of
+    half-integers k + 1/2 (the rounding boundaries of the quantizers), with
+    the row maximum fixing s = f32(max / 127)."""
+    rng = np.random.default_rng(seed)
+    out = np.empty((rows, n), F32)
+    for r in range(rows):
+        mx = F32(rng.uniform(0.05, 40.0))
+        sf = F32(np.float64(mx) / 127.0)
+        k = rng.integers(-127, 127, n).astype(np.float64)
+        v = ((k + 0.5) * np.float64(sf)).astype(F32)
+        ulps = rng.integers(-3, 4, n).astype(np.int32)
+        v = (v.view(np.int32) + ulps).view(F32)
+        v = np.clip(v, -mx, mx)
+        v[0] = mx
+        out[r] = v
+    return out
+
+
+@pytest.mark.parametrize("n", [2048, 5632, 1000])
+def test_quantizers_at_rounding_boundaries(rt, n):
+    """rint(RN(x / s)) exactly at and around every rounding boundary of the
+    quantizers (row, tensor and RMSNorm-prologue paths)."""
+    x = near_half_integer_rows(8, n, seed=n)
+    q, s = empty((8, n), np.int8), empty(8, np.float64)
+    rt.call("tl_quantize_rows", dev(x), 8, n, q, s)
+    want_q, want_s = oracle.quantize_rows(x)
+    assert_bits_equal(host(q), want_q, "rows q at half-integers")
+    assert_bits_equal(host(s), want_s, "rows s")
+    qt, st = empty((8, n), np.int8), empty(1, np.float64)
+    rt.call("tl_quantize_tensor", dev(x), x.size, qt, st)
+    wq, ws = oracle.quantize_int8(x)
+    assert_bits_equal(host(qt), wq, "tensor q at half-integers")
+    if n % 256 == 0:
+        # the RMSNorm prologue with unit gains on rows already at unit RMS
+        # keeps the quotients near the boundaries
+        g = np.ones(n, F32)
+        y, q2, s2 = empty((8, n), np.float32), empty((8, n), np.int8), empty(8, np.float64)
+        rt.call("tl_rmsnorm_quant", dev(x), dev(g), 8, n, None, q2, s2)
+        want_q2, want_s2 = oracle.quantize_rows(oracle.rms_norm(x, g, F32(1e-5)))
+        assert_bits_equal(host(q2), want_q2, "rmsnorm prologue q")
+        assert_bits_equal(host(s2), want_s2, "rmsnorm prologue s")
+
+
 def test_quantize_weight_rows(rt):
     rng = np.random.default_rng(4)
     w = (rng.standard_normal((300, 2048)) * 0.02).astype(F32)
