@@ -476,14 +476,14 @@ __global__ __launch_bounds__(256) void attention_row_kernel(AttnDecodeArgs p) {
     float mx = 0.0f;
 #pragma unroll
     for (int j = 0; j < kRowQPerThread; j++) {
-        const float o = __shfl_xor(qv[j], 32);
+        const float o = lane_xor<32>(qv[j]);
         const float rot = d < 32 ? -o : o;
         if (j < nq) mx = fmaxf(mx, fabsf((qv[j] * cs) + (rot * sn)));
     }
     mx = wave_max_f32(mx);
     if (lane == 0) red[wave] = mx;
     // this head's rotated Q, this row's K (RoPE, static scale) and V
-    const float qo = __shfl_xor(qh, 32), ko = __shfl_xor(kx, 32);
+    const float qo = lane_xor<32>(qh), ko = lane_xor<32>(kx);
     const float qr = (qh * cs) + ((d < 32 ? -qo : qo) * sn);
     const float kr = (kx * cs) + ((d < 32 ? -ko : ko) * sn);
     const int8_t k8 = sat_i8(__builtin_rintf(__fdiv_rn(kr, sk)));
@@ -680,7 +680,7 @@ __global__ __launch_bounds__(kGW * 64) void attention_group_kernel(AttnDecodeArg
     float mx = 0.0f;
 #pragma unroll
     for (int j = 0; j < kQPer; j++) {
-        const float o = __shfl_xor(qv[j], 32);
+        const float o = lane_xor<32>(qv[j]);
         if (tid + kGW * 64 * j < D) mx = fmaxf(mx, fabsf((qv[j] * cs) + ((d < 32 ? -o : o) * sn)));
     }
     mx = wave_max_f32(mx);
@@ -692,11 +692,11 @@ __global__ __launch_bounds__(kGW * 64) void attention_group_kernel(AttnDecodeArg
     for (int w = 1; w < kGW; w++) mx = fmaxf(mx, red[w]);
     const double s_q = quant_scale(mx);
     if (wave < HPW) {
-        const float qo = __shfl_xor(qh, 32);
+        const float qo = lane_xor<32>(qh);
         const float qr = (qh * cs) + ((d < 32 ? -qo : qo) * sn);
         qs[wave][d] = sat_i8(__builtin_rintf(__fdiv_rn(qr, (float)s_q)));
     } else if (wave == HPW) {
-        const float ko = __shfl_xor(kx, 32);
+        const float ko = lane_xor<32>(kx);
         const float kr = (kx * cs) + ((d < 32 ? -ko : ko) * sn);
         const int8_t k8 = sat_i8(__builtin_rintf(__fdiv_rn(kr, sk)));
         const int8_t v8 = sat_i8(__builtin_rintf(__fdiv_rn(vx, sv)));

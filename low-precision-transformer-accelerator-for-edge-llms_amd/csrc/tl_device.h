@@ -105,34 +105,177 @@ TL_DEV int32_t key_index(unsigned long long key) {
     return (int32_t)(0xFFFFFFFFu - (unsigned)(key & 0xFFFFFFFFull));
 }
 
-TL_DEV int wave_sum_i32(int v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-    return v;
+// ---------------------------------------------------------------------------
+// cross-lane exchange without the LDS crossbar (a ds_bpermute costs an LDS
+// round trip per step): DPP moves inside rows of 16 lanes, gfx950's
+// v_permlane16_swap / v_permlane32_swap across rows and wavefront halves.
+// Every helper expects the whole wavefront active.
+// ---------------------------------------------------------------------------
+TL_DEV int lane_id() { return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+
+// DPP controls
+constexpr int kDppXor1 = 0xB1;          // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;          // quad_perm [2,3,0,1]
+// row_ror:n hands lane j the value of lane (j - n) mod 16 of its row
+constexpr int kDppRor4 = 0x124;         // row_ror:4  (lane - 4 within the row)
+constexpr int kDppRor8 = 0x128;         // row_ror:8  (= lane ^ 8)
+constexpr int kDppRor12 = 0x12C;        // row_ror:12 (lane + 4 within the row)
+constexpr int kDppRowMirror = 0x140;    // lane 15 - j within the row
+constexpr int kDppHalfMirror = 0x141;   // lane 7 - j within each half-row
+
+// every control used reads a lane of the same row, so no lane takes the
+// 0 given for out-of-row sources; the 0 lets the move fold into its user
+template <int CTRL>
+TL_DEV int dpp(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
 }
 
-TL_DEV float wave_max_f32(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-    return v;
-}
-
-// the fixed 64-wide butterfly (same tree as or_block_sum64)
-TL_DEV float wave_butterfly_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off);
-    return v;
-}
-
-TL_DEV unsigned long long wave_max_u64(unsigned long long v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        unsigned lo = __shfl_xor((unsigned)(v & 0xFFFFFFFFull), off);
-        unsigned hi = __shfl_xor((unsigned)(v >> 32), off);
-        unsigned long long o = ((unsigned long long)hi << 32) | lo;
-        v = o > v ? o : v;
+// the value of lane (lane ^ OFF): __shfl_xor(v, OFF) of a full wavefront
+template <int OFF>
+TL_DEV int lane_xor(int v) {
+    static_assert(OFF == 1 || OFF == 2 || OFF == 4 || OFF == 8 || OFF == 16 || OFF == 32, "lane_xor: 1 .. 32");
+    if constexpr (OFF == 1) {
+        return dpp<kDppXor1>(v);
+    } else if constexpr (OFF == 2) {
+        return dpp<kDppXor2>(v);
+    } else if constexpr (OFF == 4) {
+        const int up = dpp<kDppRor12>(v), dn = dpp<kDppRor4>(v);
+        return (lane_id() & 4) ? dn : up;
+    } else if constexpr (OFF == 8) {
+        return dpp<kDppRor8>(v);
+    } else if constexpr (OFF == 16) {
+        // rows 1, 3 of the first operand trade places with rows 0, 2 of the
+        // second: p[0] = rows (0, 0, 2, 2), p[1] = rows (1, 1, 3, 3)
+        const auto p = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+        return (int)((lane_id() & 16) ? p[0] : p[1]);
+    } else {
+        // the upper half of the first operand trades places with the lower
+        // half of the second: p[0] = halves (lo, lo), p[1] = halves (hi, hi)
+        const auto p = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+        return (int)((lane_id() & 32) ? p[0] : p[1]);
     }
+}
+
+template <int OFF>
+TL_DEV float lane_xor(float v) {
+    return __int_as_float(lane_xor<OFF>(__float_as_int(v)));
+}
+
+// lane ^ off for a wavefront-uniform run-time off (a power of two below 64)
+TL_DEV float lane_xor_rt(float v, int off) {
+    switch (off) {
+        case 1: return lane_xor<1>(v);
+        case 2: return lane_xor<2>(v);
+        case 4: return lane_xor<4>(v);
+        case 8: return lane_xor<8>(v);
+        case 16: return lane_xor<16>(v);
+        default: return lane_xor<32>(v);
+    }
+}
+
+// pair sums of the xor-16 / xor-32 levels of a butterfly: both swap results
+// added give v[lane] + v[lane ^ OFF] in every lane
+template <int OFF>
+TL_DEV float pair_sum(float v) {
+    static_assert(OFF == 16 || OFF == 32, "pair_sum: 16 or 32");
+    const unsigned u = __float_as_uint(v);
+    const auto p = OFF == 16 ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                             : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
+// the four row values of a row-uniform register, combined by the caller
+TL_DEV int row_value(int v, int row) { return __builtin_amdgcn_readlane(v, 16 * row); }
+
+// integer sum over the wavefront (exact in any order), in every lane
+TL_DEV int wave_sum_i32(int v) {
+    v += dpp<kDppXor1>(v);
+    v += dpp<kDppXor2>(v);
+    v += dpp<kDppHalfMirror>(v);
+    v += dpp<kDppRowMirror>(v);   // every lane: its row's sum
+    return (row_value(v, 0) + row_value(v, 1)) + (row_value(v, 2) + row_value(v, 3));
+}
+
+// maximum over the wavefront (order-free), in every lane
+TL_DEV float wave_max_f32(float v) {
+    v = fmaxf(v, __int_as_float(dpp<kDppXor1>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp<kDppXor2>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp<kDppHalfMirror>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp<kDppRowMirror>(__float_as_int(v))));
+    const int iv = __float_as_int(v);
+    return fmaxf(fmaxf(__int_as_float(row_value(iv, 0)), __int_as_float(row_value(iv, 1))),
+                 fmaxf(__int_as_float(row_value(iv, 2)), __int_as_float(row_value(iv, 3))));
+}
+
+// maximum over each half-wavefront (lanes 0-31, 32-63), in every lane of it
+TL_DEV float half_max_f32(float v) {
+    v = fmaxf(v, __int_as_float(dpp<kDppXor1>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp<kDppXor2>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp<kDppHalfMirror>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp<kDppRowMirror>(__float_as_int(v))));
+    const unsigned u = __float_as_uint(v);
+    const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+
+// the fixed 64-wide butterfly: levels 32, 16, 8, 4, 2, 1, each adding lane
+// pairs (lane, lane ^ off) (same tree as or_block_sum64)
+TL_DEV float wave_butterfly_sum(float v) {
+    v = pair_sum<32>(v);
+    v = pair_sum<16>(v);
+    v = v + lane_xor<8>(v);
+    v = v + lane_xor<4>(v);
+    v = v + lane_xor<2>(v);
+    v = v + lane_xor<1>(v);
     return v;
+}
+
+// the same butterfly over each half-wavefront: levels 16, 8, 4, 2, 1
+TL_DEV float half_butterfly_sum(float v) {
+    v = pair_sum<16>(v);
+    v = v + lane_xor<8>(v);
+    v = v + lane_xor<4>(v);
+    v = v + lane_xor<2>(v);
+    v = v + lane_xor<1>(v);
+    return v;
+}
+
+TL_DEV unsigned long long max_u64(unsigned long long a, unsigned long long b) { return b > a ? b : a; }
+
+template <int CTRL>
+TL_DEV unsigned long long dpp_u64(unsigned long long v) {
+    const unsigned lo = (unsigned)dpp<CTRL>((int)(unsigned)(v & 0xFFFFFFFFull));
+    const unsigned hi = (unsigned)dpp<CTRL>((int)(unsigned)(v >> 32));
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+TL_DEV unsigned long long row_max_u64(unsigned long long v) {
+    v = max_u64(v, dpp_u64<kDppXor1>(v));
+    v = max_u64(v, dpp_u64<kDppXor2>(v));
+    v = max_u64(v, dpp_u64<kDppHalfMirror>(v));
+    return max_u64(v, dpp_u64<kDppRowMirror>(v));
+}
+
+TL_DEV unsigned long long row_value_u64(unsigned long long v, int row) {
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(v & 0xFFFFFFFFull), 16 * row);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(v >> 32), 16 * row);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+// maximum of 64-bit keys over the wavefront, in every lane
+TL_DEV unsigned long long wave_max_u64(unsigned long long v) {
+    v = row_max_u64(v);
+    return max_u64(max_u64(row_value_u64(v, 0), row_value_u64(v, 1)),
+                   max_u64(row_value_u64(v, 2), row_value_u64(v, 3)));
+}
+
+// maximum of 64-bit keys over each half-wavefront, in every lane of it
+TL_DEV unsigned long long half_max_u64(unsigned long long v) {
+    v = row_max_u64(v);
+    const unsigned lo = (unsigned)(v & 0xFFFFFFFFull), hi = (unsigned)(v >> 32);
+    const auto pl = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto ph = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    return max_u64(((unsigned long long)ph[0] << 32) | pl[0], ((unsigned long long)ph[1] << 32) | pl[1]);
 }
 
 // 128-bit loads that stay 128-bit: weights stream through once (non-temporal)

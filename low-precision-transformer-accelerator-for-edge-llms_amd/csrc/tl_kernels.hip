@@ -514,7 +514,7 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs a, int32_t sl
         __builtin_amdgcn_s_waitcnt(0);   // the partial tile has reached the coherence point
         unsigned before = 0;
         if (lane == 0) before = __hip_atomic_fetch_add(counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        before = __shfl(before, 0);
+        before = (unsigned)__builtin_amdgcn_readlane((int)before, 0);
         if ((int)before != slices - 1) return;   // not the last: the last one finishes the tile
         // every other slice's tile straight into LDS (device-coherent loads,
         // 1 KiB per instruction, all in flight at once), then the sums
@@ -860,8 +860,7 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(AttnTileArgs p) {
 #pragma unroll
     for (int i = 0; i < 16; i++) {
         float v = mx[i];
-#pragma unroll
-        for (int off = 16; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+        v = half_max_f32(v);
         if (col == 0) wmax[wave][8 * (i >> 2) + 4 * hi + (i & 3)] = v;
     }
     __syncthreads();
@@ -880,8 +879,7 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(AttnTileArgs p) {
             const float e0 = t0 <= rpos[i] ? tl_expf((float)S0[i] * rs[i] - m[i]) : 0.0f;
             const float e1 = t1 <= rpos[i] ? tl_expf((float)S1[i] * rs[i] - m[i]) : 0.0f;
             float v = e0 + e1;
-#pragma unroll
-            for (int off = 16; off >= 1; off >>= 1) v = v + __shfl_xor(v, off);
+            v = half_butterfly_sum(v);
             if (col == 0) bsum[(8 * (i >> 2) + 4 * hi + (i & 3)) * nblk + b] = v;
         }
     }
@@ -1345,13 +1343,7 @@ __global__ __launch_bounds__(1024) void gemm_rows32_kernel(GemmArgs a) {
             if (a.y) a.y[(int64_t)m * a.n + n] = lg;
             k = argmax_key(lg, n);
         }
-#pragma unroll
-        for (int off = 16; off >= 1; off >>= 1) {
-            const unsigned lo = __shfl_xor((unsigned)(k & 0xFFFFFFFFull), off);
-            const unsigned hi2 = __shfl_xor((unsigned)(k >> 32), off);
-            const unsigned long long o = ((unsigned long long)hi2 << 32) | lo;
-            k = o > k ? o : k;
-        }
+        k = half_max_u64(k);
         if ((l & 31) == 0 && m < a.m) a.key[(int64_t)blockIdx.x * a.m + m] = k;
         return;
     }
@@ -1602,7 +1594,7 @@ __global__ __launch_bounds__(256) void attention_tile_reg_kernel(AttnTileArgs p)
                 mx = (blk && t <= rpos) ? fmaxf(mx, v) : mx;
             }
         }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = fmaxf(mx, lane_xor<32>(mx));
     if (hi == 0) wmax[wave][col] = mx;
     __syncthreads();
     const float m = fmaxf(fmaxf(wmax[0][col], wmax[1][col]), fmaxf(wmax[2][col], wmax[3][col]));
@@ -1630,7 +1622,7 @@ __global__ __launch_bounds__(256) void attention_tile_reg_kernel(AttnTileArgs p)
         }
         float d[4];
 #pragma unroll
-        for (int r = 0; r < 4; r++) d[r] = c[r] + __shfl_xor(c[r], 32);      // distance 4
+        for (int r = 0; r < 4; r++) d[r] = pair_sum<32>(c[r]);      // distance 4
         const float f = (d[0] + d[2]) + (d[1] + d[3]);                        // distances 2, 1
         if (hi == 0 && b < nblk) bsum[col * nblk + b] = f;
     }

@@ -91,7 +91,7 @@ TL_DEV void prologue_rmsnorm(const float4 (&xv)[KCH], const float4 (&gv)[KCH], i
             const float* r = part + 8 * lane;
             v = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
         }
-        for (int off = 1; off < L; off <<= 1) v = v + __shfl_xor(v, off);
+        for (int off = 1; off < L; off <<= 1) v = v + lane_xor_rt(v, off);
         if (lane == 0) red[8] = v;
     }
     __syncthreads();

@@ -161,6 +161,55 @@ def test_lm_head_argmax_operator(small_model):
     eng.close()
 
 
+def _leaf_sums(sq):
+    """Sums of the 16 leaves of 128 squares each (NumPy's 8-accumulator leaf)."""
+    import ctypes as C
+    out = []
+    for j in range(16):
+        leaf = np.ascontiguousarray(sq[128 * j:128 * (j + 1)])
+        out.append(np.float32(oracle.lib().or_pairwise_sum(oracle.ptr(leaf, C.c_float), 128)))
+    return out
+
+
+def _combine(lv, partner):
+    """Pairwise levels 1, 2, 4, 8 over 16 leaf sums; partner(j, off) names the
+    leaf position added to position j at level off; returns position 0."""
+    v = list(lv)
+    for off in (1, 2, 4, 8):
+        v = [np.float32(v[j] + v[partner(j, off)]) for j in range(16)]
+    return v[0]
+
+
+def test_rmsnorm_leaf_order_lm_head(layer_model):
+    """Rows whose 128-element leaves span 2^-4 .. 2^4 in magnitude, so that the
+    float32 sum of squares depends on how the 16 leaf sums are paired.  The
+    final RMSNorm + LM-head GEMV, whose prologue combines the leaf sums across
+    lanes, must give the oracle's logits bit for bit.  The rows are first shown
+    to tell NumPy's pairing (j ^ off) from a rotated one (j - off within 16)."""
+    import ctypes
+    m = layer_model
+    eng = engine_for(m)
+    rng = np.random.default_rng(77)
+    told_apart = 0
+    orc = oracle.Oracle(m)
+    for r in range(24):
+        x = rng.standard_normal(2048).astype(F32)
+        x *= np.repeat(np.exp2(rng.integers(-4, 5, 16)), 128).astype(F32)
+        sq = (x * x).astype(F32)
+        lv = _leaf_sums(sq)
+        right = _combine(lv, lambda j, off: j ^ off)
+        assert right == np.float32(oracle.lib().or_pairwise_sum(oracle.ptr(sq, ctypes.c_float), sq.size))
+        told_apart += right != _combine(lv, lambda j, off: (j & ~15) | ((j - off) & 15))
+        tok, lg = ctypes.c_int32(), ctypes.c_float()
+        logits = dev(np.zeros(m.cfg["vocab"], F32))
+        eng.rt.call("tl_lm_head_argmax", dev(x), ctypes.byref(tok), ctypes.byref(lg), logits)
+        want_tok, want_lg, want_logits = orc.lm_head(x, want_logits=True)
+        assert_bits_equal(host(logits), want_logits, f"logits of row {r}")
+        assert tok.value == want_tok and lg.value == want_lg
+    assert told_apart >= 8
+    eng.close()
+
+
 def test_bad_arguments_raise_value_error(small_model):
     from lpta import TlValueError
     eng = engine_for(small_model)
