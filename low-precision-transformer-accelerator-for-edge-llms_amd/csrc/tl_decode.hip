@@ -33,7 +33,7 @@ __global__ __launch_bounds__(kNT) void gemv_fused_kernel(GemvArgs a) {
     constexpr int NM = (EPI == EPI_GLU) ? 2 : 1;
     __shared__ __align__(16) int8_t xs8[KCH * 1024];
     __shared__ __align__(16) float sq[PRO == PRO_RMSNORM ? KCH * 1024 : 4];
-    __shared__ float part[PRO == PRO_RMSNORM ? 8 * 64 : 4];
+    __shared__ __align__(16) float part[PRO == PRO_RMSNORM ? 8 * 64 : 4];
     __shared__ float red[16];
     __shared__ double xscale;
     __shared__ unsigned long long wbest[kNW];

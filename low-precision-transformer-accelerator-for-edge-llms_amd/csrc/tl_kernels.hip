@@ -92,7 +92,7 @@ __global__ __launch_bounds__(kNT) void rows_prologue_kernel(const float* __restr
                                                            double* __restrict__ scales) {
     __shared__ __align__(16) int8_t xs8[KCH * 1024];
     __shared__ __align__(16) float sq[PRO == PRO_RMSNORM ? KCH * 1024 : 4];
-    __shared__ float part[PRO == PRO_RMSNORM ? 8 * 64 : 4];
+    __shared__ __align__(16) float part[PRO == PRO_RMSNORM ? 8 * 64 : 4];
     __shared__ float red[16];
     __shared__ double xscale;
     const int tid = threadIdx.x, row = blockIdx.x;

@@ -51,9 +51,10 @@ TL_DEV void prologue_quant(const float4 (&xv)[KCH], int K, int8_t* xs8, float* r
     __syncthreads();
 }
 
+// sum of squares of a row through LDS in NumPy's pairwise order (plan's
+// perfect tree); every thread gets the sum
 template <int KCH>
-TL_DEV void prologue_rmsnorm(const float4 (&xv)[KCH], const float4 (&gv)[KCH], int K, float eps, PwPlan plan,
-                             float* sq, float* part, int8_t* xs8, float* red, double* xscale) {
+TL_DEV float prologue_sumsq(const float4 (&xv)[KCH], int K, PwPlan plan, float* sq, float* part, float* red) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 #pragma unroll
     for (int c = 0; c < KCH; c++) {
@@ -95,7 +96,74 @@ TL_DEV void prologue_rmsnorm(const float4 (&xv)[KCH], const float4 (&gv)[KCH], i
         if (lane == 0) red[8] = v;
     }
     __syncthreads();
-    const float var = __fdiv_rn(red[8], (float)K);
+    return red[8];
+}
+
+// ---------------------------------------------------------------------------
+// NumPy's pairwise sum of squares of a 2048-element row (16 leaves of 128)
+// with one barrier.  Wavefront w holds leaves 2w, 2w+1 (chunk 0) and
+// 8+2w, 9+2w (chunk 1) in its float4 registers; it transposes their squares
+// through its own 512 floats of LDS (element e of local leaf ll at
+// 128 ll + (e ^ 8 ll), so the strided reads of 32 lanes hit 32 banks), lane
+// 8 ll + r sums accumulator r of local leaf ll in order, lane pairs 1, 2, 4
+// apart combine a leaf's accumulators and lane pairs 8 apart the two leaves
+// of a chunk.  The eight pair sums meet in LDS and every thread finishes the
+// tree ((P0+P1)+(P2+P3))+((P4+P5)+(P6+P7)).  sq needs 2048 floats, part 8.
+// ---------------------------------------------------------------------------
+
+TL_DEV bool pw_by_waves(PwPlan plan, int K) {
+    return plan.leaf_len == 128 && plan.n_leaves == 16 && K == 2048;
+}
+
+TL_DEV float pw_sumsq_2048(const float4 (&xv)[2], float* sq, float* part) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float* mine = sq + wave * 512;
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        float4 q;
+        q.x = xv[c].x * xv[c].x;
+        q.y = xv[c].y * xv[c].y;
+        q.z = xv[c].z * xv[c].z;
+        q.w = xv[c].w * xv[c].w;
+        const int ll = 2 * c + (lane >> 5);
+        *(float4*)(mine + 128 * ll + ((4 * (lane & 31)) ^ (8 * ll))) = q;
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wavefront's stores are in LDS
+    __builtin_amdgcn_wave_barrier();
+    const int ll = (lane & 31) >> 3;
+    const float* a = mine + 128 * ll;
+    float v[16];
+#pragma unroll
+    for (int u = 0; u < 16; u++) v[u] = a[((lane & 7) + 8 * u) ^ (8 * ll)];
+    float r = v[0];
+#pragma unroll
+    for (int u = 1; u < 16; u++) r = r + v[u];
+    r = r + lane_xor<1>(r);
+    r = r + lane_xor<2>(r);
+    r = r + lane_xor<4>(r);   // local leaf ll = (lane & 31) >> 3
+    r = r + lane_xor<8>(r);   // lane 0: leaves 2w + 2w+1, lane 16: leaves 8+2w + 9+2w
+    if (lane == 0) part[wave] = r;
+    if (lane == 16) part[4 + wave] = r;
+    __syncthreads();
+    const float4 p0 = *(const float4*)part, p1 = *(const float4*)(part + 4);
+    return ((p0.x + p0.y) + (p0.z + p0.w)) + ((p1.x + p1.y) + (p1.z + p1.w));
+}
+
+template <int KCH>
+TL_DEV void prologue_rmsnorm(const float4 (&xv)[KCH], const float4 (&gv)[KCH], int K, float eps, PwPlan plan,
+                             float* sq, float* part, int8_t* xs8, float* red, double* xscale) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float total;
+    if constexpr (KCH == 2) {
+        if (pw_by_waves(plan, K)) {
+            total = pw_sumsq_2048(xv, sq, part);
+        } else {
+            total = prologue_sumsq<KCH>(xv, K, plan, sq, part, red);
+        }
+    } else {
+        total = prologue_sumsq<KCH>(xv, K, plan, sq, part, red);
+    }
+    const float var = __fdiv_rn(total, (float)K);
     const float inv = __fdiv_rn(1.0f, __builtin_sqrtf(var + eps));
     float4 av[KCH];
     float mx = 0.0f;
