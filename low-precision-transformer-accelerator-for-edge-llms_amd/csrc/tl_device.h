@@ -80,6 +80,50 @@ TL_DEV int8_t sat_i8(float v) {
     return (int8_t)(int)v;
 }
 
+// a / b rounded to nearest for many a over one b.  y = RN(1/b) is formed
+// once; each quotient starts from q0 = RN(a y) and takes two residual
+// corrections q <- RN(q + RN(a - b q) y), both fused multiply-adds.  The
+// first leaves q within half an ulp plus 2^-46 relative of a / b (so
+// faithful); the second is Markstein's correction, which from a faithful q
+// and y within half an ulp of 1/b gives RN(a / b) exactly.  The proof needs
+// normal residuals: callers take this path only when rn_div_ok(b)
+// (|b| in [2^-64, 2^64]) and |a y| stays finite, and a correctly rounded
+// division otherwise.  A quotient below the normal range may differ in its
+// last bits; it rounds to integer 0 either way.
+struct RnDiv {
+    float b, y;
+    bool fast;   // the same in every lane
+};
+
+TL_DEV RnDiv rn_div_prep(float b) {
+    RnDiv d;
+    d.b = b;
+    d.y = __fdiv_rn(1.0f, b);
+    const float ab = fabsf(b);
+    d.fast = __builtin_amdgcn_readfirstlane((int)(ab >= 0x1p-64f && ab <= 0x1p64f)) != 0;
+    return d;
+}
+
+TL_DEV float rn_div_fast(float a, const RnDiv& d) {
+    const float q0 = a * d.y;
+    const float q1 = __builtin_fmaf(__builtin_fmaf(-d.b, q0, a), d.y, q0);
+    return __builtin_fmaf(__builtin_fmaf(-d.b, q1, a), d.y, q1);
+}
+
+// four quotients -> four saturated INT8 bytes (GI:39-41), x in byte 0
+template <bool FAST>
+TL_DEV unsigned quant4(float4 v, const RnDiv& d) {
+    const float q0 = FAST ? rn_div_fast(v.x, d) : __fdiv_rn(v.x, d.b);
+    const float q1 = FAST ? rn_div_fast(v.y, d) : __fdiv_rn(v.y, d.b);
+    const float q2 = FAST ? rn_div_fast(v.z, d) : __fdiv_rn(v.z, d.b);
+    const float q3 = FAST ? rn_div_fast(v.w, d) : __fdiv_rn(v.w, d.b);
+    const unsigned b0 = (uint8_t)sat_i8(__builtin_rintf(q0));
+    const unsigned b1 = (uint8_t)sat_i8(__builtin_rintf(q1));
+    const unsigned b2 = (uint8_t)sat_i8(__builtin_rintf(q2));
+    const unsigned b3 = (uint8_t)sat_i8(__builtin_rintf(q3));
+    return b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+}
+
 // GI:36-42 scale: max|x| / 127 in float64, 1.0 for an all-zero tensor
 TL_DEV double quant_scale(float mx) { return mx != 0.0f ? (double)mx / 127.0 : 1.0; }
 

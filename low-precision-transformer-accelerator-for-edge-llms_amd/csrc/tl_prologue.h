@@ -14,6 +14,18 @@ namespace tl {
 constexpr int kNT = 256;   // threads per workgroup of the fused GEMV
 constexpr int kNW = kNT / 64;
 
+// INT8 row into LDS: chunk c of thread t holds elements 4 (256 c + t) .. +3;
+// bytes beyond K stay zero (they meet padded weight lanes)
+template <bool FAST, int KCH>
+TL_DEV void quant_row(const float4 (&v)[KCH], int K, const RnDiv& dv, int8_t* xs8) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int c = 0; c < KCH; c++) {
+        const int idx = c * kNT + tid;
+        ((unsigned*)xs8)[idx] = idx * 4 < K ? quant4<FAST>(v[c], dv) : 0u;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // activation prologues: f32 row (K elements, 4 per float4 chunk) -> INT8 row
 // in LDS (natural byte order) + its float64 scale
@@ -33,20 +45,10 @@ TL_DEV void prologue_quant(const float4 (&xv)[KCH], int K, int8_t* xs8, float* r
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     const double s = quant_scale(mx);
-    const float sf = (float)s;
-#pragma unroll
-    for (int c = 0; c < KCH; c++) {
-        const int idx = c * kNT + tid;
-        unsigned word = 0;  // bytes beyond K stay zero: they meet padded weight lanes
-        if (idx * 4 < K) {
-            const unsigned b0 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(xv[c].x, sf)));
-            const unsigned b1 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(xv[c].y, sf)));
-            const unsigned b2 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(xv[c].z, sf)));
-            const unsigned b3 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(xv[c].w, sf)));
-            word = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-        }
-        ((unsigned*)xs8)[idx] = word;
-    }
+    const RnDiv dv = rn_div_prep((float)s);
+    // |x| <= max |x| = 127 b (1 + 2^-24) keeps every x y finite
+    if (dv.fast) quant_row<true, KCH>(xv, K, dv, xs8);
+    else quant_row<false, KCH>(xv, K, dv, xs8);
     if (tid == 0) *xscale = s;
     __syncthreads();
 }
@@ -182,20 +184,10 @@ TL_DEV void prologue_rmsnorm(const float4 (&xv)[KCH], const float4 (&gv)[KCH], i
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     const double s = quant_scale(mx);
-    const float sf = (float)s;
-#pragma unroll
-    for (int c = 0; c < KCH; c++) {
-        const int idx = c * kNT + tid;
-        unsigned word = 0;
-        if (idx * 4 < K) {
-            const unsigned b0 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(av[c].x, sf)));
-            const unsigned b1 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(av[c].y, sf)));
-            const unsigned b2 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(av[c].z, sf)));
-            const unsigned b3 = (uint8_t)sat_i8(__builtin_rintf(__fdiv_rn(av[c].w, sf)));
-            word = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-        }
-        ((unsigned*)xs8)[idx] = word;
-    }
+    const RnDiv dv = rn_div_prep((float)s);
+    // |x| <= max |x| = 127 b (1 + 2^-24) keeps every x y finite
+    if (dv.fast) quant_row<true, KCH>(av, K, dv, xs8);
+    else quant_row<false, KCH>(av, K, dv, xs8);
     if (tid == 0) *xscale = s;
     __syncthreads();
 }
