@@ -129,7 +129,8 @@ __global__ __launch_bounds__(kNT) void gemv_fused_kernel(GemvArgs a) {
         if (tid == 0) {
             unsigned long long b = wbest[0];
             for (int i = 1; i < kNW; i++) b = wbest[i] > b ? wbest[i] : b;
-            if (b) atomicMax(a.key, b);
+            if (a.wg_keys) a.wg_keys[blockIdx.x] = b;   // folded by the consumer
+            else if (b) atomicMax(a.key, b);
         }
         return;
     }
@@ -861,10 +862,14 @@ __global__ __launch_bounds__(256) void embed_step_kernel(const int32_t* __restri
 // ---------------------------------------------------------------------------
 static inline int cdiv(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
+static int gemv_fused_rows(int pro, int epi, int kch);
+
 template <int PRO, int EPI, int R>
 static hipError_t gemv_fused_r(hipStream_t s, const GemvArgs& a) {
     const int kch = cdiv(a.k, 1024);
     const dim3 grid(cdiv(a.n, kNW * R)), block(kNT);
+    // the caller sized wg_keys by gemv_fused_workgroups
+    if (a.wg_keys && (int)grid.x != gemv_fused_workgroups(PRO, EPI, a.n, a.k)) return hipErrorInvalidValue;
     switch (kch) {
         case 1: TL_KLAUNCH((gemv_fused_kernel<PRO, EPI, R, 1>), grid, block, 0, s, a); break;
         case 2: TL_KLAUNCH((gemv_fused_kernel<PRO, EPI, R, 2>), grid, block, 0, s, a); break;
@@ -875,6 +880,22 @@ static hipError_t gemv_fused_r(hipStream_t s, const GemvArgs& a) {
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+static int gemv_fused_rows(int pro, int epi, int kch) {
+    if (pro == PRO_RMSNORM) {
+        if (epi == EPI_DEQUANT || epi == EPI_GLU) return kch <= 2 ? 3 : 1;
+        if (epi == EPI_ARGMAX) return kch <= 2 ? 12 : 2;
+    } else if (pro == PRO_QUANT) {
+        if (epi == EPI_DEQUANT_RES) return 2;
+        if (epi == EPI_DEQUANT) return kch <= 2 ? 2 : 1;
+    }
+    return 0;
+}
+
+int32_t gemv_fused_workgroups(int pro, int epi, int32_t n, int32_t k) {
+    const int r = gemv_fused_rows(pro, epi, cdiv(k, 1024));
+    return r > 0 ? cdiv(n, kNW * r) : 0;
 }
 
 hipError_t launch_gemv_fused(hipStream_t s, int pro, int epi, const GemvArgs& a) {

@@ -85,6 +85,7 @@ struct GemvArgs {
     int8_t* y8;              // [N] (EPI_REQUANT)
     int32_t* acc;            // [N] optional raw accumulators
     unsigned long long* key; // argmax slot (EPI_ARGMAX)
+    unsigned long long* wg_keys; // EPI_ARGMAX: one key per workgroup (no atomic) instead of key
     int32_t n, k;
 };
 
@@ -164,7 +165,10 @@ hipError_t launch_embed(hipStream_t s, const int32_t* tokens, int32_t rows, int3
 hipError_t launch_reset_keys(hipStream_t s, unsigned long long* keys, int32_t n);
 hipError_t launch_finalize_tokens(hipStream_t s, unsigned long long* keys, int32_t rows,
                                   int32_t* token_cur, int32_t* tokens_out, int32_t out_stride,
-                                  int32_t* n_gen, int32_t* cursor, float* best_logit, int32_t advance);
+                                  int32_t* n_gen, int32_t* cursor, float* best_logit, int32_t advance,
+                                  const unsigned long long* wg_keys = nullptr, int32_t n_wg = 0);
+// workgroups launch_gemv_fused uses for this prologue / epilogue / shape
+int32_t gemv_fused_workgroups(int pro, int epi, int32_t n, int32_t k);
 hipError_t launch_argmax_rows(hipStream_t s, const float* logits, int32_t rows, int32_t n,
                               unsigned long long* keys);
 hipError_t launch_argmax_tiles(hipStream_t s, const unsigned long long* part, int32_t tiles, int32_t rows,

@@ -1042,12 +1042,20 @@ __global__ void reset_keys_kernel(unsigned long long* keys, int32_t n) {
 
 // after the LM head: decode each row's argmax key into the current token,
 // append it to the row's output list, advance the cursor, clear the key
-__global__ void finalize_tokens_kernel(unsigned long long* keys, int32_t rows, int32_t* token_cur,
-                                       int32_t* tokens_out, int32_t out_stride, int32_t* n_gen,
-                                       int32_t* cursor, float* best_logit, int32_t advance) {
+__global__ __launch_bounds__(64) void finalize_tokens_kernel(unsigned long long* keys, int32_t rows,
+                                                             int32_t* token_cur, int32_t* tokens_out,
+                                                             int32_t out_stride, int32_t* n_gen, int32_t* cursor,
+                                                             float* best_logit, int32_t advance,
+                                                             const unsigned long long* wg_keys, int32_t n_wg) {
     const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    // one row whose LM head left one key per workgroup: the wavefront folds them
+    unsigned long long fold = 0;
+    if (n_wg > 0) {
+        for (int i = threadIdx.x; i < n_wg; i += 64) fold = max_u64(fold, wg_keys[i]);
+        fold = wave_max_u64(fold);
+    }
     if (r >= rows) return;
-    const unsigned long long k = keys[r];
+    const unsigned long long k = max_u64(keys[r], fold);
     const int32_t tok = key_index(k);
     token_cur[r] = tok;
     const int32_t i = n_gen[r];
@@ -1763,9 +1771,11 @@ hipError_t launch_reset_keys(hipStream_t s, unsigned long long* keys, int32_t n)
 
 hipError_t launch_finalize_tokens(hipStream_t s, unsigned long long* keys, int32_t rows,
                                   int32_t* token_cur, int32_t* tokens_out, int32_t out_stride,
-                                  int32_t* n_gen, int32_t* cursor, float* best_logit, int32_t advance) {
+                                  int32_t* n_gen, int32_t* cursor, float* best_logit, int32_t advance,
+                                  const unsigned long long* wg_keys, int32_t n_wg) {
+    if (n_wg > 0 && rows != 1) return hipErrorInvalidValue;
     TL_KLAUNCH(finalize_tokens_kernel, dim3(ceil_div(rows, 64)), dim3(64), 0, s, keys, rows,
-                       token_cur, tokens_out, out_stride, n_gen, cursor, best_logit, advance);
+                       token_cur, tokens_out, out_stride, n_gen, cursor, best_logit, advance, wg_keys, n_wg);
     return hipGetLastError();
 }
 

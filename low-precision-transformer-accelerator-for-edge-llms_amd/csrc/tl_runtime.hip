@@ -95,6 +95,7 @@ struct tl_handle {
     int32_t* tokens = nullptr;    // [max_rows]
     float* fscratch = nullptr;    // small scratch
     unsigned long long* op_key = nullptr;  // argmax slot of the standalone LM-head operator
+    unsigned long long* lm_wg_keys = nullptr;  // [vocab / 4] batch-1 LM head: argmax key per workgroup
     int32_t* partials = nullptr;
     unsigned* tile_ctr = nullptr;         // [kSkinnyTiles] arrival counters of the small-M GEMM, zero between launches
     size_t partial_cap = 0;       // int32 elements
@@ -497,9 +498,13 @@ int32_t lm_head_rows(tl_handle* h, const float* xrow, int32_t rows, int32_t seq,
     const tl_config& c = h->cfg;
     const int D = h->D, V = c.vocab;
     unsigned long long* keys = h->keys + (rows == 1 ? seq : 0);
+    int32_t n_wg = 0;   // rows == 1: the finalize kernel folds one key per LM-head workgroup
     if (rows == 1) {
         GemvArgs g = gemv_args(h);
         g.xf = xrow; g.gamma = h->g_final; g.w = h->lm_w; g.ws = h->lm_s; g.key = keys; g.n = V; g.k = D;
+        n_wg = gemv_fused_workgroups(PRO_RMSNORM, EPI_ARGMAX, V, D);
+        if (n_wg <= 0 || n_wg > (V + 3) / 4) return fail(h, TL_ERR_INTERNAL, "LM head workgroup count");
+        g.wg_keys = h->lm_wg_keys;
         Prof p(h, TL_K_LMHEAD, (double)V * D + V * 4.0 + D * 8.0);
         TL_LAUNCH(h, launch_gemv_fused(h->stream, PRO_RMSNORM, EPI_ARGMAX, g));
     } else {
@@ -531,7 +536,8 @@ int32_t lm_head_rows(tl_handle* h, const float* xrow, int32_t rows, int32_t seq,
     TL_LAUNCH(h, launch_finalize_tokens(h->stream, keys, rows, h->token_cur + (rows == 1 ? seq : 0),
                                         h->tokens_out + (int64_t)(rows == 1 ? seq : 0) * c.max_pos, c.max_pos,
                                         h->n_gen + (rows == 1 ? seq : 0), h->cursor + (rows == 1 ? seq : 0),
-                                        h->logit_out + (int64_t)(rows == 1 ? seq : 0) * c.max_pos, advance));
+                                        h->logit_out + (int64_t)(rows == 1 ? seq : 0) * c.max_pos, advance,
+                                        h->lm_wg_keys, n_wg));
     return TL_OK;
 }
 
@@ -715,6 +721,7 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
         (e = dalloc(h, &h->logits, (size_t)max_seqs * c.vocab)) || (e = dalloc(h, &h->row_seq, (size_t)R)) || (e = dalloc(h, &h->tile_ctr, (size_t)kSkinnyTiles)) ||
         (e = dalloc(h, &h->row_pos, (size_t)R)) || (e = dalloc(h, &h->tokens, (size_t)R)) ||
         (e = dalloc(h, &h->fscratch, 64)) || (e = dalloc(h, &h->op_key, 1)) || (e = dalloc(h, &h->keys, (size_t)max_seqs)) ||
+        (e = dalloc(h, &h->lm_wg_keys, (size_t)(c.vocab + 3) / 4)) ||
         (e = dalloc(h, &h->token_cur, (size_t)max_seqs)) || (e = dalloc(h, &h->cursor, (size_t)max_seqs)) ||
         (e = dalloc(h, &h->n_gen, (size_t)max_seqs)) ||
         (e = dalloc(h, &h->tokens_out, (size_t)max_seqs * c.max_pos)) ||
