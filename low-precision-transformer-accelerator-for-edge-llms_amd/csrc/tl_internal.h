@@ -163,10 +163,19 @@ hipError_t launch_dequant_i32(hipStream_t s, const int32_t* acc, int64_t n, int3
 hipError_t launch_embed(hipStream_t s, const int32_t* tokens, int32_t rows, int32_t d, int32_t vocab,
                         const int8_t* emb, const float* emb_s, float* x);
 hipError_t launch_reset_keys(hipStream_t s, unsigned long long* keys, int32_t n);
+// embedding of the next step's token (row 0), written by the finalize kernel
+struct EmbedNext {
+    const int8_t* emb;
+    const float* emb_s;
+    int32_t d, vocab;
+    float* x;            // nullptr: no embedding
+    int32_t* row_pos;
+};
 hipError_t launch_finalize_tokens(hipStream_t s, unsigned long long* keys, int32_t rows,
                                   int32_t* token_cur, int32_t* tokens_out, int32_t out_stride,
                                   int32_t* n_gen, int32_t* cursor, float* best_logit, int32_t advance,
-                                  const unsigned long long* wg_keys = nullptr, int32_t n_wg = 0);
+                                  const unsigned long long* wg_keys = nullptr, int32_t n_wg = 0,
+                                  EmbedNext nx = EmbedNext{});
 // workgroups launch_gemv_fused uses for this prologue / epilogue / shape
 int32_t gemv_fused_workgroups(int pro, int epi, int32_t n, int32_t k);
 hipError_t launch_argmax_rows(hipStream_t s, const float* logits, int32_t rows, int32_t n,

@@ -1041,31 +1041,61 @@ __global__ void reset_keys_kernel(unsigned long long* keys, int32_t n) {
 }
 
 // after the LM head: decode each row's argmax key into the current token,
-// append it to the row's output list, advance the cursor, clear the key
+// append it to the row's output list, advance the cursor, clear the key.
+// With one row (single = one wavefront): the LM head may have left one key
+// per workgroup (wg_keys, folded here), and with x the new token's embedding
+// and position are written for the next step (what embed_step_kernel does).
 __global__ __launch_bounds__(64) void finalize_tokens_kernel(unsigned long long* keys, int32_t rows,
                                                              int32_t* token_cur, int32_t* tokens_out,
                                                              int32_t out_stride, int32_t* n_gen, int32_t* cursor,
                                                              float* best_logit, int32_t advance,
-                                                             const unsigned long long* wg_keys, int32_t n_wg) {
-    const int r = blockIdx.x * blockDim.x + threadIdx.x;
-    // one row whose LM head left one key per workgroup: the wavefront folds them
+                                                             const unsigned long long* wg_keys, int32_t n_wg,
+                                                             EmbedNext nx) {
+    const bool single = n_wg > 0 || nx.x != nullptr;
     unsigned long long fold = 0;
     if (n_wg > 0) {
         for (int i = threadIdx.x; i < n_wg; i += 64) fold = max_u64(fold, wg_keys[i]);
         fold = wave_max_u64(fold);
     }
+    const int r = single ? 0 : blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= rows) return;
-    const unsigned long long k = max_u64(keys[r], fold);
+    const unsigned long long k = max_u64(keys[r], fold);   // every lane reads before lane 0 clears
     const int32_t tok = key_index(k);
-    token_cur[r] = tok;
-    const int32_t i = n_gen[r];
-    if (i >= 0 && i < out_stride) {
-        if (tokens_out) tokens_out[(int64_t)r * out_stride + i] = tok;
-        if (best_logit) best_logit[(int64_t)r * out_stride + i] = key_logit(k);
+    const int32_t cur = cursor[r] + advance;
+    if (!single || threadIdx.x == 0) {
+        token_cur[r] = tok;
+        const int32_t i = n_gen[r];
+        if (i >= 0 && i < out_stride) {
+            if (tokens_out) tokens_out[(int64_t)r * out_stride + i] = tok;
+            if (best_logit) best_logit[(int64_t)r * out_stride + i] = key_logit(k);
+        }
+        n_gen[r] = i + 1;
+        cursor[r] = cur;
+        keys[r] = 0ull;
+        if (nx.x) *nx.row_pos = cur;
     }
-    n_gen[r] = i + 1;
-    cursor[r] = cursor[r] + advance;
-    keys[r] = 0ull;
+    if (nx.x) {
+        const bool ok = tok >= 0 && tok < nx.vocab;   // otherwise a zero row, as embed_step_kernel
+        const int t = ok ? tok : 0;
+        const int8_t* e = nx.emb + (int64_t)t * nx.d;
+        const float sc = nx.emb_s[t];
+        if (nx.d % 16 == 0) {   // 16 bytes in, four float4 out per step (rows are 16-byte aligned)
+            for (int i = 16 * threadIdx.x; i < nx.d; i += 16 * 64) {
+                const v4i w = *(const v4i*)(e + i);
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    float4 f;
+                    f.x = ok ? (float)(int8_t)(w[q] & 0xFF) * sc : 0.0f;
+                    f.y = ok ? (float)(int8_t)((w[q] >> 8) & 0xFF) * sc : 0.0f;
+                    f.z = ok ? (float)(int8_t)((w[q] >> 16) & 0xFF) * sc : 0.0f;
+                    f.w = ok ? (float)(int8_t)((w[q] >> 24) & 0xFF) * sc : 0.0f;
+                    *(float4*)(nx.x + i + 4 * q) = f;
+                }
+            }
+        } else {
+            for (int i = threadIdx.x; i < nx.d; i += 64) nx.x[i] = ok ? (float)e[i] * sc : 0.0f;
+        }
+    }
 }
 
 // argmax of each logits row (one workgroup per row) into its key slot
@@ -1772,10 +1802,10 @@ hipError_t launch_reset_keys(hipStream_t s, unsigned long long* keys, int32_t n)
 hipError_t launch_finalize_tokens(hipStream_t s, unsigned long long* keys, int32_t rows,
                                   int32_t* token_cur, int32_t* tokens_out, int32_t out_stride,
                                   int32_t* n_gen, int32_t* cursor, float* best_logit, int32_t advance,
-                                  const unsigned long long* wg_keys, int32_t n_wg) {
-    if (n_wg > 0 && rows != 1) return hipErrorInvalidValue;
+                                  const unsigned long long* wg_keys, int32_t n_wg, EmbedNext nx) {
+    if ((n_wg > 0 || nx.x) && rows != 1) return hipErrorInvalidValue;
     TL_KLAUNCH(finalize_tokens_kernel, dim3(ceil_div(rows, 64)), dim3(64), 0, s, keys, rows,
-                       token_cur, tokens_out, out_stride, n_gen, cursor, best_logit, advance, wg_keys, n_wg);
+                       token_cur, tokens_out, out_stride, n_gen, cursor, best_logit, advance, wg_keys, n_wg, nx);
     return hipGetLastError();
 }
 

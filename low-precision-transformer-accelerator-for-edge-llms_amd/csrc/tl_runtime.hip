@@ -499,6 +499,8 @@ int32_t lm_head_rows(tl_handle* h, const float* xrow, int32_t rows, int32_t seq,
     const int D = h->D, V = c.vocab;
     unsigned long long* keys = h->keys + (rows == 1 ? seq : 0);
     int32_t n_wg = 0;   // rows == 1: the finalize kernel folds one key per LM-head workgroup
+    EmbedNext nx{};     // rows == 1: and embeds the new token into row 0 for the next step
+    if (rows == 1) nx = EmbedNext{h->emb, h->emb_s, h->D, c.vocab, h->x, h->row_pos};
     if (rows == 1) {
         GemvArgs g = gemv_args(h);
         g.xf = xrow; g.gamma = h->g_final; g.w = h->lm_w; g.ws = h->lm_s; g.key = keys; g.n = V; g.k = D;
@@ -537,7 +539,7 @@ int32_t lm_head_rows(tl_handle* h, const float* xrow, int32_t rows, int32_t seq,
                                         h->tokens_out + (int64_t)(rows == 1 ? seq : 0) * c.max_pos, c.max_pos,
                                         h->n_gen + (rows == 1 ? seq : 0), h->cursor + (rows == 1 ? seq : 0),
                                         h->logit_out + (int64_t)(rows == 1 ? seq : 0) * c.max_pos, advance,
-                                        h->lm_wg_keys, n_wg));
+                                        h->lm_wg_keys, n_wg, nx));
     return TL_OK;
 }
 
@@ -563,14 +565,20 @@ int32_t check_model_loaded(tl_handle* h) {
     return TL_OK;
 }
 
-// one batch-1 decode step of sequence seq (row 0 of the workspaces): embed
-// the sequence's current token at its cursor, 22 fused layers, fused LM head +
-// argmax, then record the token and advance the cursor.  Every argument is a
-// fixed device pointer, so the step can be captured once and replayed.
+// one batch-1 decode step of sequence seq (row 0 of the workspaces): 22
+// fused layers over the embedding in row 0, fused LM head + argmax, then
+// record the token, advance the cursor and embed the new token in row 0 at
+// the new position for the next step (the first step's embedding comes from
+// decode_embed1).  Every argument is a fixed device pointer, so the step can
+// be captured once and replayed.
+int32_t decode_embed1(tl_handle* h) {
+    TL_LAUNCH(h, launch_embed_step(h->stream, h->token_cur, h->row_seq, 1, h->cursor, h->row_pos, h->D,
+                                   h->cfg.vocab, h->emb, h->emb_s, h->x));
+    return TL_OK;
+}
+
 int32_t decode_step1(tl_handle* h, int32_t seq, int32_t max_t) {
     const tl_config& c = h->cfg;
-    TL_LAUNCH(h, launch_embed_step(h->stream, h->token_cur, h->row_seq, 1, h->cursor, h->row_pos, h->D, c.vocab,
-                                   h->emb, h->emb_s, h->x));
     int32_t r;
     for (int l = 0; l < c.n_layers; l++)
         if ((r = layer_row1(h, l, max_t))) return r;
@@ -1290,6 +1298,7 @@ int32_t tl_decode(tl_handle* h, int32_t seq, int32_t max_new, int32_t eos_id, co
         return TL_OK;
     }
     if ((r = upload_rows(h, 1, seq, false, h->host_cursor[seq]))) return r;
+    if ((r = decode_embed1(h))) return r;
     for (int step = 0; step < max_new; step++) {
         if (abort_flag && *abort_flag) {
             if (stop_reason) *stop_reason = TL_STOP_HOST_ABORT;
