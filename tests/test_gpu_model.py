@@ -82,6 +82,28 @@ def test_generate_matches_oracle(small_model, persist, monkeypatch):
     eng.close()
 
 
+@DECODE_PATHS
+def test_interleaved_sequences_match_oracle(small_model, persist, monkeypatch):
+    """Batch-1 decode of two sequences in turns (3 steps of A, 5 of B, 4 of A,
+    2 of B): every call starts from its own sequence's token and cursor, so
+    each continuation equals the oracle's greedy generation of that prompt."""
+    monkeypatch.setenv("TL_PERSIST", persist)
+    eng = engine_for(small_model, max_seqs=2)
+    prompts = [np.array([5, 17, 1000, 3, 3, 2047, 64], np.int32), np.array([9, 8, 7, 300, 1], np.int32)]
+    got = [[], []]
+    for s, p in enumerate(prompts):
+        tok, _ = eng.prefill(p, seq=s)
+        got[s].append(tok)
+    for s, n in ((0, 3), (1, 5), (0, 4), (1, 2)):
+        toks, _ = eng.decode(n, seq=s)
+        got[s].extend(int(t) for t in toks)
+    orc = oracle.Oracle(small_model)
+    for s, p in enumerate(prompts):
+        want, _ = orc.generate(p, len(got[s]))
+        assert_bits_equal(np.array(got[s], np.int32), want, f"sequence {s}")
+    eng.close()
+
+
 def test_prefill_cache_equals_sequential_decode(small_model):
     """Rows of a prefill are the same rows sequential decode would produce."""
     m = small_model
