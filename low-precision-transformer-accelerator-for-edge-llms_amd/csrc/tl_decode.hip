@@ -18,6 +18,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "tl_device.h"
 #include "tl_internal.h"
@@ -555,20 +556,27 @@ __global__ __launch_bounds__(256) void attention_row_kernel(AttnDecodeArgs p) {
         if (lane == 0) bsum[b] = bs;
     }
     __syncthreads();
-    const float tot = ordered_sum(bsum, nblk);
+    const float tot = ordered_sum_aligned(bsum, nblk);   // bsum: 16-byte aligned, 16 bytes of slack
 
-    // 5) INT8 probabilities of this wavefront's keys, then P . V over the
-    //    same keys (lane <-> dimension; this row's V is v8 of lane d)
-    for (int b = wave; b < nblk; b += NW) {
-        const int t = b * 64 + lane;
-        int8_t pq = 0;
-        if (t < T) {
-            float pr = __builtin_rintf(__fdiv_rn(s_buf[t], tot) * 127.0f);
-            pr = pr < 0.0f ? 0.0f : (pr > 127.0f ? 127.0f : pr);
-            pq = (int8_t)(int)pr;
+    // 5) INT8 probabilities of this wavefront's keys (exponential / total,
+    //    correctly rounded: e <= 1 <= total keeps e y finite), then P . V over
+    //    the same keys (lane <-> dimension; this row's V is v8 of lane d)
+    const RnDiv dt = rn_div_prep(tot);
+    auto probs = [&](auto fast) {
+        for (int b = wave; b < nblk; b += NW) {
+            const int t = b * 64 + lane;
+            int8_t pq = 0;
+            if (t < T) {
+                const float q = decltype(fast)::value ? rn_div_fast(s_buf[t], dt) : __fdiv_rn(s_buf[t], tot);
+                float pr = __builtin_rintf(q * 127.0f);
+                pr = pr < 0.0f ? 0.0f : (pr > 127.0f ? 127.0f : pr);
+                pq = (int8_t)(int)pr;
+            }
+            p8[t] = pq;
         }
-        p8[t] = pq;
-    }
+    };
+    if (dt.fast) probs(std::true_type{});
+    else probs(std::false_type{});
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");   // p8 of these keys: this wavefront's
     int o = 0;
     const int cpos = pos >> 4, bpos = pos & 15;

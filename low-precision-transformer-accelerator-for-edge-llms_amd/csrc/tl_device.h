@@ -360,6 +360,20 @@ TL_DEV float ordered_sum(const float* v, int n) {
     return t;
 }
 
+// ordered_sum for 16-byte aligned v whose allocation holds 3 readable floats
+// past v[n - 1]: n <= 8 values come in one or two 16-byte reads
+TL_DEV float ordered_sum_aligned(const float* v, int n) {
+    if (n > 8) return ordered_sum(v, n);
+    const float4 a = *(const float4*)v;
+    const float4 b = n > 4 ? *(const float4*)(v + 4) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float r[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+        if (i < n) t = t + r[i];
+    return t;
+}
+
 // block-wide max of a non-negative float (all threads get the result)
 TL_DEV float block_max(float v, float* red /* >= 16 floats */) {
     v = wave_max_f32(v);
