@@ -17,6 +17,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "tl_device.h"
 #include "tl_internal.h"
@@ -574,33 +575,47 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(const float* __restrict__
                                                        int8_t* __restrict__ q8,
                                                        double* __restrict__ q_scale,
                                                        float* __restrict__ q_rot_out, int32_t append_kv) {
-    extern __shared__ float lds[];
+    extern __shared__ __align__(16) float lds[];
     __shared__ float red[16];
     const int row = blockIdx.x, tid = threadIdx.x;
-    const int D = n_heads * kHeadDim, KVD = n_kv * kHeadDim, W = D + 2 * KVD;
+    const int D = n_heads * kHeadDim, KVD = n_kv * kHeadDim, W = D + 2 * KVD;   // multiples of 64
     float* v = lds;          // [W] inputs
     float* o = lds + W;      // [D + KVD] rotated q, k
-    const float* src = qkv + (int64_t)row * W;
-    for (int i = tid; i < W; i += blockDim.x) v[i] = src[i];
+    const float4* src = (const float4*)(qkv + (int64_t)row * W);
+    for (int c = tid; c < W / 4; c += blockDim.x) ((float4*)v)[c] = src[c];
     __syncthreads();
     const int pos = rm.pos[row], seq = rm.seq[row];
     const float* cp = cosb + (int64_t)pos * kHeadDim;
     const float* sp = sinb + (int64_t)pos * kHeadDim;
+    // four dimensions d .. d + 3 per step, all on one side of d = 32
     float mx = 0.0f;
-    for (int i = tid; i < D + KVD; i += blockDim.x) {
-        const int d = i & 63;
-        const float rot = d < 32 ? -v[i + 32] : v[i - 32];
-        const float r = (v[i] * cp[d]) + (rot * sp[d]);
-        o[i] = r;
-        if (i < D) mx = fmaxf(mx, fabsf(r));
+    for (int c = tid; c < (D + KVD) / 4; c += blockDim.x) {
+        const int d = (4 * c) & 63;
+        const bool lo = d < 32;
+        const float4 x = ((const float4*)v)[c];
+        const float4 pr = ((const float4*)v)[lo ? c + 8 : c - 8];
+        const float4 cc = *(const float4*)(cp + d), ss = *(const float4*)(sp + d);
+        float4 r;
+        r.x = (x.x * cc.x) + ((lo ? -pr.x : pr.x) * ss.x);
+        r.y = (x.y * cc.y) + ((lo ? -pr.y : pr.y) * ss.y);
+        r.z = (x.z * cc.z) + ((lo ? -pr.z : pr.z) * ss.z);
+        r.w = (x.w * cc.w) + ((lo ? -pr.w : pr.w) * ss.w);
+        ((float4*)o)[c] = r;
+        if (4 * c < D) mx = fmaxf(mx, fmaxf(fmaxf(fabsf(r.x), fabsf(r.y)), fmaxf(fabsf(r.z), fabsf(r.w))));
     }
     mx = block_max(mx, red);  // includes the barrier that publishes o[]
     const double s = quant_scale(mx);
-    const float sf = (float)s;
-    for (int i = tid; i < D; i += blockDim.x) {
-        q8[(int64_t)row * D + i] = sat_i8(__builtin_rintf(__fdiv_rn(o[i], sf)));
-        if (q_rot_out) q_rot_out[(int64_t)row * D + i] = o[i];
-    }
+    // Q at the row's scale, four bytes per store; |q| <= max |q| keeps q y finite
+    const RnDiv dq = rn_div_prep((float)s);
+    auto qrow = [&](auto fast) {
+        for (int c = tid; c < D / 4; c += blockDim.x) {
+            const float4 r = ((const float4*)o)[c];
+            ((unsigned*)(q8 + (int64_t)row * D))[c] = quant4<decltype(fast)::value>(r, dq);
+            if (q_rot_out) ((float4*)(q_rot_out + (int64_t)row * D))[c] = r;
+        }
+    };
+    if (dq.fast) qrow(std::true_type{});
+    else qrow(std::false_type{});
     if (tid == 0) q_scale[row] = s;
     if (!append_kv) return;
     for (int i = tid; i < KVD; i += blockDim.x) {
