@@ -105,6 +105,25 @@ def test_rmsnorm_quant(rt, n, rows):
     assert_bits_equal(host(s2), want_s, "scale (no float output)")
 
 
+@pytest.mark.parametrize("gain", [1e-30, 2.0 ** -58, 1e30], ids=["tiny", "near_2^-64", "huge"])
+def test_rmsnorm_quant_extreme_scales(rt, gain):
+    """Row scales below 2^-64 and above 2^64 take the quantizer's correctly
+    rounded division; scales just above 2^-64 the reciprocal-and-corrections
+    path.  Both equal the oracle bit for bit (2048-wide rows: the fused
+    row prologue)."""
+    n, rows = 2048, 4
+    rng = np.random.default_rng(31)
+    x = (rng.standard_normal((rows, n)) * rng.uniform(0.5, 4, (rows, 1))).astype(F32)
+    g = ((1 + 0.1 * rng.standard_normal(n)) * gain).astype(F32)
+    want_q, want_s = oracle.quantize_rows(oracle.rms_norm(x, g, F32(1e-5)))
+    q, s = empty((rows, n), np.int8), empty(rows, np.float64)
+    rt.call("tl_rmsnorm_quant", dev(x), dev(g), rows, n, None, q, s)
+    assert_bits_equal(host(q), want_q, "q")
+    assert_bits_equal(host(s), want_s, "scale")
+    f32_scale = want_s.astype(np.float32)
+    assert ((f32_scale < 2.0 ** -64) | (f32_scale > 2.0 ** 64)).all() == (gain != 2.0 ** -58)
+
+
 def test_quantize_rows_and_tensor(rt):
     rng = np.random.default_rng(9)
     x = (rng.standard_normal((4, 5632)) * 3).astype(F32)
