@@ -86,9 +86,9 @@ TL_DEV int8_t sat_i8(float v) {
 // first leaves q within half an ulp plus 2^-46 relative of a / b (so
 // faithful); the second is Markstein's correction, which from a faithful q
 // and y within half an ulp of 1/b gives RN(a / b) exactly.  The proof needs
-// normal residuals: callers take this path only when rn_div_ok(b)
-// (|b| in [2^-64, 2^64]) and |a y| stays finite, and a correctly rounded
-// division otherwise.  A quotient below the normal range may differ in its
+// normal residuals: callers take this path only when RnDiv::fast (set by
+// rn_div_prep for |b| in [2^-64, 2^64]) and |a y| stays finite, and a
+// correctly rounded division otherwise.  A quotient below the normal range may differ in its
 // last bits; it rounds to integer 0 either way.
 struct RnDiv {
     float b, y;

@@ -565,18 +565,19 @@ int32_t check_model_loaded(tl_handle* h) {
     return TL_OK;
 }
 
-// one batch-1 decode step of sequence seq (row 0 of the workspaces): 22
-// fused layers over the embedding in row 0, fused LM head + argmax, then
-// record the token, advance the cursor and embed the new token in row 0 at
-// the new position for the next step (the first step's embedding comes from
-// decode_embed1).  Every argument is a fixed device pointer, so the step can
-// be captured once and replayed.
+// the embedding of row 0's sequence's current token at its cursor, before
+// the first step of a decode call (later steps get it from the step before)
 int32_t decode_embed1(tl_handle* h) {
     TL_LAUNCH(h, launch_embed_step(h->stream, h->token_cur, h->row_seq, 1, h->cursor, h->row_pos, h->D,
                                    h->cfg.vocab, h->emb, h->emb_s, h->x));
     return TL_OK;
 }
 
+// one batch-1 decode step of sequence seq (row 0 of the workspaces): 22
+// fused layers over the embedding in row 0, fused LM head + argmax, then
+// record the token, advance the cursor and embed the new token in row 0 at
+// the new position for the next step.  Every argument is a fixed device
+// pointer, so the step can be captured once and replayed.
 int32_t decode_step1(tl_handle* h, int32_t seq, int32_t max_t) {
     const tl_config& c = h->cfg;
     int32_t r;
