@@ -502,9 +502,11 @@ __global__ __launch_bounds__(256) void attention_row_kernel(AttnDecodeArgs p) {
     const float scl = (float)((s_q * (double)sk) * p.attn_scale);
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");   // qs, kn: written and read by this wavefront
 
-    // 3) scores of this wavefront's keys (lane <-> key)
+    // 3) scores of this wavefront's keys (lane <-> key); the head's INT8 Q
+    //    is read from LDS once (the score stores below could alias it)
     const v4i* q4 = (const v4i*)qs[wave];
     const v4i* kn4 = (const v4i*)kn[wave];
+    const v4i qa = q4[0], qb = q4[1], qc = q4[2], qd = q4[3];
     float lmax = -INFINITY;
     auto score_block = [&](int b, v4i k0, v4i k1, v4i k2, v4i k3) {
         const int t = b * 64 + lane;
@@ -515,10 +517,10 @@ __global__ __launch_bounds__(256) void attention_row_kernel(AttnDecodeArgs p) {
                 k2 = kn4[2];
                 k3 = kn4[3];
             }
-            int S = sdot4v(k0, q4[0], 0);
-            S = sdot4v(k1, q4[1], S);
-            S = sdot4v(k2, q4[2], S);
-            S = sdot4v(k3, q4[3], S);
+            int S = sdot4v(k0, qa, 0);
+            S = sdot4v(k1, qb, S);
+            S = sdot4v(k2, qc, S);
+            S = sdot4v(k3, qd, S);
             const float s = (float)S * scl;
             s_buf[t] = s;
             lmax = fmaxf(lmax, s);
