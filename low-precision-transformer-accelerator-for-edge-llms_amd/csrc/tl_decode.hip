@@ -201,6 +201,7 @@ __global__ __launch_bounds__(NW * 64) void attention_decode_kernel(AttnDecodeArg
     const int row = blockIdx.y;
     const int D = p.n_heads * kHeadDim, KVD = p.n_kv * kHeadDim, W = D + 2 * KVD;
     const int pos = p.rm.pos[row], seq = p.rm.seq[row];
+    if (pos < 0 || pos >= p.kv.max_pos) return;   // a row outside the cache (uniform per workgroup)
     const int T = pos + 1;
     const int tpad = (T + 63) & ~63;
     const int nblk = tpad >> 6;
@@ -437,6 +438,7 @@ __global__ __launch_bounds__(256) void attention_row_kernel(AttnDecodeArgs p) {
     const int g = h0 / G, row = blockIdx.y;
     const int D = p.n_heads * kHeadDim, KVD = p.n_kv * kHeadDim, W = D + 2 * KVD;
     const int pos = p.rm.pos[row], seq = p.rm.seq[row];
+    if (pos < 0 || pos >= p.kv.max_pos) return;   // a row outside the cache (uniform per workgroup)
     const int T = pos + 1, tpad = (T + 63) & ~63, nblk = tpad >> 6;
     const int64_t pl = p.kv.plane(seq, p.layer, g);
     const int8_t* kp = p.kv.k + pl;
@@ -647,6 +649,7 @@ __global__ __launch_bounds__(kGW * 64) void attention_group_kernel(AttnDecodeArg
     const int h0 = blockIdx.x * HPW, g = h0 / G, row = blockIdx.y;
     const int D = p.n_heads * kHeadDim, KVD = p.n_kv * kHeadDim, W = D + 2 * KVD;
     const int pos = p.rm.pos[row], seq = p.rm.seq[row];
+    if (pos < 0 || pos >= p.kv.max_pos) return;   // a row outside the cache (uniform per workgroup)
     const int T = pos + 1, tpad = (T + 63) & ~63, nblk = tpad >> 6, ngrp = tpad >> 4;
     const int64_t pl = p.kv.plane(seq, p.layer, g);
     const int8_t* kp = p.kv.k + pl;

@@ -585,6 +585,7 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(const float* __restrict__
     for (int c = tid; c < W / 4; c += blockDim.x) ((float4*)v)[c] = src[c];
     __syncthreads();
     const int pos = rm.pos[row], seq = rm.seq[row];
+    if (pos < 0 || pos >= kv.max_pos) return;   // a row outside the cache (uniform per workgroup)
     const float* cp = cosb + (int64_t)pos * kHeadDim;
     const float* sp = sinb + (int64_t)pos * kHeadDim;
     // four dimensions d .. d + 3 per step, all on one side of d = 32
@@ -654,6 +655,7 @@ __global__ __launch_bounds__(256) void attention_kernel(const int8_t* __restrict
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int G = n_heads / n_kv;
     const int pos = rm.pos[row], seq = rm.seq[row];
+    if (pos < 0 || pos >= kv.max_pos) return;   // a row outside the cache (uniform per workgroup)
     const int T = pos + 1;
     const int tpad = (T + 63) & ~63;
     const int nblk = tpad >> 6;
@@ -1060,6 +1062,8 @@ __global__ void reset_keys_kernel(unsigned long long* keys, int32_t n) {
 // With one row (single = one wavefront): the LM head may have left one key
 // per workgroup (wg_keys, folded here), and with x the new token's embedding
 // and position are written for the next step (what embed_step_kernel does).
+// With nx.stopped, a stopped sequence records nothing; the token that stopped
+// it is embedded again at the unchanged cursor.
 __global__ __launch_bounds__(64) void finalize_tokens_kernel(unsigned long long* keys, int32_t rows,
                                                              int32_t* token_cur, int32_t* tokens_out,
                                                              int32_t out_stride, int32_t* n_gen, int32_t* cursor,
@@ -1067,27 +1071,40 @@ __global__ __launch_bounds__(64) void finalize_tokens_kernel(unsigned long long*
                                                              const unsigned long long* wg_keys, int32_t n_wg,
                                                              EmbedNext nx) {
     const bool single = n_wg > 0 || nx.x != nullptr;
-    unsigned long long fold = 0;
-    if (n_wg > 0) {
-        for (int i = threadIdx.x; i < n_wg; i += 64) fold = max_u64(fold, wg_keys[i]);
-        fold = wave_max_u64(fold);
-    }
     const int r = single ? 0 : blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= rows) return;
-    const unsigned long long k = max_u64(keys[r], fold);   // every lane reads before lane 0 clears
-    const int32_t tok = key_index(k);
-    const int32_t cur = cursor[r] + advance;
-    if (!single || threadIdx.x == 0) {
-        token_cur[r] = tok;
-        const int32_t i = n_gen[r];
-        if (i >= 0 && i < out_stride) {
-            if (tokens_out) tokens_out[(int64_t)r * out_stride + i] = tok;
-            if (best_logit) best_logit[(int64_t)r * out_stride + i] = key_logit(k);
+    // every lane reads the flag before lane 0 may set it
+    const bool halted = single && nx.stopped != nullptr && *nx.stopped != 0;
+    int32_t tok, cur;
+    if (halted) {
+        tok = token_cur[r];
+        cur = cursor[r];
+        if (threadIdx.x == 0) {
+            keys[r] = 0ull;
+            if (nx.x) *nx.row_pos = cur;
         }
-        n_gen[r] = i + 1;
-        cursor[r] = cur;
-        keys[r] = 0ull;
-        if (nx.x) *nx.row_pos = cur;
+    } else {
+        unsigned long long fold = 0;
+        if (n_wg > 0) {
+            for (int i = threadIdx.x; i < n_wg; i += 64) fold = max_u64(fold, wg_keys[i]);
+            fold = wave_max_u64(fold);
+        }
+        const unsigned long long k = max_u64(keys[r], fold);   // every lane reads before lane 0 clears
+        tok = key_index(k);
+        cur = cursor[r] + advance;
+        if (!single || threadIdx.x == 0) {
+            token_cur[r] = tok;
+            const int32_t i = n_gen[r];
+            if (i >= 0 && i < out_stride) {
+                if (tokens_out) tokens_out[(int64_t)r * out_stride + i] = tok;
+                if (best_logit) best_logit[(int64_t)r * out_stride + i] = key_logit(k);
+            }
+            n_gen[r] = i + 1;
+            cursor[r] = cur;
+            keys[r] = 0ull;
+            if (nx.x) *nx.row_pos = cur;
+            if (single && nx.stopped && nx.eos && *nx.eos >= 0 && tok == *nx.eos) *nx.stopped = 1;
+        }
     }
     if (nx.x) {
         const bool ok = tok >= 0 && tok < nx.vocab;   // otherwise a zero row, as embed_step_kernel

@@ -45,6 +45,7 @@ struct LayerDev {
 };
 
 constexpr int kPersistChunk = 64;   // decode steps per persistent launch at most
+constexpr int kStopChunk = 16;      // decode steps replayed between reads of the stop flag
 constexpr int kPersistCounters = 8 * 8 * 32;   // phases x XCD slices x one 128-byte line
 
 struct ProfEvent {
@@ -93,6 +94,7 @@ struct tl_handle {
     int32_t* row_seq = nullptr;
     int32_t* row_pos = nullptr;
     int32_t* tokens = nullptr;    // [max_rows]
+    int8_t* kv_stage = nullptr;   // [2][max_pos][64] staging of tl_kv_write / tl_kv_read rows
     float* fscratch = nullptr;    // small scratch
     unsigned long long* op_key = nullptr;  // argmax slot of the standalone LM-head operator
     unsigned long long* lm_wg_keys = nullptr;  // [vocab / 4] batch-1 LM head: argmax key per workgroup
@@ -105,9 +107,12 @@ struct tl_handle {
     int32_t* token_cur = nullptr;
     int32_t* cursor = nullptr;
     int32_t* n_gen = nullptr;
+    int32_t* eos_id = nullptr;       // [max_seqs] EOS id the captured step checks (< 0: none)
+    int32_t* stopped = nullptr;      // [max_seqs] set on the device when the EOS token is recorded
     int32_t* tokens_out = nullptr;   // [max_seqs][max_pos]
     float* logit_out = nullptr;      // [max_seqs][max_pos]
     std::vector<int32_t> host_cursor;
+    int32_t stop_state[2] = {-1, 0};  // host words copied into eos_id / stopped
     std::vector<int32_t> host_ngen;
 
     std::vector<void*> allocs;
@@ -500,7 +505,7 @@ int32_t lm_head_rows(tl_handle* h, const float* xrow, int32_t rows, int32_t seq,
     unsigned long long* keys = h->keys + (rows == 1 ? seq : 0);
     int32_t n_wg = 0;   // rows == 1: the finalize kernel folds one key per LM-head workgroup
     EmbedNext nx{};     // rows == 1: and embeds the new token into row 0 for the next step
-    if (rows == 1) nx = EmbedNext{h->emb, h->emb_s, h->D, c.vocab, h->x, h->row_pos};
+    if (rows == 1) nx = EmbedNext{h->emb, h->emb_s, h->D, c.vocab, h->x, h->row_pos, h->eos_id + seq, h->stopped + seq};
     if (rows == 1) {
         GemvArgs g = gemv_args(h);
         g.xf = xrow; g.gamma = h->g_final; g.w = h->lm_w; g.ws = h->lm_s; g.key = keys; g.n = V; g.k = D;
@@ -555,6 +560,17 @@ int32_t upload_rows(tl_handle* h, int32_t rows, int32_t seq_first, bool seq_per_
     TL_HIP(h, hipMemcpyAsync(h->row_seq, s.data(), rows * sizeof(int32_t), hipMemcpyHostToDevice, h->stream));
     TL_HIP(h, hipMemcpyAsync(h->row_pos, p.data(), rows * sizeof(int32_t), hipMemcpyHostToDevice, h->stream));
     // the host vectors must outlive the async copies
+    TL_HIP(h, hipStreamSynchronize(h->stream));
+    return TL_OK;
+}
+
+// the EOS id a sequence's decode steps check, and its stop flag cleared
+int32_t set_stop_state(tl_handle* h, int32_t seq, int32_t eos_id) {
+    h->stop_state[0] = eos_id < 0 ? -1 : eos_id;
+    h->stop_state[1] = 0;
+    TL_HIP(h, hipMemcpyAsync(h->eos_id + seq, &h->stop_state[0], sizeof(int32_t), hipMemcpyHostToDevice, h->stream));
+    TL_HIP(h, hipMemcpyAsync(h->stopped + seq, &h->stop_state[1], sizeof(int32_t), hipMemcpyHostToDevice, h->stream));
+    // the host words must stay unchanged until the copies have run
     TL_HIP(h, hipStreamSynchronize(h->stream));
     return TL_OK;
 }
@@ -732,7 +748,8 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
         (e = dalloc(h, &h->fscratch, 64)) || (e = dalloc(h, &h->op_key, 1)) || (e = dalloc(h, &h->keys, (size_t)max_seqs)) ||
         (e = dalloc(h, &h->lm_wg_keys, (size_t)(c.vocab + 3) / 4)) ||
         (e = dalloc(h, &h->token_cur, (size_t)max_seqs)) || (e = dalloc(h, &h->cursor, (size_t)max_seqs)) ||
-        (e = dalloc(h, &h->n_gen, (size_t)max_seqs)) ||
+        (e = dalloc(h, &h->n_gen, (size_t)max_seqs)) || (e = dalloc(h, &h->eos_id, (size_t)max_seqs)) ||
+        (e = dalloc(h, &h->stopped, (size_t)max_seqs)) ||
         (e = dalloc(h, &h->tokens_out, (size_t)max_seqs * c.max_pos)) ||
         (e = dalloc(h, &h->logit_out, (size_t)max_seqs * c.max_pos)) ||
         (e = dalloc(h, &h->rope_cos, (size_t)c.max_pos * kHeadDim)) ||
@@ -741,7 +758,8 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
         (e = dalloc(h, &h->kv_sv, (size_t)c.n_layers * c.n_kv_heads)) ||
         (e = dalloc(h, &h->g_final, (size_t)D)) || (e = dalloc(h, &h->lm_w, (size_t)c.vocab * D)) ||
         (e = dalloc(h, &h->lm_s, (size_t)c.vocab)) || (e = dalloc(h, &h->emb, (size_t)c.vocab * D)) ||
-        (e = dalloc(h, &h->emb_s, (size_t)c.vocab)))
+        (e = dalloc(h, &h->emb_s, (size_t)c.vocab)) ||
+        (e = dalloc(h, &h->kv_stage, (size_t)2 * c.max_pos * kHeadDim)))
         return bad(e);
     const size_t plane = (size_t)c.max_pos * kHeadDim;
     const size_t kv_bytes = (size_t)max_seqs * c.n_layers * c.n_kv_heads * plane;
@@ -769,6 +787,8 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
         (e = hipMemsetAsync(h->keys, 0, sizeof(unsigned long long) * max_seqs, h->stream)) ||
         (e = hipMemsetAsync(h->cursor, 0, sizeof(int32_t) * max_seqs, h->stream)) ||
         (e = hipMemsetAsync(h->n_gen, 0, sizeof(int32_t) * max_seqs, h->stream)) ||
+        (e = hipMemsetAsync(h->eos_id, 0xFF, sizeof(int32_t) * max_seqs, h->stream)) ||
+        (e = hipMemsetAsync(h->stopped, 0, sizeof(int32_t) * max_seqs, h->stream)) ||
         (e = hipMemsetAsync(h->tile_ctr, 0, sizeof(unsigned) * kSkinnyTiles, h->stream)))
         return bad(e);
     std::vector<float> cs, sn;
@@ -922,26 +942,16 @@ int32_t tl_kv_write(tl_handle* h, int32_t seq, int32_t layer, int32_t g, int32_t
     const tl_config& c = h->cfg;
     TL_REQ(h, seq >= 0 && seq < h->max_seqs && layer >= 0 && layer < c.n_layers && g >= 0 && g < c.n_kv_heads,
            "KV index out of range");
-    TL_REQ(h, t0 >= 0 && n >= 0 && t0 + n <= c.max_pos, "KV token range out of bounds");
+    TL_REQ(h, t0 >= 0 && n >= 0 && (int64_t)t0 + n <= c.max_pos, "KV token range out of bounds");
     if (n == 0) return TL_OK;
+    // rows pass through the handle's staging buffer (n <= max_pos rows each)
     const size_t bytes = (size_t)n * kHeadDim;
-    int8_t* kd = nullptr;
-    int8_t* vd = nullptr;
-    TL_HIP(h, hipMalloc(&kd, bytes));
-    hipError_t e = hipMalloc(&vd, bytes);
-    if (e != hipSuccess) {
-        hipFree(kd);
-        return fail(h, TL_ERR_INTERNAL, "hipMalloc");
-    }
-    int32_t rc = TL_OK;
-    if (k_rows && hipMemcpy(kd, k_rows, bytes, hipMemcpyHostToDevice) != hipSuccess) rc = TL_ERR_INTERNAL;
-    if (v_rows && hipMemcpy(vd, v_rows, bytes, hipMemcpyHostToDevice) != hipSuccess) rc = TL_ERR_INTERNAL;
-    if (!rc && launch_kv_scatter(h->stream, h->kv, seq, layer, g, t0, n, k_rows ? kd : nullptr, v_rows ? vd : nullptr) != hipSuccess)
-        rc = TL_ERR_INTERNAL;
-    if (!rc) rc = finish(h);
-    hipFree(kd);
-    hipFree(vd);
-    return rc ? fail(h, rc, h->err.empty() ? "kv write failed" : h->err) : TL_OK;
+    int8_t* kd = h->kv_stage;
+    int8_t* vd = h->kv_stage + (size_t)c.max_pos * kHeadDim;
+    if (k_rows) TL_HIP(h, hipMemcpyAsync(kd, k_rows, bytes, hipMemcpyHostToDevice, h->stream));
+    if (v_rows) TL_HIP(h, hipMemcpyAsync(vd, v_rows, bytes, hipMemcpyHostToDevice, h->stream));
+    TL_LAUNCH(h, launch_kv_scatter(h->stream, h->kv, seq, layer, g, t0, n, k_rows ? kd : nullptr, v_rows ? vd : nullptr));
+    return finish(h);
 }
 
 int32_t tl_kv_read(tl_handle* h, int32_t seq, int32_t layer, int32_t g, int32_t t0, int32_t n,
@@ -950,25 +960,15 @@ int32_t tl_kv_read(tl_handle* h, int32_t seq, int32_t layer, int32_t g, int32_t 
     const tl_config& c = h->cfg;
     TL_REQ(h, seq >= 0 && seq < h->max_seqs && layer >= 0 && layer < c.n_layers && g >= 0 && g < c.n_kv_heads,
            "KV index out of range");
-    TL_REQ(h, t0 >= 0 && n >= 0 && t0 + n <= c.max_pos, "KV token range out of bounds");
+    TL_REQ(h, t0 >= 0 && n >= 0 && (int64_t)t0 + n <= c.max_pos, "KV token range out of bounds");
     if (n == 0) return TL_OK;
     const size_t bytes = (size_t)n * kHeadDim;
-    int8_t* kd = nullptr;
-    int8_t* vd = nullptr;
-    TL_HIP(h, hipMalloc(&kd, bytes));
-    hipError_t e = hipMalloc(&vd, bytes);
-    if (e != hipSuccess) {
-        hipFree(kd);
-        return fail(h, TL_ERR_INTERNAL, "hipMalloc");
-    }
-    int32_t rc = TL_OK;
-    if (launch_kv_gather(h->stream, h->kv, seq, layer, g, t0, n, kd, vd) != hipSuccess) rc = TL_ERR_INTERNAL;
-    if (!rc) rc = finish(h);
-    if (!rc && k_rows && hipMemcpy(k_rows, kd, bytes, hipMemcpyDeviceToHost) != hipSuccess) rc = TL_ERR_INTERNAL;
-    if (!rc && v_rows && hipMemcpy(v_rows, vd, bytes, hipMemcpyDeviceToHost) != hipSuccess) rc = TL_ERR_INTERNAL;
-    hipFree(kd);
-    hipFree(vd);
-    return rc ? fail(h, rc, h->err.empty() ? "kv read failed" : h->err) : TL_OK;
+    int8_t* kd = h->kv_stage;
+    int8_t* vd = h->kv_stage + (size_t)c.max_pos * kHeadDim;
+    TL_LAUNCH(h, launch_kv_gather(h->stream, h->kv, seq, layer, g, t0, n, kd, vd));
+    if (k_rows) TL_HIP(h, hipMemcpyAsync(k_rows, kd, bytes, hipMemcpyDeviceToHost, h->stream));
+    if (v_rows) TL_HIP(h, hipMemcpyAsync(v_rows, vd, bytes, hipMemcpyDeviceToHost, h->stream));
+    return finish(h);
 }
 
 // ---- operators ----------------------------------------------------------------
@@ -1085,7 +1085,8 @@ int32_t tl_qkv_append(tl_handle* h, int32_t seq, int32_t layer, int32_t pos0, in
     if (!h) return TL_ERR_BAD_DESCRIPTOR;
     const tl_config& c = h->cfg;
     TL_REQ(h, seq >= 0 && seq < h->max_seqs && layer >= 0 && layer < c.n_layers, "index out of range");
-    TL_REQ(h, rows >= 1 && rows <= h->max_rows && pos0 >= 0 && pos0 + rows <= c.max_pos, "position range out of bounds");
+    TL_REQ(h, rows >= 1 && rows <= h->max_rows && pos0 >= 0 && (int64_t)pos0 + rows <= c.max_pos,
+           "position range out of bounds");
     TL_REQ(h, qkv && q8 && q_scale, "null pointer");
     int32_t r = upload_rows(h, rows, seq, false, pos0);
     if (r) return r;
@@ -1099,7 +1100,8 @@ int32_t tl_attention(tl_handle* h, int32_t seq, int32_t layer, int32_t pos0, int
     if (!h) return TL_ERR_BAD_DESCRIPTOR;
     const tl_config& c = h->cfg;
     TL_REQ(h, seq >= 0 && seq < h->max_seqs && layer >= 0 && layer < c.n_layers, "index out of range");
-    TL_REQ(h, rows >= 1 && rows <= h->max_rows && pos0 >= 0 && pos0 + rows <= c.max_pos, "position range out of bounds");
+    TL_REQ(h, rows >= 1 && rows <= h->max_rows && pos0 >= 0 && (int64_t)pos0 + rows <= c.max_pos,
+           "position range out of bounds");
     TL_REQ(h, q8 && q_scale && out, "null pointer");
     int32_t r = upload_rows(h, rows, seq, false, pos0);
     if (r) return r;
@@ -1182,6 +1184,7 @@ int32_t prefill_layers(tl_handle* h, int32_t seq, const int32_t* tokens, int32_t
     TL_HIP(h, hipMemcpyAsync(h->n_gen + seq, &zero, sizeof zero, hipMemcpyHostToDevice, h->stream));
     TL_HIP(h, hipMemcpyAsync(h->cursor + seq, &n, sizeof n, hipMemcpyHostToDevice, h->stream));
     TL_LAUNCH(h, launch_reset_keys(h->stream, h->keys + seq, 1));
+    if ((r = set_stop_state(h, seq, -1))) return r;
     TL_LAUNCH(h, launch_embed(h->stream, h->tokens, n, h->D, h->cfg.vocab, h->emb, h->emb_s, h->x));
     for (int l = 0; l < c.n_layers; l++)
         if ((r = layer_rows(h, l, n, n, false))) return r;
@@ -1233,7 +1236,7 @@ int32_t tl_layer_rows(tl_handle* h, int32_t seq, int32_t layer, int32_t pos0, in
     const tl_config& c = h->cfg;
     TL_REQ(h, seq >= 0 && seq < h->max_seqs && layer >= 0 && layer < c.n_layers, "index out of range");
     TL_REQ(h, rows >= 1 && rows <= h->max_rows, "row count out of range");
-    TL_REQ(h, pos0 >= 0 && pos0 + rows <= c.max_pos, "Sequence length exceeds max_position_embeddings");
+    TL_REQ(h, pos0 >= 0 && (int64_t)pos0 + rows <= c.max_pos, "Sequence length exceeds max_position_embeddings");
     TL_REQ(h, x, "null pointer");
     if (!h->layers[layer].wqkv) return fail(h, TL_ERR_BAD_DESCRIPTOR, "layer not loaded");
     int32_t r = upload_rows(h, rows, seq, false, pos0);
@@ -1261,10 +1264,9 @@ int32_t tl_decode(tl_handle* h, int32_t seq, int32_t max_new, int32_t eos_id, co
     TL_REQ(h, max_new >= 1, "--max-tokens must be at least 1");
     TL_REQ(h, tokens_out && n_out, "null pointer");
     TL_REQ(h, h->host_ngen[seq] >= 1, "tl_decode needs a prefilled sequence");
-    TL_REQ(h, h->host_cursor[seq] + max_new <= c.max_pos, "Sequence length exceeds max_position_embeddings");
+    TL_REQ(h, (int64_t)h->host_cursor[seq] + max_new <= c.max_pos, "Sequence length exceeds max_position_embeddings");
     *n_out = 0;
     if (stop_reason) *stop_reason = TL_STOP_NONE;
-    const bool per_step = eos_id >= 0 || abort_flag;
     const int32_t first = h->host_ngen[seq];
     int32_t r;
     if (h->use_persist && h->persist_ok && !h->profiling) {
@@ -1298,38 +1300,53 @@ int32_t tl_decode(tl_handle* h, int32_t seq, int32_t max_new, int32_t eos_id, co
             *stop_reason = (eos_id >= 0 && done > 0 && tokens_out[done - 1] == eos_id) ? TL_STOP_EOS : TL_STOP_MAX_TOKENS;
         return TL_OK;
     }
+    // graph replays (or direct launches) in chunks: with an EOS id or an abort
+    // flag the stop flag the step sets on the device is read once per chunk
+    // (kStopChunk steps); steps replayed after the stop record nothing
+    if ((r = set_stop_state(h, seq, eos_id))) return r;
     if ((r = upload_rows(h, 1, seq, false, h->host_cursor[seq]))) return r;
     if ((r = decode_embed1(h))) return r;
-    for (int step = 0; step < max_new; step++) {
+    const bool watch = eos_id >= 0 || abort_flag;
+    const int32_t chunk = watch ? kStopChunk : max_new;
+    int32_t launched = 0;
+    bool eos_seen = false, aborted = false;
+    while (launched < max_new) {
         if (abort_flag && *abort_flag) {
-            if (stop_reason) *stop_reason = TL_STOP_HOST_ABORT;
+            aborted = true;
             break;
         }
-        if (h->use_graphs && !h->profiling) {
-            if ((r = decode_graph_launch(h, seq))) return r;
-        } else if ((r = decode_step1(h, seq, h->host_cursor[seq] + 1))) {
-            return r;
+        const int32_t cnt = std::min(chunk, max_new - launched);
+        for (int32_t i = 0; i < cnt; i++) {
+            if (h->use_graphs && !h->profiling) {
+                if ((r = decode_graph_launch(h, seq))) return r;
+            } else if ((r = decode_step1(h, seq, h->host_cursor[seq] + launched + i + 1))) {
+                return r;
+            }
         }
-        h->host_cursor[seq] += 1;
-        h->host_ngen[seq] += 1;
-        *n_out = step + 1;
-        if (per_step) {
-            int32_t tok = -1;
-            TL_HIP(h, hipMemcpyAsync(&tok, h->tokens_out + (size_t)seq * c.max_pos + first + step, sizeof tok,
-                                     hipMemcpyDeviceToHost, h->stream));
+        launched += cnt;
+        if (watch) {
+            TL_HIP(h, hipMemcpyAsync(&h->stop_state[1], h->stopped + seq, sizeof(int32_t), hipMemcpyDeviceToHost,
+                                     h->stream));
             if ((r = finish(h))) return r;
-            tokens_out[step] = tok;
-            if (eos_id >= 0 && tok == eos_id) {
-                if (stop_reason) *stop_reason = TL_STOP_EOS;
-                return TL_OK;
+            if (h->stop_state[1]) {
+                eos_seen = true;
+                break;
             }
         }
     }
+    int32_t ngen = 0;
+    TL_HIP(h, hipMemcpyAsync(&ngen, h->n_gen + seq, sizeof ngen, hipMemcpyDeviceToHost, h->stream));
     if ((r = finish(h))) return r;
-    if (!per_step && *n_out > 0)
-        TL_HIP(h, hipMemcpy(tokens_out, h->tokens_out + (size_t)seq * c.max_pos + first, sizeof(int32_t) * *n_out,
+    const int32_t got = ngen - first;
+    if (got < 0 || got > launched) return fail(h, TL_ERR_INTERNAL, "decode: device token count out of range");
+    h->host_cursor[seq] += got;
+    h->host_ngen[seq] += got;
+    *n_out = got;
+    if (got > 0)
+        TL_HIP(h, hipMemcpy(tokens_out, h->tokens_out + (size_t)seq * c.max_pos + first, sizeof(int32_t) * got,
                             hipMemcpyDeviceToHost));
-    if (stop_reason && *stop_reason == TL_STOP_NONE) *stop_reason = TL_STOP_MAX_TOKENS;
+    if (stop_reason)
+        *stop_reason = eos_seen ? TL_STOP_EOS : (aborted ? TL_STOP_HOST_ABORT : TL_STOP_MAX_TOKENS);
     return TL_OK;
 }
 
@@ -1339,7 +1356,7 @@ int32_t tl_generate(tl_handle* h, int32_t seq, const int32_t* prompt, int32_t n_
     TL_REQ(h, max_new >= 1, "--max-tokens must be at least 1");
     TL_REQ(h, tokens_out && n_out, "null pointer");
     TL_REQ(h, prompt && n_prompt >= 1, "Input token sequence is empty");
-    TL_REQ(h, n_prompt + max_new - 1 <= h->cfg.max_pos, "Sequence length exceeds max_position_embeddings");
+    TL_REQ(h, (int64_t)n_prompt + max_new - 1 <= h->cfg.max_pos, "Sequence length exceeds max_position_embeddings");
     *n_out = 0;
     if (stop_reason) *stop_reason = TL_STOP_NONE;
     if (abort_flag && *abort_flag) {
@@ -1374,7 +1391,8 @@ int32_t tl_decode_batch(tl_handle* h, int32_t n_seqs, const int32_t* tokens, con
     int32_t max_t = 0;
     for (int b = 0; b < n_seqs; b++) {
         TL_REQ(h, tokens[b] >= 0 && tokens[b] < c.vocab, "token id out of range");
-        TL_REQ(h, start_pos[b] >= 0 && start_pos[b] + n_steps <= c.max_pos, "Sequence length exceeds max_position_embeddings");
+        TL_REQ(h, start_pos[b] >= 0 && (int64_t)start_pos[b] + n_steps <= c.max_pos,
+               "Sequence length exceeds max_position_embeddings");
         max_t = std::max(max_t, start_pos[b] + n_steps);
     }
     int32_t r = check_model_loaded(h);
@@ -1497,9 +1515,10 @@ int32_t tl_capture_step(tl_handle* h, int32_t seq, tl_capture* cap) {
     TL_REQ(h, pos + 1 <= c.max_pos, "Sequence length exceeds max_position_embeddings");
     TL_REQ(h, cap->key0 >= 0 && cap->key0 <= pos + 1, "attention window outside keys 0..pos");
     if (cap->n_keys < 0) cap->n_keys = pos + 1 - cap->key0;
-    TL_REQ(h, cap->key0 + cap->n_keys <= pos + 1, "attention window outside keys 0..pos");
+    TL_REQ(h, cap->n_keys >= 0 && (int64_t)cap->key0 + cap->n_keys <= pos + 1, "attention window outside keys 0..pos");
     int32_t r = check_model_loaded(h);
     if (r) return r;
+    if ((r = set_stop_state(h, seq, -1))) return r;
     const int D = h->D, V = c.vocab;
     const int32_t first = h->host_ngen[seq];
     CaptureScratch sc(h->stream);

@@ -12,6 +12,7 @@ memory (``data_ptr()`` handed to the library).
 from __future__ import annotations
 
 import ctypes as C
+from types import SimpleNamespace
 
 import numpy as np
 
@@ -66,6 +67,57 @@ class Engine:
             sin = model.rope_sin
         self.set_rope_table(cos, sin)
         return self
+
+    def load_random(self, seed: int, kv_range=(0.02, 0.06)) -> SimpleNamespace:
+        """Load a seeded random-init model of this engine's geometry and return
+        host copies of what was loaded (the attributes ``load_model`` reads).
+
+        Float weights are drawn N(0, 0.02) on the device (torch's generator,
+        plumbing only) and quantized per output channel by the library's own
+        ``tl_quantize_weight_rows``; RMSNorm gains are N(1, 0.02); static KV
+        scales are uniform in ``kv_range`` (NumPy generator of the same seed).
+        Drawing 1.1 G weights on the device takes well under a second, which
+        is what makes full-size runs practical."""
+        import torch
+        g = torch.Generator(device="cuda")
+        g.manual_seed(int(seed))
+        c = self.cfg
+        D, F, V = c["hidden"], c["intermediate"], c["vocab"]
+        kvd = c["n_kv_heads"] * c["head_dim"]
+        shapes = [(D, D), (kvd, D), (kvd, D), (D, D), (F, D), (F, D), (D, F)]
+
+        def qrows(rows, cols):
+            w = torch.randn(rows, cols, generator=g, device="cuda", dtype=torch.float32) * 0.02
+            q = torch.empty(rows, cols, dtype=torch.int8, device="cuda")
+            sc = torch.empty(rows, dtype=torch.float32, device="cuda")
+            self.rt.call("tl_quantize_weight_rows", w, rows, cols, q, sc)
+            return q, sc
+
+        def gains():
+            return 1.0 + 0.02 * torch.randn(D, generator=g, device="cuda")
+
+        host_layers = []
+        for layer in range(c["n_layers"]):
+            ws, ss = zip(*[qrows(*shp) for shp in shapes])
+            L = dict(w=list(ws), s=list(ss), g_in=gains(), g_post=gains())
+            self.load_layer(layer, L)
+            host_layers.append(dict(w=[t.cpu().numpy() for t in L["w"]], s=[t.cpu().numpy() for t in L["s"]],
+                                    g_in=L["g_in"].cpu().numpy(), g_post=L["g_post"].cpu().numpy()))
+        lm_w, lm_s = qrows(V, D)
+        emb, emb_s = qrows(V, D)
+        g_final = gains()
+        self.load_lm_head(lm_w, lm_s, g_final)
+        self.load_embedding(emb, emb_s)
+        rng = np.random.default_rng(int(seed))
+        sk = rng.uniform(*kv_range, (c["n_layers"], c["n_kv_heads"])).astype(np.float32)
+        sv = rng.uniform(*kv_range, (c["n_layers"], c["n_kv_heads"])).astype(np.float32)
+        self.set_kv_scales(sk, sv)
+        cos, sin = build_rope_cache(c["max_pos"], c["head_dim"], c["rope_theta"])
+        self.set_rope_table(cos, sin)
+        torch.cuda.synchronize()
+        return SimpleNamespace(cfg=dict(c), layers=host_layers, lm_w=lm_w.cpu().numpy(), lm_s=lm_s.cpu().numpy(),
+                               g_final=g_final.cpu().numpy(), emb=emb.cpu().numpy(), emb_s=emb_s.cpu().numpy(),
+                               rope_cos=cos, rope_sin=sin, kv_sk=sk, kv_sv=sv)
 
     def load_layer(self, i: int, L) -> None:
         w = [self._keep(t, np.int8) for t in L["w"]]

@@ -99,6 +99,9 @@ def lib() -> C.CDLL:
                                              _i8p, _i8p, _f32p]),
             "or_generate": (C.c_int32, [C.POINTER(OrModel), _i32p, C.c_int32, C.c_int32, C.c_int32,
                                         C.c_int32, _i8p, _i8p, _i32p, _f32p]),
+            "or_decode_rows": (None, [C.POINTER(OrModel), C.c_int32, C.c_int32, _i32p, _f32p,
+                                      C.POINTER(_i8p), C.POINTER(_i8p)]),
+            "or_lm_head_rows": (None, [C.POINTER(OrModel), C.c_int32, _f32p, _i32p, _f32p]),
             "or_set_threads": (None, [C.c_int32]),
             "or_get_threads": (C.c_int32, []),
         }
@@ -307,6 +310,55 @@ class Oracle:
         lib().or_decode_row(C.byref(self.cm), layer, pos, ptr(x, C.c_float), ptr(kc, C.c_int8),
                             ptr(vc, C.c_int8), C.byref(tr) if tr is not None else None)
         return x
+
+    def decode_rows(self, layer, pos, x, caches):
+        """or_decode_rows: rows x[r] (updated in place, float32 [rows][D]) at
+        positions pos[r] of the sequences whose (K, V) caches are caches[r]."""
+        pos = np.ascontiguousarray(pos, np.int32)
+        assert x.dtype == np.float32 and x.flags["C_CONTIGUOUS"] and x.shape[0] == pos.size == len(caches)
+        kp = (_i8p * pos.size)(*[ptr(k, C.c_int8) for k, _ in caches])
+        vp = (_i8p * pos.size)(*[ptr(v, C.c_int8) for _, v in caches])
+        lib().or_decode_rows(C.byref(self.cm), layer, pos.size, ptr(pos, C.c_int32), ptr(x, C.c_float), kp, vp)
+        return x
+
+    def lm_head_rows(self, x):
+        """or_lm_head_rows: greedy token and its logit for every row of x."""
+        x = f32(x)
+        rows = x.shape[0]
+        tok = np.empty(rows, np.int32)
+        lg = np.empty(rows, np.float32)
+        lib().or_lm_head_rows(C.byref(self.cm), rows, ptr(x, C.c_float), ptr(tok, C.c_int32), ptr(lg, C.c_float))
+        return tok, lg
+
+    def prefill(self, prompt, cache):
+        """Every prompt row through every layer (layer-major), then the LM head
+        of the last row: (next token, its logit); the prompt's K/V rows land
+        in cache."""
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        x = np.stack([self.embed(int(t)) for t in prompt]).astype(np.float32)
+        pos = np.arange(prompt.size, dtype=np.int32)
+        caches = [cache] * prompt.size
+        for layer in range(self.a.cfg["n_layers"]):
+            self.decode_rows(layer, pos, x, caches)
+        tok, lg = self.lm_head_rows(x[-1:])
+        return int(tok[0]), float(lg[0])
+
+    def generate_layer_major(self, prompt, max_new, cache=None):
+        """Greedy generation whose prompt runs layer-major (prefill) and whose
+        new tokens run one row at a time: the same ids and cache rows as
+        generate(), faster for long prompts."""
+        kc, vc = cache if cache is not None else self.a.new_cache()
+        tok, _ = self.prefill(prompt, (kc, vc))
+        out = [tok]
+        pos = len(prompt)
+        while len(out) < max_new:
+            x = self.embed(out[-1])[None, :].copy()
+            for layer in range(self.a.cfg["n_layers"]):
+                self.decode_rows(layer, [pos], x, [(kc, vc)])
+            t, _ = self.lm_head_rows(x)
+            out.append(int(t[0]))
+            pos += 1
+        return np.array(out, np.int32)
 
     def embed(self, tok):
         x = np.empty(self.a.cfg["hidden"], np.float32)

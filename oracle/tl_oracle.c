@@ -42,6 +42,9 @@
  *   or_decode_row                  vs golden mixed_precision_decoder_layer at one
  *                                  token within tolerance
  *   or_lm_head_argmax              argmax_reduction KATs (lower id wins a tie)
+ *   or_decode_rows, or_lm_head_rows  bit-exact vs or_decode_row / or_lm_head_argmax
+ *                                  row by row (prompt rows of one sequence and
+ *                                  rows of different sequences)
  */
 #include "tl_oracle.h"
 
@@ -150,7 +153,25 @@ void or_gemm_i8(const int8_t *a, const int8_t *w, int32_t m, int32_t n, int32_t 
 #pragma omp parallel for schedule(static)
     for (int32_t j = 0; j < n; j++) {
         const int8_t *wr = w + (int64_t)j * k;
-        for (int32_t i = 0; i < m; i++) {
+        int32_t i = 0;
+        /* four rows per pass over the weight row (exact integer sums, so the
+         * grouping changes nothing but speed) */
+        for (; i + 4 <= m; i += 4) {
+            const int8_t *a0 = a + (int64_t)i * k, *a1 = a0 + k, *a2 = a1 + k, *a3 = a2 + k;
+            int32_t s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+            for (int32_t t = 0; t < k; t++) {
+                const int32_t wv = wr[t];
+                s0 += (int32_t)a0[t] * wv;
+                s1 += (int32_t)a1[t] * wv;
+                s2 += (int32_t)a2[t] * wv;
+                s3 += (int32_t)a3[t] * wv;
+            }
+            c[(int64_t)i * n + j] = s0;
+            c[(int64_t)(i + 1) * n + j] = s1;
+            c[(int64_t)(i + 2) * n + j] = s2;
+            c[(int64_t)(i + 3) * n + j] = s3;
+        }
+        for (; i < m; i++) {
             const int8_t *ar = a + (int64_t)i * k;
             int32_t s = 0;
             for (int32_t t = 0; t < k; t++) s += (int32_t)ar[t] * (int32_t)wr[t];
@@ -342,6 +363,7 @@ void or_attention_row(const or_config *cfg, int32_t layer, int32_t pos,
                       float *attended, int32_t *scores, int8_t *probs, int32_t *pv_acc) {
     const int32_t hd = cfg->head_dim, hq = cfg->n_heads, hkv = cfg->n_kv_heads;
     const int32_t groups = hq / hkv, n = pos + 1;
+    if (hd > 256) abort();
     const double attn_scale = 1.0 / sqrt((double)hd);
     int32_t *S = (int32_t *)malloc(sizeof(int32_t) * (size_t)n);
     float *s = (float *)malloc(sizeof(float) * (size_t)n);
@@ -363,11 +385,19 @@ void or_attention_row(const or_config *cfg, int32_t layer, int32_t pos,
         or_softmax_row(s, n, p);
         or_quantize_probs(p, n, p8);
         const float pv_mult = or_dequant_mult(1.0 / 127.0, (double)sv);
+        /* integer sums are exact, so visiting the keys row by row (the cache's
+         * contiguous order) gives the same accumulators as any other order */
+        int32_t acc[256];
+        for (int32_t d = 0; d < hd; d++) acc[d] = 0;
+        for (int32_t t = 0; t < n; t++) {
+            const int8_t *vr = vb + (int64_t)t * hd;
+            const int32_t pt = p8[t];
+            if (pt == 0) continue;
+            for (int32_t d = 0; d < hd; d++) acc[d] += pt * (int32_t)vr[d];
+        }
         for (int32_t d = 0; d < hd; d++) {
-            int32_t acc = 0;
-            for (int32_t t = 0; t < n; t++) acc += (int32_t)p8[t] * (int32_t)vb[(int64_t)t * hd + d];
-            if (pv_acc) pv_acc[h * hd + d] = acc;
-            attended[h * hd + d] = (float)acc * pv_mult;
+            if (pv_acc) pv_acc[h * hd + d] = acc[d];
+            attended[h * hd + d] = (float)acc[d] * pv_mult;
         }
         if (scores) memcpy(scores + (int64_t)h * n, S, sizeof(int32_t) * (size_t)n);
         if (probs) memcpy(probs + (int64_t)h * n, p8, (size_t)n);
@@ -481,6 +511,131 @@ int32_t or_lm_head_argmax(const or_model *m, const float *x, float *logits_out, 
     if (!logits_out) free(logits);
     free(a); free(a8);
     return tok;
+}
+
+/* Several rows through one decoder layer, layer-major as GI:437-467
+ * forward_mixed runs a whole sequence: row r sits at position pos[r] of the
+ * sequence whose caches are k_caches[r] / v_caches[r] (rows of one sequence
+ * pass the same pointers).  Each row's arithmetic is or_decode_row's, step
+ * for step; the projections run as one int32 GEMM over all rows, whose exact
+ * integer sums equal the per-row ones.  Every row's K/V is appended before
+ * any row's attention reads the cache, and attention of a row at position p
+ * visits keys 0..p only, so the rows of one prompt see exactly what
+ * token-by-token decoding would have written. */
+void or_decode_rows(const or_model *m, int32_t layer, int32_t rows, const int32_t *pos, float *x,
+                    int8_t *const *k_caches, int8_t *const *v_caches) {
+    const or_config *c = &m->cfg;
+    const or_layer *L = &m->layers[layer];
+    const int32_t D = c->hidden, F = c->intermediate, hd = c->head_dim;
+    const int32_t hkv = c->n_kv_heads, kvd = hkv * hd, QKV = D + 2 * kvd;
+    const int32_t KF = D > F ? D : F;
+    float *a = (float *)malloc(sizeof(float) * (size_t)rows * D);
+    int8_t *a8 = (int8_t *)malloc((size_t)rows * KF);
+    double *sa = (double *)malloc(sizeof(double) * (size_t)rows);
+    int32_t *acc = (int32_t *)malloc(sizeof(int32_t) * (size_t)rows * F);
+    float *qkv = (float *)malloc(sizeof(float) * (size_t)rows * QKV);
+    int8_t *q8 = (int8_t *)malloc((size_t)rows * D);
+    double *sq = (double *)malloc(sizeof(double) * (size_t)rows);
+    float *att = (float *)malloc(sizeof(float) * (size_t)rows * D);
+    float *gt = (float *)malloc(sizeof(float) * (size_t)rows * F);
+    const int8_t *wqkv[3] = {L->w[OR_Q], L->w[OR_K], L->w[OR_V]};
+    const float *sqkv[3] = {L->s[OR_Q], L->s[OR_K], L->s[OR_V]};
+    const int32_t nqkv[3] = {D, kvd, kvd}, oqkv[3] = {0, D, D + kvd};
+
+    /* GI:264 attention input, per row */
+#pragma omp parallel for schedule(static)
+    for (int32_t r = 0; r < rows; r++) {
+        or_rms_norm(x + (int64_t)r * D, L->g_in, D, c->rms_eps, a + (int64_t)r * D);
+        sa[r] = or_quantize_int8(a + (int64_t)r * D, D, a8 + (int64_t)r * D);
+    }
+    /* GI:146-148 Q/K/V projections */
+    for (int i = 0; i < 3; i++) {
+        or_gemm_i8(a8, wqkv[i], rows, nqkv[i], D, acc);
+        for (int32_t r = 0; r < rows; r++)
+            for (int32_t j = 0; j < nqkv[i]; j++)
+                qkv[(int64_t)r * QKV + oqkv[i] + j] =
+                    (float)acc[(int64_t)r * nqkv[i] + j] * or_dequant_mult(sa[r], (double)sqkv[i][j]);
+    }
+    /* GI:154 RoPE; Q to INT8 at the row's scale; K/V rows to the cache */
+#pragma omp parallel for schedule(static)
+    for (int32_t r = 0; r < rows; r++) {
+        float *v = qkv + (int64_t)r * QKV;
+        const float *cp = m->rope_cos + (int64_t)pos[r] * hd, *sp = m->rope_sin + (int64_t)pos[r] * hd;
+        int8_t kv8[256];
+        or_apply_rope(v, c->n_heads, hd, cp, sp);
+        or_apply_rope(v + D, hkv, hd, cp, sp);
+        sq[r] = or_quantize_int8(v, D, q8 + (int64_t)r * D);
+        for (int32_t g = 0; g < hkv; g++) {
+            or_quantize_static(v + D + g * hd, hd, m->kv_sk[layer * hkv + g], kv8);
+            memcpy(k_caches[r] + cache_row(c, layer, g, pos[r]), kv8, (size_t)hd);
+            or_quantize_static(v + D + kvd + g * hd, hd, m->kv_sv[layer * hkv + g], kv8);
+            memcpy(v_caches[r] + cache_row(c, layer, g, pos[r]), kv8, (size_t)hd);
+        }
+    }
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int32_t r = 0; r < rows; r++)
+        or_attention_row(c, layer, pos[r], q8 + (int64_t)r * D, sq[r], k_caches[r], v_caches[r], m->kv_sk,
+                         m->kv_sv, att + (int64_t)r * D, NULL, NULL, NULL);
+    /* GI:164 O projection, GI:266 residual */
+#pragma omp parallel for schedule(static)
+    for (int32_t r = 0; r < rows; r++) sa[r] = or_quantize_int8(att + (int64_t)r * D, D, a8 + (int64_t)r * D);
+    or_gemm_i8(a8, L->w[OR_O], rows, D, D, acc);
+    for (int32_t r = 0; r < rows; r++)
+        for (int32_t d = 0; d < D; d++) {
+            const float o = (float)acc[(int64_t)r * D + d] * or_dequant_mult(sa[r], (double)L->s[OR_O][d]);
+            x[(int64_t)r * D + d] = x[(int64_t)r * D + d] + o;
+        }
+    /* GI:268 post-attention norm, GI:210-213 SwiGLU, GI:270 residual */
+#pragma omp parallel for schedule(static)
+    for (int32_t r = 0; r < rows; r++) {
+        or_rms_norm(x + (int64_t)r * D, L->g_post, D, c->rms_eps, a + (int64_t)r * D);
+        sa[r] = or_quantize_int8(a + (int64_t)r * D, D, a8 + (int64_t)r * D);
+    }
+    or_gemm_i8(a8, L->w[OR_GATE], rows, F, D, acc);
+    for (int32_t r = 0; r < rows; r++)
+        for (int32_t j = 0; j < F; j++)
+            gt[(int64_t)r * F + j] = (float)acc[(int64_t)r * F + j] * or_dequant_mult(sa[r], (double)L->s[OR_GATE][j]);
+    or_gemm_i8(a8, L->w[OR_UP], rows, F, D, acc);
+    for (int32_t r = 0; r < rows; r++)
+        for (int32_t j = 0; j < F; j++) {
+            const float up = (float)acc[(int64_t)r * F + j] * or_dequant_mult(sa[r], (double)L->s[OR_UP][j]);
+            gt[(int64_t)r * F + j] = or_silu(gt[(int64_t)r * F + j]) * up;
+        }
+#pragma omp parallel for schedule(static)
+    for (int32_t r = 0; r < rows; r++) sa[r] = or_quantize_int8(gt + (int64_t)r * F, F, a8 + (int64_t)r * F);
+    or_gemm_i8(a8, L->w[OR_DOWN], rows, D, F, acc);
+    for (int32_t r = 0; r < rows; r++)
+        for (int32_t d = 0; d < D; d++) {
+            const float o = (float)acc[(int64_t)r * D + d] * or_dequant_mult(sa[r], (double)L->s[OR_DOWN][d]);
+            x[(int64_t)r * D + d] = x[(int64_t)r * D + d] + o;
+        }
+    free(a); free(a8); free(sa); free(acc); free(qkv); free(q8); free(sq); free(att); free(gt);
+}
+
+/* or_lm_head_argmax for several rows at once (one int32 GEMM over the rows):
+ * tokens[r] is row r's greedy token, best_logits[r] its logit (may be NULL). */
+void or_lm_head_rows(const or_model *m, int32_t rows, const float *x, int32_t *tokens, float *best_logits) {
+    const int32_t D = m->cfg.hidden, V = m->cfg.vocab;
+    float *a = (float *)malloc(sizeof(float) * (size_t)rows * D);
+    int8_t *a8 = (int8_t *)malloc((size_t)rows * D);
+    double *sa = (double *)malloc(sizeof(double) * (size_t)rows);
+    int32_t *acc = (int32_t *)malloc(sizeof(int32_t) * (size_t)rows * V);
+#pragma omp parallel for schedule(static)
+    for (int32_t r = 0; r < rows; r++) {
+        or_rms_norm(x + (int64_t)r * D, m->g_final, D, m->cfg.rms_eps, a + (int64_t)r * D);
+        sa[r] = or_quantize_int8(a + (int64_t)r * D, D, a8 + (int64_t)r * D);
+    }
+    or_gemm_i8(a8, m->lm_w, rows, V, D, acc);
+#pragma omp parallel for schedule(static)
+    for (int32_t r = 0; r < rows; r++) {
+        float *lg = (float *)malloc(sizeof(float) * (size_t)V);
+        for (int32_t j = 0; j < V; j++)
+            lg[j] = (float)acc[(int64_t)r * V + j] * or_dequant_mult(sa[r], (double)m->lm_s[j]);
+        tokens[r] = or_argmax_first(lg, V);
+        if (best_logits) best_logits[r] = lg[tokens[r]];
+        free(lg);
+    }
+    free(a); free(a8); free(sa); free(acc);
 }
 
 /* Embed one token at position pos, run n_layers decoder layers (appending to

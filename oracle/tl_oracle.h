@@ -113,6 +113,12 @@ void    or_embed(const or_model *m, int32_t token, float *x);
 void    or_decode_row(const or_model *m, int32_t layer, int32_t pos, float *x,
                       int8_t *k_cache, int8_t *v_cache, or_trace *tr);
 int32_t or_lm_head_argmax(const or_model *m, const float *x, float *logits_out, float *best_logit);
+/* layer-major multi-row forms of or_decode_row / or_lm_head_argmax (same
+ * per-row arithmetic; row r at position pos[r] of the sequence whose caches
+ * are k_caches[r] / v_caches[r]) */
+void    or_decode_rows(const or_model *m, int32_t layer, int32_t rows, const int32_t *pos, float *x,
+                       int8_t *const *k_caches, int8_t *const *v_caches);
+void    or_lm_head_rows(const or_model *m, int32_t rows, const float *x, int32_t *tokens, float *best_logits);
 int32_t or_forward_token(const or_model *m, int32_t token, int32_t pos, int32_t n_layers,
                          int8_t *k_cache, int8_t *v_cache, float *best_logit);
 int32_t or_generate(const or_model *m, const int32_t *prompt, int32_t n_prompt, int32_t max_new,

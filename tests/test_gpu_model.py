@@ -144,6 +144,26 @@ def test_generate_eos_and_abort(small_model, persist, monkeypatch):
     eng.close()
 
 
+@DECODE_PATHS
+def test_decode_continues_after_eos_stop(small_model, persist, monkeypatch):
+    """Steps replayed after the EOS stop record nothing and leave the cache
+    and cursor as they were: decoding on from the stop gives the oracle's
+    greedy continuation of the same sequence (EOS fed back like any token)."""
+    monkeypatch.setenv("TL_PERSIST", persist)
+    eng = engine_for(small_model)
+    prompt = np.array([3, 1, 4, 1, 5, 9, 2, 6], np.int32)
+    free, _ = eng.generate(prompt, 30)
+    eos = int(free[3])
+    first = int(np.argmax(free == eos))
+    got, stop = eng.generate(prompt, 30, eos_id=eos)      # stops inside the first 16-step chunk
+    assert stop == "eos" and got.tolist() == free[:first + 1].tolist()
+    more, stop2 = eng.decode(9, seq=0)
+    assert stop2 == "max_tokens"
+    want, _ = oracle.Oracle(small_model).generate(prompt, first + 1 + 9)
+    assert_bits_equal(np.concatenate([got, more]), want, "tokens across the stop")
+    eng.close()
+
+
 def test_decode_batch_matches_oracle(small_model):
     m = small_model
     B, steps = 4, 6

@@ -393,3 +393,98 @@ def test_generate_equals_token_by_token_forward():
                                                 oracle.ptr(kc, oracle.C.c_int8), oracle.ptr(vc, oracle.C.c_int8), None)
         assert tok == toks[step]
         seq.append(int(tok))
+
+
+def test_attention_pv_multiplier_closed_form():
+    """Closed form for the P.V step (EX:1839, softmax_wrapper.sv:23: the
+    probability scale is 1/127).  With an all-zero query every key scores 0,
+    so softmax gives p = 1/n and the INT8 probability is rne(127/n) for every
+    key; the accumulator is then rne(127/n) * sum_t v8[t][d] and the output
+    is that integer times f32((1/127) * s_v), bit for bit.  A 1/128 scale,
+    a dropped key or a transposed V index fails it."""
+    cfg = dict(oracle.SMALL_CFG, n_layers=1)
+    c = oracle.OrConfig(*(cfg[k] for k in ("hidden", "intermediate", "n_layers", "n_heads", "n_kv_heads",
+                                            "head_dim", "vocab", "max_pos", "rms_eps", "rope_theta")))
+    H, Hkv, hd = cfg["n_heads"], cfg["n_kv_heads"], 64
+    rng = np.random.default_rng(4)
+    sk = rng.uniform(0.01, 0.1, (1, Hkv)).astype(F32)
+    sv = rng.uniform(0.01, 0.1, (1, Hkv)).astype(F32)
+    kc = np.zeros((1, Hkv, cfg["max_pos"], hd), np.int8)
+    vc = np.zeros_like(kc)
+    q8 = np.zeros(H * hd, np.int8)
+    for n in (1, 3, 5, 64, 65, 200):
+        kc[0, :, :n] = rng.integers(-127, 128, (Hkv, n, hd))
+        vc[0, :, :n] = rng.integers(-127, 128, (Hkv, n, hd))
+        att = np.empty(H * hd, F32)
+        acc = np.empty(H * hd, np.int32)
+        probs = np.empty((H, n), np.int8)
+        oracle.lib().or_attention_row(oracle.C.byref(c), 0, n - 1, oracle.ptr(q8, oracle.C.c_int8), 0.01,
+                                      oracle.ptr(kc, oracle.C.c_int8), oracle.ptr(vc, oracle.C.c_int8),
+                                      oracle.ptr(sk, oracle.C.c_float), oracle.ptr(sv, oracle.C.c_float),
+                                      oracle.ptr(att, oracle.C.c_float), None, oracle.ptr(probs, oracle.C.c_int8),
+                                      oracle.ptr(acc, oracle.C.c_int32))
+        p8 = int(np.rint(np.float32(127.0) * (np.float32(1.0) / np.float32(n))))
+        assert np.all(probs == p8), n
+        for h in range(H):
+            g = h // (H // Hkv)
+            want_acc = p8 * vc[0, g, :n].astype(np.int64).sum(axis=0)
+            assert np.array_equal(acc[h * hd:(h + 1) * hd], want_acc), (n, h)
+            mult = np.float32(np.float64(1.0 / 127.0) * np.float64(sv[0, g]))
+            want = want_acc.astype(F32) * mult
+            assert bits_equal(att[h * hd:(h + 1) * hd], want), (n, h)
+            wrong = want_acc.astype(F32) * np.float32(np.float64(1.0 / 128.0) * np.float64(sv[0, g]))
+            assert not bits_equal(att[h * hd:(h + 1) * hd], wrong)
+
+
+# ---- layer-major multi-row forms (used to check full-size runs) ----------------------
+
+def test_decode_rows_equal_decode_row():
+    """or_decode_rows (rows of one prompt, layer-major; and rows of different
+    sequences at different positions) equals or_decode_row row by row: every
+    output bit and every cache row."""
+    m = oracle.synthetic_model(dict(oracle.SMALL_CFG), seed=3)
+    orc = oracle.Oracle(m)
+    L = m.cfg["n_layers"]
+    prompt = np.random.default_rng(1).integers(0, m.cfg["vocab"], 37)
+    # one prompt, layer-major vs token by token
+    c1, c2 = m.new_cache(), m.new_cache()
+    x = np.stack([orc.embed(int(t)) for t in prompt]).astype(F32)
+    for layer in range(L):
+        orc.decode_rows(layer, np.arange(prompt.size), x, [c1] * prompt.size)
+    for i, t in enumerate(prompt):
+        y = orc.embed(int(t))
+        for layer in range(L):
+            y = orc.decode_row(layer, i, y, *c2)
+        assert bits_equal(x[i], y), i
+    assert np.array_equal(c1[0], c2[0]) and np.array_equal(c1[1], c2[1])
+    # three sequences at different positions (the batched-decode shape)
+    rng = np.random.default_rng(2)
+    caches = [m.new_cache() for _ in range(3)]
+    for kc, vc in caches:
+        kc[:, :, :100] = rng.integers(-127, 128, kc[:, :, :100].shape)
+        vc[:, :, :100] = rng.integers(-127, 128, vc[:, :, :100].shape)
+    copies = [(kc.copy(), vc.copy()) for kc, vc in caches]
+    pos = np.array([7, 99, 40], np.int32)
+    x = rng.standard_normal((3, m.cfg["hidden"])).astype(F32)
+    want = [x[r].copy() for r in range(3)]
+    for layer in range(L):
+        orc.decode_rows(layer, pos, x, caches)
+        for r in range(3):
+            want[r] = orc.decode_row(layer, int(pos[r]), want[r], *copies[r])
+    for r in range(3):
+        assert bits_equal(x[r], want[r]), r
+        assert np.array_equal(caches[r][0], copies[r][0]) and np.array_equal(caches[r][1], copies[r][1])
+    tok, lg = orc.lm_head_rows(x)
+    for r in range(3):
+        assert (int(tok[r]), F32(lg[r])) == tuple(orc.lm_head(x[r])[:1]) + (F32(orc.lm_head(x[r])[1]),)
+
+
+def test_generate_layer_major_equals_generate():
+    m = oracle.synthetic_model(dict(oracle.SMALL_CFG), seed=4)
+    orc = oracle.Oracle(m)
+    prompt = np.array([5, 17, 1000, 3, 3, 2047, 64, 9, 9, 100], np.int32)
+    c1, c2 = m.new_cache(), m.new_cache()
+    want, _ = orc.generate(prompt, 9, cache=c1)
+    got = orc.generate_layer_major(prompt, 9, cache=c2)
+    assert np.array_equal(got, want)
+    assert np.array_equal(c1[0], c2[0]) and np.array_equal(c1[1], c2[1])
