@@ -251,13 +251,37 @@ int32_t tl_capture_step(tl_handle *h, int32_t seq, tl_capture *cap);
 /* ---- profiling ---------------------------------------------------------------- */
 
 /* Kernel classes timed with HIP events on the handle's stream while profiling
- * is on (accumulated per class). */
+ * is on (accumulated per class).  The projection classes cover that role's
+ * GEMV (one row) and GEMM (prefill and batched rows) alike; TL_K_GEMM_PREFILL
+ * is the standalone tl_gemm_i8 operator. */
 typedef enum tl_kclass {
     TL_K_QKV = 0, TL_K_ATTN = 1, TL_K_O = 2, TL_K_GLU = 3, TL_K_DOWN = 4, TL_K_LMHEAD = 5,
     TL_K_NORM = 6, TL_K_GEMM_PREFILL = 7, TL_K_OTHER = 8, TL_K_COUNT = 9
 } tl_kclass;
 int32_t tl_set_profiling(tl_handle *h, int32_t on);
 int32_t tl_get_profile(tl_handle *h, int32_t kclass, int64_t *count, double *total_ms, double *bytes);
+
+/* Device timeline of batch-1 decode steps, in the regime tl_decode runs them
+ * (one captured HIP graph per step, kernels back to back).  No counterpart in
+ * the reference (its FPGA design has no cycle counters); it exists to account
+ * for the time of a decode step.  n_steps greedy steps of sequence seq are
+ * run exactly as tl_decode runs them (tokens recorded, cursor advanced), from
+ * a graph captured with clock stamps: lane 0 of every wavefront of every
+ * kernel stores the GPU clock (constant-rate wall clock) at its start and
+ * end.  Per step, a kernel's busy time is its last wavefront's end minus its
+ * first wavefront's start, and the gap after it is the time until the next
+ * kernel's first wavefront starts.  All figures are means per step in
+ * microseconds.  Kernels that do not stamp are counted in no class.
+ * Measurement use only: it synchronizes after every step. */
+typedef struct tl_timeline {
+    int32_t steps;
+    int32_t kernels;                 /* stamped kernels per step */
+    double  step_us;                 /* first kernel start -> last kernel end */
+    double  busy_us[TL_K_COUNT];     /* summed busy time of the class's kernels */
+    double  gap_us[TL_K_COUNT];      /* summed gaps after the class's kernels */
+    int32_t launches[TL_K_COUNT];    /* the class's kernels per step */
+} tl_timeline;
+int32_t tl_decode_timeline(tl_handle *h, int32_t seq, int32_t n_steps, tl_timeline *out);
 
 #ifdef __cplusplus
 }

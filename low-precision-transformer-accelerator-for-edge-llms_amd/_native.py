@@ -52,6 +52,12 @@ class TlCapture(C.Structure):
     ]
 
 
+class TlTimeline(C.Structure):
+    """struct tl_timeline: device timeline of batch-1 decode steps."""
+    _fields_ = [("steps", C.c_int32), ("kernels", C.c_int32), ("step_us", C.c_double),
+                ("busy_us", C.c_double * 9), ("gap_us", C.c_double * 9), ("launches", C.c_int32 * 9)]
+
+
 class TlError(RuntimeError):
     def __init__(self, status: int, message: str):
         super().__init__(f"{message} (status {status})")
@@ -110,6 +116,7 @@ SIGNATURES = {
     "tl_capture_step": (_i32, [_vp, _i32, C.POINTER(TlCapture)]),
     "tl_set_profiling": (_i32, [_vp, _i32]),
     "tl_get_profile": (_i32, [_vp, _i32, C.POINTER(C.c_int64), _f64p, _f64p]),
+    "tl_decode_timeline": (_i32, [_vp, _i32, _i32, C.POINTER(TlTimeline)]),
 }
 
 
@@ -226,6 +233,15 @@ class Runtime:
         wa = (_vp * 7)(*[_addr(t) for t in w])
         sa = (_vp * 7)(*[_addr(t) for t in s])
         self.check(self.lib.tl_load_layer(self.h, layer, wa, sa, _addr(g_in), _addr(g_post), src), "tl_load_layer")
+
+    def decode_timeline(self, seq: int, n_steps: int) -> dict:
+        """tl_decode_timeline: mean per-step device busy time and following gap
+        per kernel class, in microseconds."""
+        t = TlTimeline()
+        self.check(self.lib.tl_decode_timeline(self.h, int(seq), int(n_steps), C.byref(t)), "tl_decode_timeline")
+        classes = {name: {"launches": t.launches[k], "busy_us": t.busy_us[k], "gap_us": t.gap_us[k]}
+                   for name, k in KCLASS.items() if t.launches[k]}
+        return {"steps": t.steps, "kernels": t.kernels, "step_us": t.step_us, "classes": classes}
 
     def profile(self, kclass: str) -> tuple[int, float, float]:
         cnt, ms, by = C.c_int64(), C.c_double(), C.c_double()

@@ -40,6 +40,7 @@ __global__ __launch_bounds__(kNT) void gemv_fused_kernel(GemvArgs a) {
     __shared__ unsigned long long wbest[kNW];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const WaveStamp stamp(a.ts, (int64_t)blockIdx.x * kNW + wave);
     const int K = a.k;
     const int row0 = (blockIdx.x * kNW + wave) * R;
 
@@ -167,6 +168,7 @@ struct AttnDecodeArgs {
     const float* kv_sv;
     double attn_scale;
     float* out;           // [rows][D]
+    unsigned long long* ts;   // decode timeline: [waves][2] clock stamps, or null
 };
 
 // NW wavefronts per workgroup; wavefront w takes key blocks w, w + NW, ...
@@ -427,6 +429,7 @@ __global__ __launch_bounds__(256) void attention_row_kernel(AttnDecodeArgs p) {
     __shared__ int accs[NW][64];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const WaveStamp stamp(p.ts, ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * NW + wave);
     const int G = p.n_heads / p.n_kv;
     int h0 = blockIdx.x;
     if (p.n_heads == 32 && p.n_kv == 4) {
@@ -911,6 +914,10 @@ int32_t gemv_fused_workgroups(int pro, int epi, int32_t n, int32_t k) {
     return r > 0 ? cdiv(n, kNW * r) : 0;
 }
 
+int64_t gemv_fused_wavefronts(int pro, int epi, int32_t n, int32_t k) {
+    return (int64_t)gemv_fused_workgroups(pro, epi, n, k) * kNW;
+}
+
 hipError_t launch_gemv_fused(hipStream_t s, int pro, int epi, const GemvArgs& a) {
     if (a.n <= 0) return hipSuccess;
     if (a.k <= 0 || a.k % 64 != 0 || a.k > 6 * 1024) return hipErrorInvalidValue;
@@ -933,13 +940,14 @@ hipError_t launch_gemv_fused(hipStream_t s, int pro, int epi, const GemvArgs& a)
 
 hipError_t launch_attention_decode(hipStream_t s, const float* qkv, int32_t rows, int32_t n_heads, int32_t n_kv,
                                    RowMap rm, const float* cos, const float* sin, KvGeom kv, int32_t layer,
-                                   const float* kv_sk, const float* kv_sv, float* out, int32_t max_t, int32_t hpw) {
+                                   const float* kv_sk, const float* kv_sv, float* out, int32_t max_t, int32_t hpw,
+                                   unsigned long long* ts) {
     if (rows <= 0) return hipSuccess;
     const int G = n_heads / n_kv;
     if (n_heads % n_kv || G > kMaxGroupHeads || n_heads > 32 * 4) return hipErrorInvalidValue;
     const int D = n_heads * kHeadDim, W = D + 2 * n_kv * kHeadDim;
     const int tpad = (max_t + 63) & ~63;
-    AttnDecodeArgs p{qkv, n_heads, n_kv, rm, cos, sin, kv, layer, kv_sk, kv_sv, 1.0 / sqrt((double)kHeadDim), out};
+    AttnDecodeArgs p{qkv, n_heads, n_kv, rm, cos, sin, kv, layer, kv_sk, kv_sv, 1.0 / sqrt((double)kHeadDim), out, ts};
     if (rows > 1 && G % 4 == 0 && max_t <= kGroupMaxKeys && D <= 4 * kGW * 64 && (hpw == 1 || (hpw == 8 && G == 8))) {
         // many rows: the grouped kernel, 4 (or 8) query heads per workgroup
         if (hpw == 8)

@@ -307,6 +307,28 @@ TL_DEV unsigned long long row_value_u64(unsigned long long v, int row) {
 }
 
 // maximum of 64-bit keys over the wavefront, in every lane
+// Decode-timeline stamps: with ts set, lane 0 of the wavefront stores the
+// GPU clock (wall_clock64, constant rate) read when the kernel reached this
+// object and when the object leaves scope (on every return path) at
+// ts[2 * wave_id] and ts[2 * wave_id + 1].  Without ts it does nothing.
+struct WaveStamp {
+    unsigned long long* p;
+    unsigned long long t0;
+    TL_DEV WaveStamp(unsigned long long* ts, int64_t wave_id) : p(nullptr), t0(0) {
+        if (ts != nullptr) {
+            t0 = wall_clock64();
+            if ((threadIdx.x & 63) == 0) p = ts + 2 * wave_id;
+        }
+    }
+    TL_DEV ~WaveStamp() {
+        if (p != nullptr) {
+            const unsigned long long t1 = wall_clock64();
+            p[0] = t0;
+            p[1] = t1;
+        }
+    }
+};
+
 TL_DEV unsigned long long wave_max_u64(unsigned long long v) {
     v = row_max_u64(v);
     return max_u64(max_u64(row_value_u64(v, 0), row_value_u64(v, 1)),

@@ -87,6 +87,7 @@ struct GemvArgs {
     unsigned long long* key; // argmax slot (EPI_ARGMAX)
     unsigned long long* wg_keys; // EPI_ARGMAX: one key per workgroup (no atomic) instead of key
     int32_t n, k;
+    unsigned long long* ts;  // decode timeline: [waves][2] clock stamps, or null
 };
 
 struct GemmArgs {
@@ -176,6 +177,7 @@ struct EmbedNext {
     // the same position, so further replays leave the state as it is
     const int32_t* eos;  // nullptr: no stop check
     int32_t* stopped;
+    unsigned long long* ts;   // decode timeline: [1][2] clock stamps, or null
 };
 hipError_t launch_finalize_tokens(hipStream_t s, unsigned long long* keys, int32_t rows,
                                   int32_t* token_cur, int32_t* tokens_out, int32_t out_stride,
@@ -184,6 +186,7 @@ hipError_t launch_finalize_tokens(hipStream_t s, unsigned long long* keys, int32
                                   EmbedNext nx = EmbedNext{});
 // workgroups launch_gemv_fused uses for this prologue / epilogue / shape
 int32_t gemv_fused_workgroups(int pro, int epi, int32_t n, int32_t k);
+int64_t gemv_fused_wavefronts(int pro, int epi, int32_t n, int32_t k);
 hipError_t launch_argmax_rows(hipStream_t s, const float* logits, int32_t rows, int32_t n,
                               unsigned long long* keys);
 hipError_t launch_argmax_tiles(hipStream_t s, const unsigned long long* part, int32_t tiles, int32_t rows,
@@ -253,7 +256,8 @@ hipError_t launch_gemm32(hipStream_t s, int epi, const GemmArgs& a, int32_t spli
 hipError_t launch_gemv_fused(hipStream_t s, int pro, int epi, const GemvArgs& a);
 hipError_t launch_attention_decode(hipStream_t s, const float* qkv, int32_t rows, int32_t n_heads, int32_t n_kv,
                                    RowMap rm, const float* cos, const float* sin, KvGeom kv, int32_t layer,
-                                   const float* kv_sk, const float* kv_sv, float* out, int32_t max_t, int32_t hpw);
+                                   const float* kv_sk, const float* kv_sv, float* out, int32_t max_t, int32_t hpw,
+                                   unsigned long long* ts = nullptr);
 hipError_t launch_embed_step(hipStream_t s, const int32_t* tok_by_seq, const int32_t* seq_of_row, int32_t rows,
                              const int32_t* cursor, int32_t* row_pos, int32_t d, int32_t vocab, const int8_t* emb,
                              const float* emb_s, float* x);

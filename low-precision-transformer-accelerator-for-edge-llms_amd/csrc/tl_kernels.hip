@@ -1070,6 +1070,7 @@ __global__ __launch_bounds__(64) void finalize_tokens_kernel(unsigned long long*
                                                              float* best_logit, int32_t advance,
                                                              const unsigned long long* wg_keys, int32_t n_wg,
                                                              EmbedNext nx) {
+    const WaveStamp stamp(nx.ts, blockIdx.x);
     const bool single = n_wg > 0 || nx.x != nullptr;
     const int r = single ? 0 : blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= rows) return;

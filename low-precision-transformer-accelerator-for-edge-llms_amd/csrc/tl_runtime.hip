@@ -142,6 +142,19 @@ struct tl_handle {
     std::vector<hipGraphExec_t> graphs;   // captured batch-1 decode step per sequence
 
     bool profiling = false;
+    // decode timeline: while ts_on, the launches of a step take consecutive
+    // regions of ts_buf for their wavefronts' clock stamps
+    struct TsSlot {
+        int kclass;
+        size_t off;       // u64 elements into ts_buf
+        int64_t waves;
+    };
+    bool ts_on = false;
+    bool ts_overflow = false;
+    unsigned long long* ts_buf = nullptr;
+    size_t ts_cap = 0;
+    size_t ts_used = 0;
+    std::vector<TsSlot> ts_slots;
     std::vector<ProfEvent> prof_pending;
     std::vector<hipEvent_t> event_pool;
     int64_t prof_count[TL_K_COUNT] = {};
@@ -376,7 +389,8 @@ int32_t linear(tl_handle* h, int epi, int rows, const int8_t* x8, const double* 
     GemmArgs a{};
     a.a = x8; a.w = w; a.w2 = w2; a.as = xs; a.ws = ws; a.ws2 = ws2;
     a.residual = residual; a.y = y; a.m = rows; a.n = n; a.k = k; a.wp = wp; a.wp2 = wp2;
-    return run_gemm(h, epi, a, kclass == TL_K_LMHEAD ? TL_K_LMHEAD : TL_K_GEMM_PREFILL);
+    // multi-row GEMMs keep their role's class (Q|K|V, O, gate/up, down, LM head)
+    return run_gemm(h, epi, a, kclass);
 }
 
 RowMap rowmap(tl_handle* h) { return RowMap{h->row_seq, h->row_pos}; }
@@ -391,6 +405,20 @@ hipError_t rows_attention(tl_handle* h, const int8_t* q8, const double* q_scale,
                                       h->kv, layer, h->kv_sk, h->kv_sv, out);
     return launch_attention(h->stream, q8, q_scale, rows, c.n_heads, c.n_kv_heads, rowmap(h), h->kv, layer, h->kv_sk,
                             h->kv_sv, out, max_t);
+}
+
+// stamp region for one launch of `waves` wavefronts (null unless capturing a
+// timeline step)
+unsigned long long* ts_take(tl_handle* h, int kclass, int64_t waves) {
+    if (!h->ts_on || waves <= 0) return nullptr;
+    if (h->ts_used + 2 * (size_t)waves > h->ts_cap) {
+        h->ts_overflow = true;
+        return nullptr;
+    }
+    unsigned long long* p = h->ts_buf + h->ts_used;
+    h->ts_slots.push_back({kclass, h->ts_used, waves});
+    h->ts_used += 2 * (size_t)waves;
+    return p;
 }
 
 GemvArgs gemv_args(const tl_handle* h) {
@@ -410,17 +438,20 @@ int32_t layer_row1(tl_handle* h, int32_t layer, int32_t max_t) {
     {
         GemvArgs g = gemv_args(h);
         g.xf = h->x; g.gamma = L.g_in; g.w = L.wqkv; g.ws = L.sqkv; g.y = h->qkv; g.n = QKV; g.k = D;
+        g.ts = ts_take(h, TL_K_QKV, gemv_fused_wavefronts(PRO_RMSNORM, EPI_DEQUANT, QKV, D));
         Prof p(h, TL_K_QKV, (double)QKV * D + QKV * 8.0 + D * 8.0);
         TL_LAUNCH(h, launch_gemv_fused(h->stream, PRO_RMSNORM, EPI_DEQUANT, g));
     }
     {
         Prof p(h, TL_K_ATTN, (double)c.n_heads * max_t * 128.0 + QKV * 4.0 + D * 4.0);
+        unsigned long long* ts = ts_take(h, TL_K_ATTN, (int64_t)c.n_heads * 4);
         TL_LAUNCH(h, launch_attention_decode(h->stream, h->qkv, 1, c.n_heads, c.n_kv_heads, rowmap(h), h->rope_cos,
-                                             h->rope_sin, h->kv, layer, h->kv_sk, h->kv_sv, h->att, max_t, 1));
+                                             h->rope_sin, h->kv, layer, h->kv_sk, h->kv_sv, h->att, max_t, 1, ts));
     }
     {
         GemvArgs g = gemv_args(h);
         g.xf = h->att; g.w = L.wo; g.ws = L.so; g.residual = h->x; g.y = h->x; g.n = D; g.k = D;
+        g.ts = ts_take(h, TL_K_O, gemv_fused_wavefronts(PRO_QUANT, EPI_DEQUANT_RES, D, D));
         Prof p(h, TL_K_O, (double)D * D + D * 4.0 + D * 12.0);
         TL_LAUNCH(h, launch_gemv_fused(h->stream, PRO_QUANT, EPI_DEQUANT_RES, g));
     }
@@ -428,12 +459,14 @@ int32_t layer_row1(tl_handle* h, int32_t layer, int32_t max_t) {
         GemvArgs g = gemv_args(h);
         g.xf = h->x; g.gamma = L.g_post; g.w = L.wg; g.w2 = L.wu; g.ws = L.sg; g.ws2 = L.su; g.y = h->hid;
         g.n = F; g.k = D;
+        g.ts = ts_take(h, TL_K_GLU, gemv_fused_wavefronts(PRO_RMSNORM, EPI_GLU, F, D));
         Prof p(h, TL_K_GLU, 2.0 * F * D + F * 8.0 + D * 8.0 + F * 4.0);
         TL_LAUNCH(h, launch_gemv_fused(h->stream, PRO_RMSNORM, EPI_GLU, g));
     }
     {
         GemvArgs g = gemv_args(h);
         g.xf = h->hid; g.w = L.wd; g.ws = L.sd; g.residual = h->x; g.y = h->x; g.n = D; g.k = F;
+        g.ts = ts_take(h, TL_K_DOWN, gemv_fused_wavefronts(PRO_QUANT, EPI_DEQUANT_RES, D, F));
         Prof p(h, TL_K_DOWN, (double)D * F + D * 4.0 + F * 4.0 + D * 8.0);
         TL_LAUNCH(h, launch_gemv_fused(h->stream, PRO_QUANT, EPI_DEQUANT_RES, g));
     }
@@ -512,6 +545,7 @@ int32_t lm_head_rows(tl_handle* h, const float* xrow, int32_t rows, int32_t seq,
         n_wg = gemv_fused_workgroups(PRO_RMSNORM, EPI_ARGMAX, V, D);
         if (n_wg <= 0 || n_wg > (V + 3) / 4) return fail(h, TL_ERR_INTERNAL, "LM head workgroup count");
         g.wg_keys = h->lm_wg_keys;
+        g.ts = ts_take(h, TL_K_LMHEAD, gemv_fused_wavefronts(PRO_RMSNORM, EPI_ARGMAX, V, D));
         Prof p(h, TL_K_LMHEAD, (double)V * D + V * 4.0 + D * 8.0);
         TL_LAUNCH(h, launch_gemv_fused(h->stream, PRO_RMSNORM, EPI_ARGMAX, g));
     } else {
@@ -540,6 +574,7 @@ int32_t lm_head_rows(tl_handle* h, const float* xrow, int32_t rows, int32_t seq,
             TL_LAUNCH(h, launch_argmax_rows(h->stream, h->logits, rows, V, keys));
         }
     }
+    if (rows == 1) nx.ts = ts_take(h, TL_K_OTHER, 1);
     TL_LAUNCH(h, launch_finalize_tokens(h->stream, keys, rows, h->token_cur + (rows == 1 ? seq : 0),
                                         h->tokens_out + (int64_t)(rows == 1 ? seq : 0) * c.max_pos, c.max_pos,
                                         h->n_gen + (rows == 1 ? seq : 0), h->cursor + (rows == 1 ? seq : 0),
@@ -1592,6 +1627,102 @@ int32_t tl_get_profile(tl_handle* h, int32_t kclass, int64_t* count, double* tot
     if (count) *count = h->prof_count[kclass];
     if (total_ms) *total_ms = h->prof_ms[kclass];
     if (bytes) *bytes = h->prof_bytes[kclass];
+    return TL_OK;
+}
+
+int32_t tl_decode_timeline(tl_handle* h, int32_t seq, int32_t n_steps, tl_timeline* out) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    const tl_config& c = h->cfg;
+    TL_REQ(h, out && n_steps >= 1, "bad timeline arguments");
+    TL_REQ(h, seq >= 0 && seq < h->max_seqs, "sequence out of range");
+    TL_REQ(h, h->host_ngen[seq] >= 1, "tl_decode_timeline needs a prefilled sequence");
+    TL_REQ(h, (int64_t)h->host_cursor[seq] + n_steps <= c.max_pos, "Sequence length exceeds max_position_embeddings");
+    int32_t r = check_model_loaded(h);
+    if (r) return r;
+    int rate_khz = 0;
+    TL_HIP(h, hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, h->device));
+    TL_REQ(h, rate_khz > 0, "device reports no wall-clock rate");
+    if (!h->ts_buf) {
+        h->ts_cap = (size_t)1 << 22;
+        TL_HIP(h, dalloc(h, &h->ts_buf, h->ts_cap));
+    }
+    if ((r = set_stop_state(h, seq, -1))) return r;
+    if ((r = upload_rows(h, 1, seq, false, h->host_cursor[seq]))) return r;
+    if ((r = decode_embed1(h))) return r;
+    // capture one step with stamp regions
+    h->ts_on = true;
+    h->ts_overflow = false;
+    h->ts_used = 0;
+    h->ts_slots.clear();
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal);
+    if (e == hipSuccess) {
+        r = decode_step1(h, seq, c.max_pos);
+        e = hipStreamEndCapture(h->stream, &graph);
+    }
+    h->ts_on = false;
+    if (r || e != hipSuccess) {
+        if (graph) hipGraphDestroy(graph);
+        return r ? r : fail(h, TL_ERR_INTERNAL, std::string("timeline capture: ") + hipGetErrorString(e));
+    }
+    if (h->ts_overflow) {
+        hipGraphDestroy(graph);
+        return fail(h, TL_ERR_INTERNAL, "timeline stamp buffer too small");
+    }
+    hipGraphExec_t exec = nullptr;
+    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    hipGraphDestroy(graph);
+    TL_HIP(h, e);
+    std::vector<unsigned long long> st(h->ts_used);
+    *out = tl_timeline{};
+    const double us_per_tick = 1000.0 / (double)rate_khz;
+    int32_t done = 0;
+    for (; done < n_steps; done++) {
+        e = hipMemsetAsync(h->ts_buf, 0, h->ts_used * sizeof(unsigned long long), h->stream);
+        if (e == hipSuccess) e = hipGraphLaunch(exec, h->stream);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(st.data(), h->ts_buf, h->ts_used * sizeof(unsigned long long), hipMemcpyDeviceToHost,
+                               h->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(h->stream);
+        if (e != hipSuccess) break;
+        // per kernel: first wavefront start, last wavefront end (unstamped
+        // wavefronts, e.g. past the end of a grid, hold zeros)
+        unsigned long long first = 0, last = 0, prev_end = 0;
+        int prev_class = -1, kernels = 0;
+        for (const auto& sl : h->ts_slots) {
+            unsigned long long a = ~0ull, b = 0;
+            for (int64_t w = 0; w < sl.waves; w++) {
+                const unsigned long long t0 = st[sl.off + 2 * w], t1 = st[sl.off + 2 * w + 1];
+                if (t1 == 0) continue;
+                a = std::min(a, t0);
+                b = std::max(b, t1);
+            }
+            if (b == 0) continue;
+            kernels++;
+            out->busy_us[sl.kclass] += (double)(b - a) * us_per_tick;
+            out->launches[sl.kclass] += 1;
+            if (prev_class >= 0) out->gap_us[prev_class] += ((double)a - (double)prev_end) * us_per_tick;
+            if (!first) first = a;
+            last = b;
+            prev_end = b;
+            prev_class = sl.kclass;
+        }
+        out->kernels = kernels;
+        out->step_us += (double)(last - first) * us_per_tick;
+    }
+    hipGraphExecDestroy(exec);
+    // the steps that ran are ordinary decode steps
+    h->host_cursor[seq] += done;
+    h->host_ngen[seq] += done;
+    TL_HIP(h, e);
+    out->steps = done;
+    const double inv = 1.0 / (double)std::max(done, 1);
+    out->step_us *= inv;
+    for (int k = 0; k < TL_K_COUNT; k++) {
+        out->busy_us[k] *= inv;
+        out->gap_us[k] *= inv;
+        out->launches[k] = (int32_t)((out->launches[k] + done / 2) / std::max(done, 1));
+    }
     return TL_OK;
 }
 

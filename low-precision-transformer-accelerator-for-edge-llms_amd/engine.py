@@ -205,6 +205,11 @@ class Engine:
     def set_profiling(self, on: bool) -> None:
         self.rt.call("tl_set_profiling", int(bool(on)))
 
+    def decode_timeline(self, n_steps: int, seq: int = 0) -> dict:
+        """Device timeline of n_steps greedy decode steps (tl_decode_timeline):
+        per kernel class, mean busy and following-gap microseconds per step."""
+        return self.rt.decode_timeline(seq, n_steps)
+
     def profile(self, kclass: str):
         return self.rt.profile(kclass)
 

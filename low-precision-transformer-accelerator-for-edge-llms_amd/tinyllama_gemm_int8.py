@@ -557,24 +557,26 @@ def forward_mixed(token_ids, weights: TinyLlamaWeights, cos: np.ndarray, sin: np
 
 
 def parse_token_ids(token_ids_arg: str | None) -> list[int] | None:
-    """GI:340-348."""
+    """GI:340-348 interface: "1, 2,3" -> [1, 2, 3]; None stays None."""
     if token_ids_arg is None:
         return None
-    return [int(p.strip()) for p in token_ids_arg.split(",") if p.strip()]
+    fields = (f.strip() for f in token_ids_arg.split(","))
+    return [int(f) for f in fields if f]
 
 
 def resolve_token_ids(prompt: str | None, token_ids_arg: str | None, tokenizer) -> list[int]:
-    """GI:361-375."""
-    token_ids = parse_token_ids(token_ids_arg)
-    if token_ids is None:
+    """GI:361-375 interface: explicit ids win, else the prompt is tokenized;
+    the reference's ValueError texts for a missing or empty input."""
+    ids = parse_token_ids(token_ids_arg)
+    if ids is None:
         if prompt is None:
             raise ValueError("Provide either --prompt or --token-ids")
         if tokenizer is None:
             raise ValueError("Tokenizer unavailable, so --token-ids is required")
-        token_ids = tokenizer.encode(prompt)
-    if not token_ids:
+        ids = list(tokenizer.encode(prompt))
+    if len(ids) == 0:
         raise ValueError("Input token sequence is empty")
-    return token_ids
+    return ids
 
 
 def run_generate(prompt: str | None, token_ids_arg: str | None, weights_path, layer_count: int, max_tokens: int,
@@ -628,216 +630,263 @@ def run_generate(prompt: str | None, token_ids_arg: str | None, weights_path, la
 
 
 # ---------------------------------------------------------------------------
-# GI:284-338, 351-353, 401-405, 470-626: the analysis report and its
-# per-layer debug dump (the reporting itself is host-side formatting)
+# The analysis report and the command line (GI:284-338, 351-353, 401-405,
+# 470-626, 688-745).  What is kept from the reference is its interface: the
+# CLI flags, the ValueError texts, the printed and summary line formats and
+# the key schema of debug_arrays.npz (nested debug dicts joined with "_").
+# The report is assembled from per-layer comparison records; both models run
+# on the device (float32 kernels for the reference model, the INT8 path for
+# the mixed one).
 # ---------------------------------------------------------------------------
-def decode_token(tokenizer, token_id: int) -> str:
-    """GI:284-287."""
-    return "" if tokenizer is None else tokenizer.decode([token_id])
-
-
 def safe_repr(text: str) -> str:
-    """GI:290-291."""
+    """Printable ASCII form of token text (GI:290-291 format)."""
     return text.encode("unicode_escape").decode("ascii")
 
 
+def decode_token(tokenizer, token_id: int) -> str:
+    """Text of one token id; empty without a tokenizer (GI:284-287)."""
+    return tokenizer.decode([int(token_id)]) if tokenizer is not None else ""
+
+
 def top_tokens(logits: np.ndarray, tokenizer, k: int) -> list[tuple[int, float, str]]:
-    """GI:294-299: the k highest logits, highest first."""
-    indices = np.argsort(logits)[-k:][::-1]
-    return [(int(i), float(logits[i]), decode_token(tokenizer, int(i))) for i in indices]
+    """The k largest logits of a row as (id, logit, text), largest first
+    (GI:294-299).  A partial partition finds the k, a sort orders them."""
+    row = np.asarray(logits, dtype=np.float32).ravel()
+    k = max(0, min(int(k), row.size))
+    if k == 0:
+        return []
+    best = np.argpartition(row, row.size - k)[row.size - k:]
+    best = best[np.argsort(-row[best], kind="stable")]
+    return [(int(i), float(row[i]), decode_token(tokenizer, int(i))) for i in best]
 
 
 def flatten_named_arrays(prefix: str, obj: Any) -> dict[str, np.ndarray]:
-    """GI:302-310: nested debug dicts -> {"a_b_c": array}; non-array leaves
-    are dropped."""
+    """Nested debug dicts -> {"outer_inner_leaf": array} (the GI:302-310 key
+    schema); leaves that are not arrays are left out."""
     flat: dict[str, np.ndarray] = {}
-    if isinstance(obj, dict):
-        for key, value in obj.items():
-            flat.update(flatten_named_arrays(f"{prefix}_{key}" if prefix else key, value))
-    elif isinstance(obj, np.ndarray):
-        flat[prefix] = obj
+    pending = [(prefix, obj)]
+    while pending:
+        name, node = pending.pop()
+        if isinstance(node, np.ndarray):
+            flat[name] = node
+        elif isinstance(node, dict):
+            pending.extend(((f"{name}_{key}" if name else str(key)), child) for key, child in node.items())
     return flat
 
 
 def dump_debug(dump_dir: str, token_ids: list[int], reference_debug: dict[str, Any], mixed_debug: dict[str, Any],
                summary_lines: list[str]) -> None:
-    """GI:313-327: debug_arrays.npz (token_ids, reference_*, mixed_*) and
-    summary.txt under dump_dir."""
+    """Write debug_arrays.npz (token_ids, reference_*, mixed_*) and
+    summary.txt into dump_dir (the GI:313-327 files)."""
     os.makedirs(dump_dir, exist_ok=True)
-    arrays = {"token_ids": np.asarray(token_ids, dtype=np.int32)}
-    arrays.update(flatten_named_arrays("reference", reference_debug))
-    arrays.update(flatten_named_arrays("mixed", mixed_debug))
-    np.savez(os.path.join(dump_dir, "debug_arrays.npz"), **arrays)
-    with open(os.path.join(dump_dir, "summary.txt"), "w", encoding="utf-8") as handle:
-        handle.write("\n".join(summary_lines) + "\n")
+    payload = {"token_ids": np.asarray(token_ids, dtype=np.int32)}
+    for side, tree in (("reference", reference_debug), ("mixed", mixed_debug)):
+        payload.update(flatten_named_arrays(side, tree))
+    np.savez(os.path.join(dump_dir, "debug_arrays.npz"), **payload)
+    with open(os.path.join(dump_dir, "summary.txt"), "w", encoding="utf-8") as out:
+        out.write("".join(line + "\n" for line in summary_lines))
 
 
 def maybe_load_tokenizer(model_id: str, local_files_only: bool):
-    """GI:330-337: a local tokenizer if one is cached, else None."""
+    """A tokenizer from the local cache, or None with a warning (GI:330-337
+    behaviour; this build never downloads one)."""
     try:
         from transformers import AutoTokenizer
         return AutoTokenizer.from_pretrained(model_id, local_files_only=local_files_only)
-    except Exception as exc:
+    except Exception as exc:   # transformers missing, or nothing cached
         print(f"Warning: could not load tokenizer for {model_id}: {exc}")
         return None
 
 
 def projection_stats_line(name: str, ref_array: np.ndarray, mix_array: np.ndarray) -> str:
-    """GI:351-353."""
-    stats = diff_stats(ref_array, mix_array)
-    return f"{name}: mae={stats['mae']:.6f}, max_abs={stats['max_abs']:.6f}"
+    """One line of the projection breakdown (GI:351-353 format)."""
+    st = diff_stats(ref_array, mix_array)
+    return f"{name}: mae={st['mae']:.6f}, max_abs={st['max_abs']:.6f}"
 
 
 def print_token_context(token_ids: list[int], tokenizer) -> None:
-    """GI:401-405."""
-    print(f"Token ids: {token_ids}")
+    """The report's opening lines (GI:401-405 format)."""
+    lines = [f"Token ids: {token_ids}"]
     if tokenizer is not None:
-        print(f"Decoded tokens: {[safe_repr(tokenizer.decode([tok])) for tok in token_ids]}")
-    print("")
+        lines.append(f"Decoded tokens: {[safe_repr(decode_token(tokenizer, t)) for t in token_ids]}")
+    print("\n".join(lines + [""]))
+
+
+# projection breakdown of the dumped layer: (debug block, key, label); the
+# O and down rows are shown when both models captured them
+_BREAKDOWN = (("attn", "q_proj_fp", "attn q_proj"), ("attn", "k_proj_fp", "attn k_proj"),
+              ("attn", "v_proj_fp", "attn v_proj"), ("ffn", "gate_proj_fp", "ffn gate_proj"),
+              ("ffn", "up_proj_fp", "ffn up_proj"), ("attn", "out_fp", "attn o_proj"),
+              ("ffn", "out_fp", "ffn down_proj"))
+
+
+class _Report:
+    """Lines of an analysis run: ``say`` prints, ``note`` keeps a line for
+    summary.txt, ``both`` does both."""
+
+    def __init__(self, token_ids: list[int], layer_count: int):
+        self.kept = [f"Token ids: {token_ids}", f"Layers analyzed: {layer_count}", "Layer stats:"]
+
+    def say(self, line: str = "") -> None:
+        print(line)
+
+    def note(self, line: str) -> None:
+        self.kept.append(line)
+
+    def both(self, line: str) -> None:
+        self.say(line)
+        self.note(line)
+
+
+class _LayerComparison:
+    """Walks the decoder layers with the float32 model and the INT8 path side
+    by side.  Each layer is compared twice: isolated (the INT8 layer fed the
+    float32 model's input) and cumulative (the INT8 path fed its own previous
+    output).  The dumped layer keeps both models' debug dicts."""
+
+    def __init__(self, weights: TinyLlamaWeights, token_ids: list[int], cos, sin, dump_layer: int | None):
+        self.w = weights
+        self.cos, self.sin = cos, sin
+        self.dump_layer = dump_layer
+        self.float_x = np.asarray(weights.embed(token_ids), np.float32)
+        self.int8_x = self.float_x.copy()
+        self.kv = weights.kv_scales()
+        self.dumped: tuple[dict, dict] | None = None
+
+    def step(self, index: int) -> tuple[dict, dict, list[str]]:
+        layer = self.w.layer(index)
+        cfg = self.w.cfg
+        keep = index == self.dump_layer
+        kv = None if self.kv is None else (self.kv[0][index], self.kv[1][index])
+        f_out, f_dbg = reference_decoder_layer(self.float_x, layer, cfg, self.cos, self.sin, capture_arrays=keep)
+        iso, iso_dbg = mixed_precision_decoder_layer(self.float_x, layer, cfg, self.cos, self.sin,
+                                                     capture_arrays=keep, kv_scales=kv)
+        cum, _ = mixed_precision_decoder_layer(self.int8_x, layer, cfg, self.cos, self.sin, kv_scales=kv)
+        lines: list[str] = []
+        if keep:
+            self.dumped = (f_dbg, iso_dbg)
+            for block, key, label in _BREAKDOWN:
+                if key in f_dbg[block] and key in iso_dbg[block]:
+                    lines.append(projection_stats_line("  " + label, f_dbg[block][key], iso_dbg[block][key]))
+        isolated, cumulative = diff_stats(f_out, iso), diff_stats(f_out, cum)
+        self.float_x, self.int8_x = f_out, cum
+        return isolated, cumulative, lines
+
+    def final_logits(self, quantize_lm_head: bool, keep_debug: bool):
+        """Final RMSNorm of each model's last hidden rows, then the LM head of
+        the last position: float32 for the reference model; for the INT8 path
+        the per-tensor quantized_linear (GI:59-88) when quantize_lm_head."""
+        eps = self.w.cfg["rms_norm_eps"]
+        g = self.w.final_norm_w()
+        head = self.w.lm_head_w()
+        ref_logits = TL.linear(TL.rms_norm(self.float_x, g, eps)[-1:], head)
+        last = TL.rms_norm(self.int8_x, g, eps)[-1:]
+        if quantize_lm_head:
+            mix_logits, dbg = quantized_linear(last, head, None, capture_arrays=keep_debug)
+            return ref_logits, mix_logits, dbg
+        return ref_logits, TL.linear(last, head), {}
 
 
 def run_analysis(prompt: str | None, token_ids_arg: str | None, weights_path, layer_count: int,
                  dump_layer: int | None = None, dump_dir: str | None = None, local_files_only: bool = True,
                  top_k: int = 5, quantize_lm_head: bool = False, cache_arrays: bool = False,
                  tokenizer=None) -> dict:
-    """GI:470-626: one pass of the float32 model and of the INT8 path over the
-    prompt, layer by layer (isolated: both from the float32 input; cumulative:
-    the INT8 path from its own previous output), then the final logits of the
-    last position.  With dump_layer, that layer's debug dicts (and the LM
-    head's when quantized) are written by dump_debug to dump_dir.  The INT8
-    layers use the archive's static KV scales when it has them, else scales
-    calibrated on the prompt.  ``weights_path`` may also be a
-    TinyLlamaWeights.  Returns the summary lines and both tokens."""
+    """The GI:470-626 analysis: the float32 model and the INT8 path over the
+    prompt, compared layer by layer and on the final logits of the last
+    position; with dump_layer, that layer's debug dicts (and the quantized LM
+    head's) are written to dump_dir.  The INT8 layers use the archive's static
+    KV scales when it has them, else scales calibrated on the prompt.
+    ``weights_path`` may also be a TinyLlamaWeights.  Returns the summary
+    lines, both next tokens and both logit rows."""
     weights = weights_path if isinstance(weights_path, TinyLlamaWeights) else load_weights(
         weights_path, cache_arrays=cache_arrays)
     cfg = weights.cfg
     validate_layer_count(cfg, layer_count)
-    if tokenizer is None and prompt is not None and token_ids_arg is None:
+    wants_text = prompt is not None and token_ids_arg is None
+    if tokenizer is None and wants_text:
         tokenizer = maybe_load_tokenizer(cfg["model_id"], local_files_only=local_files_only)
     token_ids = resolve_token_ids(prompt, token_ids_arg, tokenizer)
-    cos, sin = build_rope_cache(cfg["max_position_embeddings"], cfg["head_dim"], cfg["rope_theta"])
-    if dump_layer is not None and (dump_layer < 0 or dump_layer >= layer_count):
+    if dump_layer is not None and not 0 <= dump_layer < layer_count:
         raise ValueError("--dump-layer must be within the executed layer range")
+    cos, sin = build_rope_cache(cfg["max_position_embeddings"], cfg["head_dim"], cfg["rope_theta"])
     print_token_context(token_ids, tokenizer)
 
-    x_ref = np.asarray(weights.embed(token_ids), np.float32)
-    x_mix = x_ref.copy()
-    summary_lines = [f"Token ids: {token_ids}", f"Layers analyzed: {layer_count}", "Layer stats:"]
-    dump_reference: dict[str, Any] | None = None
-    dump_mixed: dict[str, Any] | None = None
-    scales = weights.kv_scales()
-    for layer_idx in range(layer_count):
-        layer = weights.layer(layer_idx)
-        capture = dump_layer == layer_idx
-        kv = None if scales is None else (scales[0][layer_idx], scales[1][layer_idx])
-        ref_out, ref_debug = reference_decoder_layer(x_ref, layer, cfg, cos, sin, capture_arrays=capture)
-        iso_mix_out, iso_mix_debug = mixed_precision_decoder_layer(x_ref, layer, cfg, cos, sin,
-                                                                   capture_arrays=capture, kv_scales=kv)
-        cum_mix_out, _ = mixed_precision_decoder_layer(x_mix, layer, cfg, cos, sin, capture_arrays=False,
-                                                       kv_scales=kv)
-        isolated = diff_stats(ref_out, iso_mix_out)
-        cumulative = diff_stats(ref_out, cum_mix_out)
-        line = (f"Layer {layer_idx}: "
-                f"isolated MAE={isolated['mae']:.6f}, isolated max={isolated['max_abs']:.6f}, "
-                f"cumulative MAE={cumulative['mae']:.6f}, cumulative max={cumulative['max_abs']:.6f}")
-        print(line)
-        summary_lines.append(line)
-        if capture:
-            dump_reference, dump_mixed = ref_debug, iso_mix_debug
-            ra, ma, rf, mf = ref_debug["attn"], iso_mix_debug["attn"], ref_debug["ffn"], iso_mix_debug["ffn"]
-            breakdown = [
-                projection_stats_line("  attn q_proj", ra["q_proj_fp"], ma["q_proj_fp"]),
-                projection_stats_line("  attn k_proj", ra["k_proj_fp"], ma["k_proj_fp"]),
-                projection_stats_line("  attn v_proj", ra["v_proj_fp"], ma["v_proj_fp"]),
-                projection_stats_line("  ffn gate_proj", rf["gate_proj_fp"], mf["gate_proj_fp"]),
-                projection_stats_line("  ffn up_proj", rf["up_proj_fp"], mf["up_proj_fp"]),
-            ]
-            if "out_fp" in ra and "out_fp" in ma:
-                breakdown.append(projection_stats_line("  attn o_proj", ra["out_fp"], ma["out_fp"]))
-            if "out_fp" in rf and "out_fp" in mf:
-                breakdown.append(projection_stats_line("  ffn down_proj", rf["out_fp"], mf["out_fp"]))
-            for b in breakdown:
-                print(b)
-                summary_lines.append(b)
-        x_ref, x_mix = ref_out, cum_mix_out
+    rep = _Report(token_ids, layer_count)
+    walk = _LayerComparison(weights, token_ids, cos, sin, dump_layer)
+    for index in range(layer_count):
+        iso, cum, breakdown = walk.step(index)
+        rep.both(f"Layer {index}: isolated MAE={iso['mae']:.6f}, isolated max={iso['max_abs']:.6f}, "
+                 f"cumulative MAE={cum['mae']:.6f}, cumulative max={cum['max_abs']:.6f}")
+        for line in breakdown:
+            rep.both(line)
 
-    eps = cfg["rms_norm_eps"]
-    x_ref = TL.rms_norm(x_ref, weights.final_norm_w(), eps)
-    x_mix = TL.rms_norm(x_mix, weights.final_norm_w(), eps)
-    ref_logits = TL.linear(x_ref[-1:], weights.lm_head_w())
-    lm_debug: dict[str, Any] = {}
-    if quantize_lm_head:
-        mix_logits, lm_debug = quantized_linear(x_mix[-1:], weights.lm_head_w(), None,
-                                                capture_arrays=dump_dir is not None)
-    else:
-        mix_logits = TL.linear(x_mix[-1:], weights.lm_head_w())
-    logit_stats = diff_stats(ref_logits, mix_logits)
-    ref_token = int(np.argmax(ref_logits[0]))
-    mix_token = int(np.argmax(mix_logits[0]))
+    ref_logits, mix_logits, lm_dbg = walk.final_logits(quantize_lm_head, keep_debug=dump_dir is not None)
+    st = diff_stats(ref_logits, mix_logits)
+    picks = {"Float32": int(np.argmax(ref_logits[0])), "INT8 path": int(np.argmax(mix_logits[0]))}
+    token_lines = [f"{who} next token: {tok} -> '{safe_repr(decode_token(tokenizer, tok))}'"
+                   for who, tok in picks.items()]
+    rep.say()
+    rep.say(f"Final logits: MAE={st['mae']:.6f}, RMSE={st['rmse']:.6f}, max_abs={st['max_abs']:.6f}")
+    for line in token_lines:
+        rep.say(line)
+    for title, row in ((f"Top {top_k} float32 tokens:", ref_logits[0]), (f"Top {top_k} INT8-path tokens:", mix_logits[0])):
+        rep.say()
+        rep.say(title)
+        for tok, value, text in top_tokens(row, tokenizer, top_k):
+            rep.say(f"  {tok:6d}  {value:12.6f}  '{safe_repr(text)}'")
+    rep.note("")
+    rep.note(f"Final logits: mae={st['mae']:.6f}, rmse={st['rmse']:.6f}, max_abs={st['max_abs']:.6f}")
+    for line in token_lines:
+        rep.note(line)
 
-    print("")
-    print(f"Final logits: MAE={logit_stats['mae']:.6f}, "
-          f"RMSE={logit_stats['rmse']:.6f}, max_abs={logit_stats['max_abs']:.6f}")
-    print(f"Float32 next token: {ref_token} -> '{safe_repr(decode_token(tokenizer, ref_token))}'")
-    print(f"INT8 path next token: {mix_token} -> '{safe_repr(decode_token(tokenizer, mix_token))}'")
-    print("")
-    print(f"Top {top_k} float32 tokens:")
-    for idx, value, decoded in top_tokens(ref_logits[0], tokenizer, top_k):
-        print(f"  {idx:6d}  {value:12.6f}  '{safe_repr(decoded)}'")
-    print("")
-    print(f"Top {top_k} INT8-path tokens:")
-    for idx, value, decoded in top_tokens(mix_logits[0], tokenizer, top_k):
-        print(f"  {idx:6d}  {value:12.6f}  '{safe_repr(decoded)}'")
-    summary_lines.extend([
-        "",
-        f"Final logits: mae={logit_stats['mae']:.6f}, rmse={logit_stats['rmse']:.6f}, "
-        f"max_abs={logit_stats['max_abs']:.6f}",
-        f"Float32 next token: {ref_token} -> '{safe_repr(decode_token(tokenizer, ref_token))}'",
-        f"INT8 path next token: {mix_token} -> '{safe_repr(decode_token(tokenizer, mix_token))}'",
-    ])
     if dump_dir is not None:
-        arrays_mix = dict(dump_mixed or {})
-        if quantize_lm_head and lm_debug:
-            arrays_mix["lm_head"] = lm_debug
-        dump_debug(dump_dir, token_ids, dump_reference or {}, arrays_mix, summary_lines)
-        print("")
-        print(f"Saved debug dump to {dump_dir}")
-    return {"summary_lines": summary_lines, "ref_token": ref_token, "mix_token": mix_token,
+        f_dbg, m_dbg = walk.dumped if walk.dumped is not None else ({}, {})
+        if lm_dbg:
+            m_dbg = {**m_dbg, "lm_head": lm_dbg}
+        dump_debug(dump_dir, token_ids, f_dbg, m_dbg, rep.kept)
+        rep.say()
+        rep.say(f"Saved debug dump to {dump_dir}")
+    return {"summary_lines": rep.kept, "ref_token": picks["Float32"], "mix_token": picks["INT8 path"],
             "ref_logits": ref_logits, "mix_logits": mix_logits}
 
 
-def main(argv: list[str] | None = None) -> None:
-    """GI:688-745: --mode analysis | generate."""
+def build_arg_parser():
+    """The reference's command line (GI:688-717 flags and defaults; --weights
+    is required here: no archive ships with this build)."""
     import argparse
-    parser = argparse.ArgumentParser()
-    parser.add_argument("--mode", choices=["analysis", "generate"], default="analysis",
-                        help="analysis = one-pass float32 vs INT8 comparison, generate = autoregressive INT8-path "
-                             "generation")
-    parser.add_argument("--prompt", type=str, default=None)
-    parser.add_argument("--token-ids", type=str, default=None)
-    parser.add_argument("--weights", type=str, required=True)
-    parser.add_argument("--layers", type=int, default=1)
-    parser.add_argument("--max-tokens", type=int, default=20)
-    parser.add_argument("--dump-layer", type=int, default=None)
-    parser.add_argument("--dump-dir", type=str, default=None)
-    parser.add_argument("--top-k", type=int, default=5)
-    parser.add_argument("--local-files-only", action="store_true")
-    parser.add_argument("--cache-arrays", action="store_true")
-    parser.add_argument("--quantize-lm-head", action="store_true",
-                        help="Also quantize the final vocab projection (always on in --mode generate).")
-    args = parser.parse_args(argv)
+    ap = argparse.ArgumentParser(description="INT8 TinyLlama decoder path on MI355X: float32-vs-INT8 analysis "
+                                             "or greedy generation")
+    ap.add_argument("--mode", choices=["analysis", "generate"], default="analysis",
+                    help="analysis = one-pass float32 vs INT8 comparison, generate = autoregressive INT8-path "
+                         "generation")
+    for flag, kind, default in (("--prompt", str, None), ("--token-ids", str, None), ("--layers", int, 1),
+                                ("--max-tokens", int, 20), ("--dump-layer", int, None), ("--dump-dir", str, None),
+                                ("--top-k", int, 5)):
+        ap.add_argument(flag, type=kind, default=default)
+    ap.add_argument("--weights", type=str, required=True)
+    for flag in ("--local-files-only", "--cache-arrays"):
+        ap.add_argument(flag, action="store_true")
+    ap.add_argument("--quantize-lm-head", action="store_true",
+                    help="Also quantize the final vocab projection (always on in --mode generate).")
+    return ap
+
+
+def main(argv: list[str] | None = None) -> None:
+    """Command-line entry: --mode analysis (run_analysis) or --mode generate
+    (run_generate)."""
+    args = build_arg_parser().parse_args(argv)
     if not os.path.exists(args.weights):
         raise FileNotFoundError(f"Weights not found at {args.weights}. Run model/tinyllama.py --save-weights first.")
-    if args.mode == "generate":
-        if args.dump_layer is not None or args.dump_dir is not None:
-            raise ValueError("--dump-layer and --dump-dir are only supported in --mode analysis")
-        tok = maybe_load_tokenizer(load_weights(args.weights).cfg["model_id"], args.local_files_only) \
-            if args.prompt is not None and args.token_ids is None else None
-        run_generate(args.prompt, args.token_ids, args.weights, args.layers, args.max_tokens,
-                     local_files_only=args.local_files_only, quantize_lm_head=True, cache_arrays=args.cache_arrays,
-                     tokenizer=tok)
+    if args.mode == "analysis":
+        run_analysis(args.prompt, args.token_ids, args.weights, args.layers, dump_layer=args.dump_layer,
+                     dump_dir=args.dump_dir, local_files_only=args.local_files_only, top_k=args.top_k,
+                     quantize_lm_head=args.quantize_lm_head, cache_arrays=args.cache_arrays)
         return
-    run_analysis(args.prompt, args.token_ids, args.weights, args.layers, dump_layer=args.dump_layer,
-                 dump_dir=args.dump_dir, local_files_only=args.local_files_only, top_k=args.top_k,
-                 quantize_lm_head=args.quantize_lm_head, cache_arrays=args.cache_arrays)
-
+    if args.dump_layer is not None or args.dump_dir is not None:
+        raise ValueError("--dump-layer and --dump-dir are only supported in --mode analysis")
+    tokenizer = None
+    if args.prompt is not None and args.token_ids is None:
+        tokenizer = maybe_load_tokenizer(load_weights(args.weights).cfg["model_id"], args.local_files_only)
+    run_generate(args.prompt, args.token_ids, args.weights, args.layers, args.max_tokens,
+                 local_files_only=args.local_files_only, quantize_lm_head=True, cache_arrays=args.cache_arrays,
+                 tokenizer=tokenizer)

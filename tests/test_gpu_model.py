@@ -302,6 +302,32 @@ def test_decode_batch_tinyllama_heads(hpw, monkeypatch):
     eng.close()
 
 
+def test_decode_timeline_steps_are_decode_steps(small_model):
+    """tl_decode_timeline runs ordinary greedy steps from a graph captured
+    with clock stamps: decoding on afterwards gives the tokens plain decode
+    gives, every kernel of the step is stamped, gaps are non-negative and the
+    per-class busy times and gaps add up to the step."""
+    eng = engine_for(small_model)
+    prompt = np.array([4, 8, 15, 16, 23, 42], np.int32)
+    eng.prefill(prompt)
+    want, _ = eng.decode(7)
+    eng.prefill(prompt)
+    tl = eng.decode_timeline(4)
+    rest, _ = eng.decode(3)
+    assert_bits_equal(rest, want[4:], "tokens after the timeline steps")
+    L = small_model.cfg["n_layers"]
+    assert tl["steps"] == 4 and tl["kernels"] == 5 * L + 2
+    cls = tl["classes"]
+    assert {k: v["launches"] for k, v in cls.items()} == {"qkv": L, "attn": L, "o": L, "glu": L, "down": L,
+                                                         "lm_head": 1, "other": 1}
+    busy = sum(v["busy_us"] for v in cls.values())
+    gaps = sum(v["gap_us"] for v in cls.values())
+    assert all(v["busy_us"] > 0 for v in cls.values())
+    assert all(v["gap_us"] >= 0 for k, v in cls.items() if k != "other")
+    assert abs(busy + gaps - tl["step_us"]) < 1e-6 * tl["step_us"] + 1e-3
+    eng.close()
+
+
 def test_graph_replay_equals_direct_launches(small_model):
     """The captured decode step (HIP graph) and direct launches give the same tokens."""
     import os
