@@ -121,6 +121,19 @@ int32_t tl_gemv_i8_requant(tl_handle *h, const int8_t *x, const int8_t *w, const
                            int32_t n, int32_t k, int8_t *y, int32_t *acc);
 /* INT8 GEMM with INT32 accumulators (GI:70): c[M][N] = a[M][K] . w[N][K]^T. */
 int32_t tl_gemm_i8(tl_handle *h, const int8_t *a, const int8_t *w, int32_t m, int32_t n, int32_t k, int32_t *c);
+/* tl_gemm_i8 without any allocation, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference.  Same kernels and
+ * results as tl_gemm_i8; the split-K scratch of its M <= 32, K > 2048 path
+ * (partial tiles and per-tile arrival counters) is a fixed per-GPU device
+ * array of 2 MiB + 1 KiB instead of a handle buffer grown with hipMalloc.  A
+ * shape whose scratch would exceed it fails with TL_ERR_UNSUPPORTED (no shape
+ * tl_gemm_i8 accepts needs more).  Every call on a GPU shares that array and
+ * finds the last call's contents (the counters are cleared at the start of
+ * each call): calls that overlap on one GPU race.  No profiling events are
+ * taken. */
+int32_t tl_gemm_i8_noalloc(tl_handle *h, const int8_t *a, const int8_t *w, int32_t m, int32_t n, int32_t k,
+                           int32_t *c);
 /* GEMM + GI:45-46 dequantization per row/channel, optional residual (GI:266):
  * y[m][n] = residual[m][n] + f32(acc) * f32(a_scales[m] * w_scales[n]). */
 int32_t tl_gemm_i8_dequant(tl_handle *h, const int8_t *a, const double *a_scales, const int8_t *w,

@@ -9,6 +9,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -56,6 +57,32 @@ struct ProfEvent {
 
 thread_local std::string g_create_error;
 
+// ---- fixed scratch of tl_gemm_i8_noalloc ---------------------------------------
+// One copy per GPU of this file-scope device array: the split-K partial tiles
+// of the small-M GEMM (tiles x slices x 1024 int32 with tiles x slices < 512,
+// so at most 2 MiB) and 256 per-tile arrival counters.  Host code never
+// passes the array's name: tl_create looks up the current device's copy with
+// hipGetSymbolAddress once per device and every handle keeps that address.
+constexpr size_t kNoAllocPartials = (size_t)512 * 1024;   // int32 elements
+constexpr int32_t kNoAllocCounters = 256;
+static __device__ __align__(256) int32_t scratch[kNoAllocPartials + kNoAllocCounters];
+
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch_dev;   // device address of `scratch`, by device ordinal
+
+hipError_t scratch_address(int dev, void** out) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if ((int)g_scratch_dev.size() <= dev) g_scratch_dev.resize(dev + 1, nullptr);
+    if (!g_scratch_dev[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch_dev[dev] = p;
+    }
+    *out = g_scratch_dev[dev];
+    return hipSuccess;
+}
+
 }  // namespace
 
 struct tl_handle {
@@ -95,6 +122,7 @@ struct tl_handle {
     int32_t* row_pos = nullptr;
     int32_t* tokens = nullptr;    // [max_rows]
     int8_t* kv_stage = nullptr;   // [2][max_pos][64] staging of tl_kv_write / tl_kv_read rows
+    int32_t* noalloc_scratch = nullptr;   // this device's copy of `scratch` (tl_gemm_i8_noalloc)
     float* fscratch = nullptr;    // small scratch
     unsigned long long* op_key = nullptr;  // argmax slot of the standalone LM-head operator
     unsigned long long* lm_wg_keys = nullptr;  // [vocab / 4] batch-1 LM head: argmax key per workgroup
@@ -219,10 +247,11 @@ struct Prof {
     tl_handle* h;
     int kc;
     double bytes;
+    bool on;
     hipEvent_t a = nullptr, b = nullptr;
     KernelTiming saved;
-    Prof(tl_handle* hh, int k, double bb) : h(hh), kc(k), bytes(bb) {
-        if (!h->profiling) return;
+    Prof(tl_handle* hh, int k, double bb, bool allow = true) : h(hh), kc(k), bytes(bb), on(hh->profiling && allow) {
+        if (!on) return;
         a = take_event(h);
         b = take_event(h);
         if (!a || !b) return;
@@ -230,7 +259,7 @@ struct Prof {
         kernel_timing() = KernelTiming{a, b, false};
     }
     ~Prof() {
-        if (!h->profiling) return;
+        if (!on) return;
         if (a && b) {
             const bool used = kernel_timing().used;
             kernel_timing() = saved;
@@ -313,15 +342,25 @@ int32_t ensure_partials(tl_handle* h, size_t need) {
     return TL_OK;
 }
 
-int32_t run_gemm(tl_handle* h, int epi, GemmArgs a, int kclass) {
+// caller-fixed scratch for the split-K small-M GEMM (the no-allocation entry
+// point): partial tiles and per-tile arrival counters
+struct FixedScratch {
+    int32_t* part;
+    size_t part_cap;      // int32 elements
+    unsigned* ctr;
+    int32_t ctr_cap;      // counters
+};
+
+int32_t run_gemm(tl_handle* h, int epi, GemmArgs a, int kclass, const FixedScratch* fx = nullptr) {
     const int nb = epi == EPI_GLU ? 2 : 1;
+    const bool prof_ok = fx == nullptr;   // profiling events are allocations
     const double bytes = (double)a.m * a.k + (double)nb * a.n * a.k + (double)a.m * a.n * 4.0;
     if (a.m >= 64) {
         // 32x32x32 MFMA tiles; 64 x 64 blocks with two K-slice wavefront
         // groups measured fastest at M = 512 (TL_GEMM_CFG overrides)
         const int cfg = h->gemm_cfg >= 0 ? h->gemm_cfg : 0;
         a.k_split = a.k;
-        Prof p(h, kclass, bytes);
+        Prof p(h, kclass, bytes, prof_ok);
         TL_LAUNCH(h, launch_gemm32(h->stream, epi, a, 1, cfg));
         return TL_OK;
     }
@@ -331,7 +370,7 @@ int32_t run_gemm(tl_handle* h, int epi, GemmArgs a, int kclass) {
         // workgroup per 32 output columns, every weight load a coalesced 1 KiB
         // (measured faster than splitting K over workgroups: the cross-XCD
         // reduction of the partial tiles costs more than the added bandwidth)
-        Prof p(h, kclass, bytes);
+        Prof p(h, kclass, bytes, prof_ok);
         TL_LAUNCH(h, launch_gemm_rows32(h->stream, epi, a));
         return TL_OK;
     }
@@ -343,13 +382,27 @@ int32_t run_gemm(tl_handle* h, int epi, GemmArgs a, int kclass) {
         int slices = 1;
         while (tiles * slices < 256 && kch / (4 * slices * 2) >= 2 && slices < kSkinnyMaxSlices) slices *= 2;
         if (tiles > kSkinnyTiles) slices = 1;
-        if (slices > 1) {
+        int32_t* part = h->partials;
+        unsigned* ctr = h->tile_ctr;
+        const bool skinny = h->gemm_small == 1 || a.k > 2048;
+        if (fx) {
+            if (skinny && slices > 1) {
+                if ((size_t)tiles * slices * nb * 1024 > fx->part_cap || tiles > fx->ctr_cap)
+                    return fail(h, TL_ERR_UNSUPPORTED, "GEMM needs more split-K scratch than the fixed " +
+                                                           std::to_string(fx->part_cap * 4) + "-byte buffer holds");
+                // the counters start at zero (the last workgroup of a tile resets its own)
+                TL_LAUNCH(h, launch_fill_u32(h->stream, fx->ctr, tiles, 0u));
+            }
+            part = fx->part;
+            ctr = fx->ctr;
+        } else if (slices > 1) {
             int32_t r = ensure_partials(h, (size_t)tiles * slices * nb * 1024);
             if (r) return r;
+            part = h->partials;
         }
-        Prof p(h, kclass, bytes);
-        if (h->gemm_small == 1 || a.k > 2048)
-            TL_LAUNCH(h, launch_gemm_skinny(h->stream, epi, a, slices, h->partials, h->tile_ctr));
+        Prof p(h, kclass, bytes, prof_ok);
+        if (skinny)
+            TL_LAUNCH(h, launch_gemm_skinny(h->stream, epi, a, slices, part, ctr));
         else TL_LAUNCH(h, launch_gemm_rows32(h->stream, epi, a));
         return TL_OK;
     }
@@ -363,11 +416,12 @@ int32_t run_gemm(tl_handle* h, int epi, GemmArgs a, int kclass) {
     a.k_split = ((a.k / 64 + splits - 1) / splits) * 64;
     splits = (a.k + a.k_split - 1) / a.k_split;
     if (splits > 1) {
+        if (fx) return fail(h, TL_ERR_UNSUPPORTED, "split GEMM of 33..63 rows has no fixed-scratch form");
         int32_t r = ensure_partials(h, (size_t)splits * nb * a.m * a.n);
         if (r) return r;
         a.acc = h->partials;
     }
-    Prof p(h, kclass, bytes);
+    Prof p(h, kclass, bytes, prof_ok);
     TL_LAUNCH(h, launch_gemm(h->stream, epi, a, splits));
     if (splits > 1) TL_LAUNCH(h, launch_gemm_reduce(h->stream, epi, a, splits));
     return TL_OK;
@@ -832,6 +886,11 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
         (e = hipMemcpy(h->rope_sin, sn.data(), sn.size() * sizeof(float), hipMemcpyHostToDevice)))
         return bad(e);
     h->rope_n = c.max_pos;
+    {
+        void* sp = nullptr;
+        if ((e = scratch_address(dev, &sp))) return bad(e);
+        h->noalloc_scratch = (int32_t*)sp;
+    }
     if ((e = init_kernels())) return bad(e);
     if ((e = init_decode_kernels())) return bad(e);
     if ((e = init_prefill_kernels())) return bad(e);
@@ -1060,6 +1119,21 @@ int32_t tl_gemm_i8(tl_handle* h, const int8_t* a, const int8_t* w, int32_t m, in
     GemmArgs g{};
     g.a = a; g.w = w; g.acc = c; g.m = m; g.n = n; g.k = k;
     int32_t r = run_gemm(h, EPI_RAW, g, TL_K_GEMM_PREFILL);
+    if (r) return r;
+    return finish(h);
+}
+
+int32_t tl_gemm_i8_noalloc(tl_handle* h, const int8_t* a, const int8_t* w, int32_t m, int32_t n, int32_t k,
+                           int32_t* c) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, a && w && c && m > 0 && n > 0, "bad gemm arguments");
+    TL_REQ(h, k > 0 && k % 64 == 0, "K must be a positive multiple of 64");
+    TL_REQ(h, h->noalloc_scratch, "no fixed scratch on this device");
+    GemmArgs g{};
+    g.a = a; g.w = w; g.acc = c; g.m = m; g.n = n; g.k = k;
+    const FixedScratch fx{h->noalloc_scratch, kNoAllocPartials, (unsigned*)(h->noalloc_scratch + kNoAllocPartials),
+                          kNoAllocCounters};
+    int32_t r = run_gemm(h, EPI_RAW, g, TL_K_GEMM_PREFILL, &fx);
     if (r) return r;
     return finish(h);
 }
