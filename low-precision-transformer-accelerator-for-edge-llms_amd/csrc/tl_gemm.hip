@@ -306,12 +306,211 @@ __global__ __launch_bounds__(WM * WN * KS * 64) void gemm32_kernel(GemmArgs a) {
         }
 }
 
+// ---------------------------------------------------------------------------
+// Block-tiled GEMM for prefill-sized M: WM x WN wavefronts, each owning
+// TM x TN blocks of 32 x 32 outputs (of each matrix for the GLU epilogue).
+// K advances BK bytes per stage through two LDS buffers with one barrier per
+// stage, so a wavefront issues BK / 32 x TM x TN x NB MFMAs between barriers
+// (16 at the 2 x 2 blocks and BK = 128 of the default).  Global loads run PD
+// stages ahead in register sets: stage k + PD is loaded while stage k
+// computes.  Every fragment of a stage is read from LDS before its MFMAs.
+// ---------------------------------------------------------------------------
+template <int WM, int WN, int TM, int TN, int BK, int PD, int EPI>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_tile_kernel(GemmArgs a) {
+    constexpr int NT = WM * WN * 64, BM = 32 * TM * WM, BN = 32 * TN * WN, CPR = BK / 16, SL = BK / 32;
+    constexpr int NB = (EPI == EPI_GLU) ? 2 : 1;
+    constexpr int ACH = BM * CPR, BCH = BN * CPR;   // 16-byte chunks per operand tile
+    static_assert(ACH % NT == 0 && BCH % NT == 0, "tile does not split evenly over threads");
+    constexpr int APT = ACH / NT, BPT = BCH / NT;
+    constexpr int STAGE = ACH + NB * BCH;            // chunks per LDS buffer
+    __shared__ v4i lds[2 * STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int nk = a.k / BK;
+
+    // staging: chunk c = tid + NT j -> row c / CPR, K chunk c % CPR
+    const int8_t* asrc[APT];
+    const int8_t* bsrc[NB][BPT];
+#pragma unroll
+    for (int j = 0; j < APT; j++) {
+        const int c = tid + NT * j;
+        asrc[j] = a.a + (int64_t)min(m0 + c / CPR, a.m - 1) * a.k + (c % CPR) * 16;
+    }
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int j = 0; j < BPT; j++) {
+            const int c = tid + NT * j;
+            bsrc[b][j] = (b ? a.w2 : a.w) + (int64_t)min(n0 + c / CPR, a.n - 1) * a.k + (c % CPR) * 16;
+        }
+    v4i ra[PD][APT], rb[PD][NB][BPT];
+    auto gload = [&](int set, int stage) {
+        const int kk = stage * BK;
+#pragma unroll
+        for (int j = 0; j < APT; j++) ra[set][j] = ld16(asrc[j] + kk);
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int j = 0; j < BPT; j++) rb[set][b][j] = ld16(bsrc[b][j] + kk);
+    };
+    auto lstore = [&](int set, int buf) {
+        v4i* base = lds + buf * STAGE;
+#pragma unroll
+        for (int j = 0; j < APT; j++) {
+            const int c = tid + NT * j;
+            base[swz<CPR>(c / CPR, c % CPR)] = ra[set][j];
+        }
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int j = 0; j < BPT; j++) {
+                const int c = tid + NT * j;
+                base[ACH + b * BCH + swz<CPR>(c / CPR, c % CPR)] = rb[set][b][j];
+            }
+    };
+
+    v16i acc[NB][TM][TN];
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc[b][i][j][e] = 0;
+
+    const int fr = lane & 31, fk = lane >> 5;   // fragment row, 16-byte chunk inside a 32-byte K slice
+    auto compute = [&](int buf) {
+        const v4i* base = lds + buf * STAGE;
+        v4i af[SL][TM], bf[SL][NB][TN];
+#pragma unroll
+        for (int q = 0; q < SL; q++) {
+            const int kc = q * 2 + fk;
+#pragma unroll
+            for (int i = 0; i < TM; i++) af[q][i] = base[swz<CPR>(wm * 32 * TM + i * 32 + fr, kc)];
+#pragma unroll
+            for (int b = 0; b < NB; b++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) bf[q][b][j] = base[ACH + b * BCH + swz<CPR>(wn * 32 * TN + j * 32 + fr, kc)];
+        }
+#pragma unroll
+        for (int q = 0; q < SL; q++)
+#pragma unroll
+            for (int b = 0; b < NB; b++)
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        acc[b][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[q][i], bf[q][b][j], acc[b][i][j], 0, 0, 0);
+    };
+
+    // stage k: store register set k % PD into buffer k % 2 (its last reader,
+    // stage k - 2, finished before the barrier of stage k - 1), reload the set
+    // with stage k + PD (clamped: a redundant in-bounds reload past the end),
+    // barrier, compute
+#pragma unroll
+    for (int u = 0; u < PD; u++) gload(u, min(u, nk - 1));
+    int k = 0;
+    for (; k + PD <= nk; k += PD) {
+#pragma unroll
+        for (int u = 0; u < PD; u++) {
+            lstore(u, (k + u) & 1);
+            gload(u, min(k + u + PD, nk - 1));
+            __syncthreads();
+            compute((k + u) & 1);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < PD; u++) {
+        if (k + u < nk) {
+            lstore(u, (k + u) & 1);
+            __syncthreads();
+            compute((k + u) & 1);
+        }
+    }
+
+    // epilogue (lane l, register e of a 32 x 32 block: row 8 (e / 4) +
+    // 4 (l / 32) + e % 4, column l % 32); all loads before the first store
+    const int rbase = m0 + wm * 32 * TM + 4 * (lane >> 5);
+    const int cbase = n0 + wn * 32 * TN + (lane & 31);
+    if (EPI == EPI_RAW) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const int n = cbase + j * 32;
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int m = rbase + i * 32 + 8 * (e >> 2) + (e & 3);
+                    if (m < a.m && n < a.n) a.acc[(int64_t)m * a.n + n] = acc[0][i][j][e];
+                }
+            }
+        return;
+    }
+    double sx[TM][16];
+    float sw[NB][TN];
+    float res[TM][TN][EPI == EPI_DEQUANT_RES ? 16 : 1];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) sx[i][e] = a.as[min(rbase + i * 32 + 8 * (e >> 2) + (e & 3), a.m - 1)];
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        const int n = min(cbase + j * 32, a.n - 1);
+        sw[0][j] = a.ws[n];
+        if (EPI == EPI_GLU) sw[NB - 1][j] = a.ws2[n];
+    }
+    if (EPI == EPI_DEQUANT_RES) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int m = min(rbase + i * 32 + 8 * (e >> 2) + (e & 3), a.m - 1);
+                    res[i][j][e] = a.residual[(int64_t)m * a.n + min(cbase + j * 32, a.n - 1)];
+                }
+    }
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = cbase + j * 32;
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int m = rbase + i * 32 + 8 * (e >> 2) + (e & 3);
+                const float v0 = (float)acc[0][i][j][e] * deq_mult(sx[i][e], sw[0][j]);
+                float out;
+                if (EPI == EPI_GLU) {
+                    const float up = (float)acc[NB - 1][i][j][e] * deq_mult(sx[i][e], sw[NB - 1][j]);
+                    out = tl_silu(v0) * up;
+                } else if (EPI == EPI_DEQUANT_RES) {
+                    out = res[i][j][e] + v0;
+                } else {
+                    out = v0;
+                }
+                if (m < a.m && n < a.n) a.y[(int64_t)m * a.n + n] = out;
+            }
+        }
+}
+
 // Tile configurations (index = cfg):
 //        waves (M x N x K)  wave tile  block tile  BK   register sets
 //   0:   2 x 2 x 2          32 x 32    64 x 64     128  3    (default)
 //   1:   2 x 2 x 2          64 x 32    128 x 64    128  3
 //   2:   2 x 2 x 2          32 x 64    64 x 128    128  3
 //   3:   2 x 2 x 2          32 x 32    64 x 64     256  3
+// and gemm_tile_kernel (one K slice group, two LDS buffers, one barrier per stage):
+//        waves (M x N)  blocks per wave  block tile  BK   register sets
+//   4:   2 x 2          2 x 2            128 x 128   128  2
+//   5:   2 x 2          2 x 1            128 x 64    128  3
+//   8:   2 x 2          1 x 1            64 x 64     128  4    (default; K a multiple of 128)
+// At M = 512 (one 22-layer TinyLlama prefill, GEMMs bit-identical across all
+// of them) cfg 8 measured fastest: GEMMs 1.41 ms against 1.61 ms for cfg 0;
+// the larger block tiles leave CUs idle at these N and were slower
+// (cfg 4: 2.22 ms).  Without K a multiple of 128, cfg 0 runs.
 template <int WM, int WN, int TM, int TN, int BK, int PD, int KS, int EPI>
 static void go32(hipStream_t s, const GemmArgs& a, int32_t splits) {
     using G = GemmShape<WM, WN, TM, TN, BK, PD, KS>;
@@ -319,9 +518,22 @@ static void go32(hipStream_t s, const GemmArgs& a, int32_t splits) {
     TL_KLAUNCH((gemm32_kernel<WM, WN, TM, TN, BK, PD, KS, EPI>), grid, dim3(G::kThreads), 0, s, a);
 }
 
+template <int WM, int WN, int TM, int TN, int BK, int PD, int EPI>
+static bool go_tile(hipStream_t s, const GemmArgs& a) {
+    constexpr int BM = 32 * TM * WM, BN = 32 * TN * WN;
+    if (a.k % BK) return false;
+    const dim3 grid((a.n + BN - 1) / BN, (a.m + BM - 1) / BM, 1);
+    TL_KLAUNCH((gemm_tile_kernel<WM, WN, TM, TN, BK, PD, EPI>), grid, dim3(WM * WN * 64), 0, s, a);
+    return true;
+}
+
 template <int EPI>
 static bool shape32(hipStream_t s, const GemmArgs& a, int32_t splits, int cfg) {
+    if (cfg >= 4 && splits != 1) return false;
     switch (cfg) {
+        case 4: return go_tile<2, 2, 2, 2, 128, 2, EPI>(s, a);
+        case 5: return go_tile<2, 2, 2, 1, 128, 3, EPI>(s, a);
+        case 8: return go_tile<2, 2, 1, 1, 128, 4, EPI>(s, a);
         case 0: go32<2, 2, 1, 1, 128, 3, 2, EPI>(s, a, splits); return true;
         case 1: go32<2, 2, 2, 1, 128, 3, 2, EPI>(s, a, splits); return true;
         case 2: go32<2, 2, 1, 2, 128, 3, 2, EPI>(s, a, splits); return true;

@@ -168,6 +168,7 @@ struct tl_handle {
     int32_t* pstatus = nullptr;
     int gemm_cfg = -1;                    // < 0: choose the MFMA tile configuration per shape
     std::vector<hipGraphExec_t> graphs;   // captured batch-1 decode step per sequence
+    std::vector<hipGraphExec_t> batch_graphs;   // captured batched decode step, by batch size
 
     bool profiling = false;
     // decode timeline: while ts_on, the launches of a step take consecutive
@@ -356,9 +357,10 @@ int32_t run_gemm(tl_handle* h, int epi, GemmArgs a, int kclass, const FixedScrat
     const bool prof_ok = fx == nullptr;   // profiling events are allocations
     const double bytes = (double)a.m * a.k + (double)nb * a.n * a.k + (double)a.m * a.n * 4.0;
     if (a.m >= 64) {
-        // 32x32x32 MFMA tiles; 64 x 64 blocks with two K-slice wavefront
-        // groups measured fastest at M = 512 (TL_GEMM_CFG overrides)
-        const int cfg = h->gemm_cfg >= 0 ? h->gemm_cfg : 0;
+        // 32x32x32 MFMA tiles: the 64 x 64 block-tiled kernel with 128-byte K
+        // stages (cfg 8) measured fastest at M = 512; K not a multiple of 128
+        // runs the two-K-slice kernel (cfg 0); TL_GEMM_CFG overrides
+        const int cfg = h->gemm_cfg >= 0 ? h->gemm_cfg : (a.k % 128 == 0 ? 8 : 0);
         a.k_split = a.k;
         Prof p(h, kclass, bytes, prof_ok);
         TL_LAUNCH(h, launch_gemm32(h->stream, epi, a, 1, cfg));
@@ -762,6 +764,45 @@ int32_t decode_graph_launch(tl_handle* h, int32_t seq) {
     return TL_OK;
 }
 
+// one batched decode step of sequences 0..n_seqs-1 (rows r = sequence r):
+// embed each sequence's current token at its cursor, the decoder layers at
+// M = n_seqs, the LM head with its argmax, then record the tokens and advance
+// the cursors.  Every argument is a fixed device pointer, so the step can be
+// captured once per batch size and replayed.
+int32_t batch_step(tl_handle* h, int32_t n_seqs, int32_t max_t) {
+    const tl_config& c = h->cfg;
+    TL_LAUNCH(h, launch_embed_step(h->stream, h->token_cur, h->row_seq, n_seqs, h->cursor, h->row_pos, h->D, c.vocab,
+                                   h->emb, h->emb_s, h->x));
+    int32_t r;
+    for (int l = 0; l < c.n_layers; l++)
+        if ((r = layer_rows(h, l, n_seqs, max_t, true))) return r;
+    return lm_head_rows(h, h->x, n_seqs, 0, 1);
+}
+
+// replay of the captured batched step (captured on first use for this batch
+// size, with the attention sized for the whole context)
+int32_t batch_graph_launch(tl_handle* h, int32_t n_seqs) {
+    if ((int)h->batch_graphs.size() <= h->max_seqs) h->batch_graphs.resize(h->max_seqs + 1, nullptr);
+    if (!h->batch_graphs[n_seqs]) {
+        TL_HIP(h, hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal));
+        int32_t r = batch_step(h, n_seqs, h->cfg.max_pos);
+        hipGraph_t cap = nullptr;
+        hipError_t e = hipStreamEndCapture(h->stream, &cap);
+        if (r) {
+            if (cap) hipGraphDestroy(cap);
+            return r;
+        }
+        TL_HIP(h, e);
+        hipGraphExec_t ex = nullptr;
+        e = hipGraphInstantiate(&ex, cap, nullptr, nullptr, 0);
+        hipGraphDestroy(cap);
+        TL_HIP(h, e);
+        h->batch_graphs[n_seqs] = ex;
+    }
+    TL_HIP(h, hipGraphLaunch(h->batch_graphs[n_seqs], h->stream));
+    return TL_OK;
+}
+
 }  // namespace
 
 // ===========================================================================
@@ -914,6 +955,8 @@ void tl_destroy(tl_handle* h) {
     }
     for (auto e : h->event_pool) hipEventDestroy(e);
     for (auto g : h->graphs)
+        if (g) hipGraphExecDestroy(g);
+    for (auto g : h->batch_graphs)
         if (g) hipGraphExecDestroy(g);
     for (void* p : h->allocs) hipFree(p);
     if (h->stream) hipStreamDestroy(h->stream);
@@ -1512,12 +1555,14 @@ int32_t tl_decode_batch(tl_handle* h, int32_t n_seqs, const int32_t* tokens, con
     TL_HIP(h, hipMemcpyAsync(h->cursor, start_pos, sizeof(int32_t) * n_seqs, hipMemcpyHostToDevice, h->stream));
     TL_HIP(h, hipMemcpyAsync(h->n_gen, zeros.data(), sizeof(int32_t) * n_seqs, hipMemcpyHostToDevice, h->stream));
     TL_LAUNCH(h, launch_reset_keys(h->stream, h->keys, n_seqs));
+    // the first step runs eagerly (it sizes the scratch the LM head's tile
+    // keys need), the rest replay the captured step
     for (int step = 0; step < n_steps; step++) {
-        TL_LAUNCH(h, launch_embed_step(h->stream, h->token_cur, h->row_seq, n_seqs, h->cursor, h->row_pos, h->D,
-                                       c.vocab, h->emb, h->emb_s, h->x));
-        for (int l = 0; l < c.n_layers; l++)
-            if ((r = layer_rows(h, l, n_seqs, max_t, true))) return r;
-        if ((r = lm_head_rows(h, h->x, n_seqs, 0, 1))) return r;
+        if (step > 0 && h->use_graphs && !h->profiling) {
+            if ((r = batch_graph_launch(h, n_seqs))) return r;
+        } else if ((r = batch_step(h, n_seqs, max_t))) {
+            return r;
+        }
     }
     if ((r = finish(h))) return r;
     for (int b = 0; b < n_seqs; b++) {
