@@ -115,6 +115,15 @@ int32_t tl_quantize_weight_rows(tl_handle *h, const float *w, int32_t rows, int3
 /* TL:45-50 rms_norm per row fused with GI:36-42 per-row quantization; y may be NULL. */
 int32_t tl_rmsnorm_quant(tl_handle *h, const float *x, const float *gamma, int32_t rows, int32_t n,
                          float *y, int8_t *q, double *scales);
+/* requantize_unit.sv:39-115 with its Q16.16 multiplier: y[i] =
+ * clamp(rne(acc[i] * scale_q16[i / lanes_per_scale] / 2^16)) where the
+ * product is exact in 64 bits, rounding is half to even on the magnitude's 16
+ * fraction bits, and the clamp is +-127, or [0, 127] with nonnegative_only;
+ * lanes i >= active give 0 (the unit's elem_count).  One multiplier per bank
+ * of lanes_per_scale lanes (32 in the reference: requantize_unit.sv:109,
+ * tinyllama_pkg.sv BANK_SLICE_INT8).  Device pointers. */
+int32_t tl_requant_q16(tl_handle *h, const int32_t *acc, const uint32_t *scale_q16, int32_t n, int32_t active,
+                       int32_t lanes_per_scale, int32_t nonnegative_only, int8_t *y);
 /* Decode GEMV + requantize (shared_gemm_engine.sv:126-135 + requantize_unit.sv:39-93):
  * acc[n] = sum_k x[k] W[n][k], y[n] = sat+-127(rne(f32(acc[n]) * m[n])).  acc may be NULL. */
 int32_t tl_gemv_i8_requant(tl_handle *h, const int8_t *x, const int8_t *w, const float *m,

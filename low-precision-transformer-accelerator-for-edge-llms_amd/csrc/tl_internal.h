@@ -250,6 +250,8 @@ size_t persist_lds_bytes(int32_t qkv, int32_t f, int32_t max_pos);
 bool persist_supported(int32_t d, int32_t f, int32_t qkv);
 hipError_t launch_persist_decode(hipStream_t s, const PersistArgs& args, int32_t grid, size_t lds);
 hipError_t launch_fill_u32(hipStream_t s, unsigned* p, int32_t n, unsigned v);
+hipError_t launch_requant_q16(hipStream_t s, const int32_t* acc, const uint32_t* scale, int32_t n, int32_t active,
+                              int32_t lanes_per_scale, int32_t nonnegative_only, int8_t* y);
 hipError_t persist_occupancy(int32_t d, int32_t f, size_t lds, int* blocks_per_cu);
 
 hipError_t launch_gemm32(hipStream_t s, int epi, const GemmArgs& a, int32_t splits, int32_t cfg);

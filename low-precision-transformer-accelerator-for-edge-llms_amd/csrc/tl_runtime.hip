@@ -1155,6 +1155,16 @@ int32_t tl_gemv_i8_requant(tl_handle* h, const int8_t* x, const int8_t* w, const
     return finish(h);
 }
 
+int32_t tl_requant_q16(tl_handle* h, const int32_t* acc, const uint32_t* scale_q16, int32_t n, int32_t active,
+                       int32_t lanes_per_scale, int32_t nonnegative_only, int8_t* y) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, acc && scale_q16 && y && n >= 0, "bad requantize arguments");
+    TL_REQ(h, lanes_per_scale >= 1, "lanes_per_scale must be at least 1");
+    TL_REQ(h, active >= 0 && active <= n, "active lane count outside 0..n");
+    TL_LAUNCH(h, launch_requant_q16(h->stream, acc, scale_q16, n, active, lanes_per_scale, nonnegative_only != 0, y));
+    return finish(h);
+}
+
 int32_t tl_gemm_i8(tl_handle* h, const int8_t* a, const int8_t* w, int32_t m, int32_t n, int32_t k, int32_t* c) {
     if (!h) return TL_ERR_BAD_DESCRIPTOR;
     TL_REQ(h, a && w && c && m > 0 && n > 0, "bad gemm arguments");

@@ -15,6 +15,9 @@
 - replay_gemm_case / replay_gemm_fixture: run an exported shared_gemm_engine
   case (EX:292-415) through the library's INT8 GEMM and compare the INT32
   accumulators.
+- replay_requant_case / replay_requant_fixture: run an exported
+  requantize_unit case (EX:528-653: 512 accumulator lanes, 16 Q16.16
+  multipliers) through tl_requant_q16 and compare the INT8 lanes.
 """
 from __future__ import annotations
 
@@ -405,17 +408,71 @@ def replay_gemm_fixture(rt: Runtime, fixture_base) -> dict:
     return {"acc": acc, "acc_lane": lanes, "match": bool(np.array_equal(lanes, acc_lane))}
 
 
+# ---------------------------------------------------------------------------
+# replay of exported requantize_unit cases (EX:528-653)
+# ---------------------------------------------------------------------------
+REQUANT_LANES_PER_SCALE = 32   # requantize_unit.sv:109: multiplier of lane i is scale[i / BANK_SLICE_INT8]
+
+
+def _requant_q16(rt: Runtime, acc: np.ndarray, scale: np.ndarray, elem_count: int) -> np.ndarray:
+    """tl_requant_q16 over the lanes; an element count of 0 means every lane
+    (requantize_unit.sv effective_elem_count)."""
+    from .tinyllama import dev, empty, host
+    acc = np.ascontiguousarray(acc, np.int32)
+    n = acc.size
+    active = n if elem_count == 0 else min(int(elem_count), n)
+    y = empty((n,), np.int8)
+    rt.call("tl_requant_q16", dev(acc), dev(np.ascontiguousarray(scale, np.uint32).view(np.int32)), n, active,
+            REQUANT_LANES_PER_SCALE, 0, y)
+    return host(y)
+
+
+def replay_requant_case(rt: Runtime, arrays: dict) -> dict:
+    """A case .npz of EX:560-568 (acc [512] int32 lanes, scale [16] uint32
+    Q16.16, elem_count [1], out_expected [512] int8): the library's output
+    lanes and whether they equal the expected ones."""
+    out = _requant_q16(rt, arrays["acc"], arrays["scale"], int(np.asarray(arrays["elem_count"]).ravel()[0]))
+    exp = np.asarray(arrays["out_expected"], np.int8)
+    return {"out": out, "match": bool(out.shape == exp.shape and np.array_equal(out, exp))}
+
+
+def replay_requant_fixture(rt: Runtime, fixture_base) -> dict:
+    """The RTL fixture files of EX:578-625 (<base>.meta.memh = active lanes;
+    .acc.memh [512] int32; .scale.memh [16] uint32 Q16.16;
+    .out_expected.memh [512] int8), replayed lane by lane."""
+    base = str(fixture_base)
+    active = int(read_scalar_memh_u32(base + ".meta.memh")[0])
+    acc = read_scalar_memh_i32(base + ".acc.memh")
+    scale = read_scalar_memh_u32(base + ".scale.memh")
+    exp = read_scalar_memh_i8(base + ".out_expected.memh")
+    out = _requant_q16(rt, acc, scale, active)
+    return {"out": out, "match": bool(out.shape == exp.shape and np.array_equal(out, exp))}
+
+
+def replay_fixture(rt: Runtime, fixture_base) -> dict:
+    """Replay one RTL fixture: a requantize_unit fixture has .acc.memh, a
+    shared_gemm_engine fixture .act_steps.memh."""
+    base = str(fixture_base)
+    if os.path.exists(base + ".acc.memh"):
+        return replay_requant_fixture(rt, base)
+    return replay_gemm_fixture(rt, base)
+
+
+REPLAYERS = {"shared_gemm_engine": replay_gemm_case, "requantize_unit": replay_requant_case}
+
+
 def replay_manifest(rt: Runtime, root) -> list[dict]:
-    """Replay every shared_gemm_engine case a manifest lists; other blocks
-    are reported as not replayed."""
+    """Replay every shared_gemm_engine and requantize_unit case a manifest
+    lists; other blocks are reported as not replayed."""
     root = Path(root)
     results = []
     for entry in read_manifest(root).get("cases", []):
-        if entry.get("block") != "shared_gemm_engine":
+        replay = REPLAYERS.get(entry.get("block"))
+        if replay is None:
             results.append({"case_id": entry.get("case_id"), "replayed": False})
             continue
         _, arrays = load_case(root, entry["case_id"])
-        r = replay_gemm_case(rt, arrays)
+        r = replay(rt, arrays)
         results.append({"case_id": entry["case_id"], "replayed": True, "match": r["match"]})
     return results
 
