@@ -58,6 +58,8 @@ enum GemvEpi : int {
     EPI_GLU = 3,          // y = silu(gate) * up, both dequantized
     EPI_ARGMAX = 4,       // argmax of dequantized logits into a 64-bit key
     EPI_RAW = 5,          // acc only
+    EPI_ACC = 6,          // acc[m][n] += the K slice's sum (integer atomic add; the row prologue that
+                          // follows folds the sums and clears them)
 };
 
 // activation prologue of the fused decode GEMV
@@ -101,7 +103,7 @@ struct GemmArgs {
     float* y;                 // [M][N]
     int32_t* acc;             // [M][N] raw (EPI_RAW) or [splits][M][N] partials
     int32_t m, n, k;
-    int32_t k_split;          // K elements per split (multiple of 64)
+    int32_t k_split;          // K elements per split (multiple of 64; gemm_rows32: multiple of 32, 0 = K)
     const int8_t* wp;         // packed copy of w (MFMA operand blocks, pack_weights_kernel) or null
     const int8_t* wp2;        // packed copy of w2
     unsigned long long* key;  // EPI_ARGMAX: [N / 32 tiles][M] best key of each tile and row
@@ -113,6 +115,26 @@ hipError_t launch_rmsnorm_quant(hipStream_t s, const float* x, const float* g, i
                                 double* scales);
 hipError_t launch_quantize_rows(hipStream_t s, const float* x, int32_t rows, int32_t n,
                                 int8_t* q, double* scales);
+
+// RMSNorm row prologue that first finishes a K-sliced small-M GEMM with a
+// residual epilogue: its integer sums acc (EPI_ACC, rows x n) are dequantized
+// with the GEMM's A-row scales and weight scales exactly as that GEMM's
+// DEQUANT_RES epilogue would (x += f32(acc) f32(sx sw), x written back),
+// cleared to zero for the next GEMM, and the row then goes through RMSNorm
+// and quantization into q / scales
+struct FoldArgs {
+    float* x;             // [rows][n] residual, overwritten with the sum
+    int32_t* acc;         // [rows][n]
+    const double* as;     // [rows] the GEMM's A-row scales (may alias scales: read first)
+    const float* ws;      // [n]
+    const float* g;       // [n] RMSNorm gains
+    int32_t rows, n;
+    float eps;
+    PwPlan plan;
+    int8_t* q;            // [rows][n]
+    double* scales;       // [rows]
+};
+hipError_t launch_rows_fold(hipStream_t s, const FoldArgs& f);
 hipError_t launch_quantize_tensor(hipStream_t s, const float* x, int64_t n, int8_t* q,
                                   double* scale, float* scratch_max);
 hipError_t launch_quantize_weight_rows(hipStream_t s, const float* w, int32_t rows, int32_t n,

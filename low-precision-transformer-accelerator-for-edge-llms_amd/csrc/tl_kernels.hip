@@ -129,6 +129,72 @@ static hipError_t launch_rows_prologue(hipStream_t s, const float* x, const floa
     return hipGetLastError();
 }
 
+// the RMSNorm row prologue above, preceded by the epilogue of a K-sliced
+// small-M GEMM whose workgroups added their integer sums into acc (EPI_ACC):
+// gemm_rows32_kernel's DEQUANT_RES arithmetic on the complete sums, so the
+// values are those of the unsliced GEMM
+template <int KCH>
+__global__ __launch_bounds__(kNT) void rows_fold_kernel(FoldArgs f) {
+    __shared__ __align__(16) int8_t xs8[KCH * 1024];
+    __shared__ __align__(16) float sq[KCH * 1024];
+    __shared__ __align__(16) float part[8 * 64];
+    __shared__ float red[16];
+    __shared__ double xscale;
+    const int tid = threadIdx.x, row = blockIdx.x, n = f.n;
+    const int kq = n / 4 - 1;
+    const int64_t ro = (int64_t)row * n;
+    // f.as[row] may be the buffer this workgroup's scale is written to: every
+    // thread reads it here, and uses it before the prologue's first barrier
+    const double sx = f.as[row];
+    v4i av[KCH];
+    float4 wv[KCH], rv[KCH], gv[KCH];
+#pragma unroll
+    for (int c = 0; c < KCH; c++) {
+        const int idx = min(c * kNT + tid, kq);
+        av[c] = ((const v4i*)(f.acc + ro))[idx];
+        wv[c] = ((const float4*)f.ws)[idx];
+        rv[c] = ((const float4*)(f.x + ro))[idx];
+        gv[c] = ((const float4*)f.g)[idx];
+    }
+    float4 xv[KCH];
+#pragma unroll
+    for (int c = 0; c < KCH; c++) {
+        xv[c].x = rv[c].x + (float)av[c][0] * deq_mult(sx, wv[c].x);
+        xv[c].y = rv[c].y + (float)av[c][1] * deq_mult(sx, wv[c].y);
+        xv[c].z = rv[c].z + (float)av[c][2] * deq_mult(sx, wv[c].z);
+        xv[c].w = rv[c].w + (float)av[c][3] * deq_mult(sx, wv[c].w);
+        const int idx = c * kNT + tid;
+        if (idx <= kq) {
+            // each element is read and cleared by the same thread
+            ((v4i*)(f.acc + ro))[idx] = (v4i){0, 0, 0, 0};
+            ((float4*)(f.x + ro))[idx] = xv[c];
+        }
+    }
+    prologue_rmsnorm<KCH>(xv, gv, n, f.eps, f.plan, sq, part, xs8, red, &xscale);
+    int8_t* qr = f.q + ro;
+    for (int o = tid * 16; o < n; o += kNT * 16) *(v4i*)(qr + o) = *(const v4i*)(xs8 + o);
+    if (tid == 0) f.scales[row] = xscale;
+}
+
+hipError_t launch_rows_fold(hipStream_t s, const FoldArgs& f) {
+    if (f.rows <= 0) return hipSuccess;
+    const uintptr_t bits = (uintptr_t)f.x | (uintptr_t)f.acc | (uintptr_t)f.ws | (uintptr_t)f.g | (uintptr_t)f.q;
+    if (f.n <= 0 || f.n % 64 || f.n > 6 * 1024 || bits % 16 || !f.x || !f.acc || !f.as || !f.ws || !f.g || !f.q ||
+        !f.scales || f.plan.n_leaves > 64)
+        return hipErrorInvalidValue;
+    const dim3 grid(f.rows), block(kNT);
+    switch ((f.n + 1023) / 1024) {
+        case 1: TL_KLAUNCH(rows_fold_kernel<1>, grid, block, 0, s, f); break;
+        case 2: TL_KLAUNCH(rows_fold_kernel<2>, grid, block, 0, s, f); break;
+        case 3: TL_KLAUNCH(rows_fold_kernel<3>, grid, block, 0, s, f); break;
+        case 4: TL_KLAUNCH(rows_fold_kernel<4>, grid, block, 0, s, f); break;
+        case 5: TL_KLAUNCH(rows_fold_kernel<5>, grid, block, 0, s, f); break;
+        case 6: TL_KLAUNCH(rows_fold_kernel<6>, grid, block, 0, s, f); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 static bool rows_fast_ok(const void* x, const void* g, const void* q, int32_t n) {
     const uintptr_t bits = (uintptr_t)x | (uintptr_t)g | (uintptr_t)q;
     return n % 64 == 0 && n <= 6 * 1024 && bits % 16 == 0;
@@ -1394,21 +1460,29 @@ constexpr int kRowsChunks = 12;   // most 32-byte K chunks per wavefront (K <= 1
 // operand order, one contiguous 1 KiB block per 32 rows x 32 K bytes), so
 // every weight load of a wavefront is one coalesced 1 KiB read; otherwise from
 // the row-major [N][K] matrix (32 rows x 32 bytes per load).
+//
+// K slices (EPI_ACC): blockIdx.y takes the 32-byte chunks
+// [y (k_split / 32), (y + 1) (k_split / 32)) of K, and the slice's integer
+// sums are added into acc with device-scope atomics (exact: the order of
+// integer additions does not change the sum)
 template <int EPI, int CH, bool PK>
 __global__ __launch_bounds__(1024) void gemm_rows32_kernel(GemmArgs a) {
     constexpr int NB = EPI == EPI_GLU ? 2 : 1;
     extern __shared__ __align__(16) int rows32_lds[];   // [16 waves][NB][16][64]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, col = lane & 31, hi = lane >> 5;
     const int n0 = blockIdx.x * 32;
-    const int kch = a.k >> 5;
-    const int8_t* arow = a.a + (int64_t)min(col, a.m - 1) * a.k + hi * 16;
+    const int cps = a.k_split >> 5, c0 = blockIdx.y * cps;
+    const int kch = min(cps, (a.k >> 5) - c0);   // chunks of this K slice (>= 1)
+    const int8_t* arow = a.a + (int64_t)min(col, a.m - 1) * a.k + (int64_t)c0 * 32 + hi * 16;
     const int8_t* wrow[NB];
     if (PK) {
-        wrow[0] = a.wp + (int64_t)blockIdx.x * kch * 1024 + lane * 16;
-        if (NB == 2) wrow[NB - 1] = a.wp2 + (int64_t)blockIdx.x * kch * 1024 + lane * 16;
+        const int64_t o = ((int64_t)blockIdx.x * (a.k >> 5) + c0) * 1024 + lane * 16;
+        wrow[0] = a.wp + o;
+        if (NB == 2) wrow[NB - 1] = a.wp2 + o;
     } else {
-        wrow[0] = a.w + (int64_t)min(n0 + col, a.n - 1) * a.k + hi * 16;
-        if (NB == 2) wrow[NB - 1] = a.w2 + (int64_t)min(n0 + col, a.n - 1) * a.k + hi * 16;
+        const int64_t o = (int64_t)min(n0 + col, a.n - 1) * a.k + (int64_t)c0 * 32 + hi * 16;
+        wrow[0] = a.w + o;
+        if (NB == 2) wrow[NB - 1] = a.w2 + o;
     }
     const int64_t wstep = PK ? 1024 : 32;   // bytes between consecutive K chunks
     const int per = (kch + kRowsWaves - 1) / kRowsWaves;   // consecutive chunks of this wavefront: 4 loads cover a 128-byte line
@@ -1467,6 +1541,10 @@ __global__ __launch_bounds__(1024) void gemm_rows32_kernel(GemmArgs a) {
         a.acc[idx] = sum[0];
         return;
     }
+    if (EPI == EPI_ACC) {
+        __hip_atomic_fetch_add(a.acc + idx, sum[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
     const double sx = a.as[m];
     const float v0 = (float)sum[0] * deq_mult(sx, a.ws[n]);
     if (EPI == EPI_GLU) {
@@ -1482,15 +1560,20 @@ __global__ __launch_bounds__(1024) void gemm_rows32_kernel(GemmArgs a) {
 static size_t rows32_lds_bytes(int nb) { return (size_t)kRowsWaves * nb * 16 * 64 * sizeof(int); }
 
 // M <= 32, K a multiple of 64 and at most 6144; with packed weights (a.wp,
-// and a.wp2 for the GLU) N must be a multiple of 32
-hipError_t launch_gemm_rows32(hipStream_t s, int epi, const GemmArgs& a) {
+// and a.wp2 for the GLU) N must be a multiple of 32.  a.k_split (a multiple
+// of 32, 0 = K) slices K over gridDim.y workgroups for EPI_ACC
+hipError_t launch_gemm_rows32(hipStream_t s, int epi, const GemmArgs& args) {
+    GemmArgs a = args;
     if (a.m < 1 || a.m > 32 || a.n <= 0 || a.k <= 0 || a.k % 64 || a.k > kRowsWaves * kRowsChunks * 32)
         return hipErrorInvalidValue;
+    if (a.k_split <= 0 || a.k_split >= a.k || epi != EPI_ACC) a.k_split = a.k;
+    if (a.k_split % 32) return hipErrorInvalidValue;
+    if (epi == EPI_ACC && !a.acc) return hipErrorInvalidValue;
     const bool pk = a.wp != nullptr;
     if (pk && (a.n % 32 || (epi == EPI_GLU && !a.wp2))) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((a.n + 31) / 32)), block(1024);
+    const dim3 grid((unsigned)((a.n + 31) / 32), (unsigned)((a.k + a.k_split - 1) / a.k_split)), block(1024);
     const size_t lds1 = rows32_lds_bytes(1), lds2 = rows32_lds_bytes(2);
-    const bool shortk = a.k <= kRowsWaves * 4 * 32;
+    const bool shortk = a.k_split <= kRowsWaves * 4 * 32;
 #define TL_R32P(E, C, L)                                                                    \
     do {                                                                                    \
         if (pk) TL_KLAUNCH((gemm_rows32_kernel<E, C, true>), grid, block, L, s, a);         \
@@ -1509,6 +1592,7 @@ hipError_t launch_gemm_rows32(hipStream_t s, int epi, const GemmArgs& a) {
             TL_R32P(EPI_GLU, 4, lds2);
             break;
         case EPI_RAW: TL_R32(EPI_RAW, lds1); break;
+        case EPI_ACC: TL_R32(EPI_ACC, lds1); break;
         case EPI_ARGMAX:
             if (!a.key || !shortk) return hipErrorInvalidValue;
             TL_R32P(EPI_ARGMAX, 4, lds1);

@@ -127,6 +127,9 @@ struct tl_handle {
     unsigned long long* op_key = nullptr;  // argmax slot of the standalone LM-head operator
     unsigned long long* lm_wg_keys = nullptr;  // [vocab / 4] batch-1 LM head: argmax key per workgroup
     int32_t* partials = nullptr;
+    int32_t* racc = nullptr;      // [32][D] integer sums of the K-sliced batched-decode down GEMM; zero
+                                  // between uses (the fold prologue clears what it read)
+    size_t racc_cap = 0;          // int32 elements
     unsigned* tile_ctr = nullptr;         // [kSkinnyTiles] arrival counters of the small-M GEMM, zero between launches
     size_t partial_cap = 0;       // int32 elements
 
@@ -152,6 +155,11 @@ struct tl_handle {
     bool use_persist = false;             // TL_PERSIST=1 turns on the single-kernel decode
     int batch_hpw = 1;                    // query heads per workgroup of multi-row decode attention (TL_BATCH_HPW)
     int gemm_small = 0;                   // M <= 32 GEMM: 0 one workgroup per tile, 1 split K, 2 16x16x64 tiles (TL_GEMM_SMALL)
+    bool batch_kslice = true;             // batched decode: K-sliced down GEMM folded by the next RMSNorm
+                                          // row prologue (TL_BATCH_KSLICE=0 turns it off)
+    const float* racc_res_ws = nullptr;   // racc holds a down projection's sums (these weight scales) that
+                                          // the next RMSNorm prologue adds to h->x
+    bool racc_clean = true;               // false from an EPI_ACC launch until its fold has run
     bool rows_one_seq = false;            // the uploaded rows are one sequence at rows_pos0 + r
     int32_t rows_seq = 0, rows_pos0 = 0;
     bool persist_ok = false;              // geometry and occupancy allow it
@@ -534,16 +542,68 @@ int32_t layer_row1(tl_handle* h, int32_t layer, int32_t max_t) {
 // decode: every row is a different sequence (its own K/V row is appended by
 // the attention kernel); otherwise the rows are consecutive prompt positions
 // of one sequence (all appended before attention reads them).
+// K slice of a batched-decode GEMM: halve the slice while the 32-column
+// tiles times the slices stay within the 256 CUs (one round of 16-wavefront
+// workgroups) and a slice keeps at least 32 chunks of 32 bytes (two per
+// wavefront).  At TinyLlama's shapes only the down projection (64 tiles,
+// K = 5632) is sliced, in four: O and gate/up measured no faster sliced (the
+// atomic adds and the fold cost what the spread gained; gate/up's 176 tiles
+// leave no room for a second slice in one round)
+static int32_t kslice_len(int32_t n, int32_t k) {
+    const int tiles = n / 32, kch = k / 32;
+    int s = 1;
+    while (tiles * 2 * s <= 256 && kch / (2 * s) >= 32) s *= 2;
+    return ((kch + s - 1) / s) * 32;
+}
+
+// batched decode can run its down GEMM K-sliced
+static bool kslice_ok(tl_handle* h, const LayerDev& L, int32_t rows) {
+    const int D = h->D, F = h->F;
+    return h->batch_kslice && h->gemm_small == 0 && rows > 1 && rows <= 32 && L.wd_p && D % 64 == 0 &&
+           F % 64 == 0 && D <= 6144 && F <= 6144 && h->plan.n_leaves <= 64 && (size_t)rows * D <= h->racc_cap;
+}
+
+// integer-sum GEMM into h->racc (EPI_ACC), K-sliced
+static int32_t linear_acc(tl_handle* h, int32_t rows, const int8_t* wp, int32_t n, int32_t k, int kclass) {
+    GemmArgs a{};
+    a.a = h->a8; a.as = h->as; a.wp = wp; a.acc = h->racc;
+    a.m = rows; a.n = n; a.k = k; a.k_split = kslice_len(n, k);
+    const double bytes = (double)rows * k + (double)n * k + (double)rows * n * 4.0;
+    h->racc_clean = false;
+    Prof p(h, kclass, bytes);
+    TL_LAUNCH(h, launch_gemm_rows32(h->stream, EPI_ACC, a));
+    return TL_OK;
+}
+
+// RMSNorm + quantization of the rows of h->x into h->a8 / h->as, first adding
+// a pending down projection's sums from h->racc (launch_rows_fold)
+static int32_t rows_rmsnorm(tl_handle* h, int32_t rows, const float* g) {
+    if (h->racc_res_ws) {
+        FoldArgs f{};
+        f.x = h->x; f.acc = h->racc; f.as = h->as; f.ws = h->racc_res_ws; f.g = g;
+        f.rows = rows; f.n = h->D; f.eps = h->cfg.rms_eps; f.plan = h->plan; f.q = h->a8; f.scales = h->as;
+        h->racc_res_ws = nullptr;
+        {
+            Prof p(h, TL_K_NORM, (double)rows * h->D * 13.0);
+            TL_LAUNCH(h, launch_rows_fold(h->stream, f));
+        }
+        h->racc_clean = true;
+        return TL_OK;
+    }
+    Prof p(h, TL_K_NORM, (double)rows * h->D * 9.0);
+    TL_LAUNCH(h, launch_rmsnorm_quant(h->stream, h->x, g, rows, h->D, h->cfg.rms_eps, h->plan, nullptr, h->a8, h->as));
+    return TL_OK;
+}
+
 int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, bool decode) {
     if (rows == 1) return layer_row1(h, layer, max_t);
     const tl_config& c = h->cfg;
     const LayerDev& L = h->layers[layer];
     const int D = h->D, F = h->F, KVD = h->KVD, QKV = h->QKV;
+    const bool ks = decode && kslice_ok(h, L, rows);
+    if (h->racc_res_ws && !ks) return fail(h, TL_ERR_INTERNAL, "pending K-slice sums outside batched decode");
     int32_t r;
-    {
-        Prof p(h, TL_K_NORM, (double)rows * D * 9.0);
-        TL_LAUNCH(h, launch_rmsnorm_quant(h->stream, h->x, L.g_in, rows, D, c.rms_eps, h->plan, nullptr, h->a8, h->as));
-    }
+    if ((r = rows_rmsnorm(h, rows, L.g_in))) return r;
     if ((r = linear(h, EPI_DEQUANT, rows, h->a8, h->as, L.wqkv, L.sqkv, nullptr, nullptr, QKV, D, nullptr, h->qkv, TL_K_QKV,
                     L.wqkv_p)))
         return r;
@@ -580,6 +640,13 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
         Prof p(h, TL_K_NORM, (double)rows * F * 5.0);
         TL_LAUNCH(h, launch_quantize_rows(h->stream, h->hid, rows, F, h->a8, h->as));
     }
+    if (ks) {
+        // the down GEMM (K = F) K-sliced over the chip: its integer sums wait
+        // in h->racc for the next layer's input RMSNorm, or the final one
+        if ((r = linear_acc(h, rows, L.wd_p, D, F, TL_K_DOWN))) return r;
+        h->racc_res_ws = L.sd;
+        return TL_OK;
+    }
     if ((r = linear(h, EPI_DEQUANT_RES, rows, h->a8, h->as, L.wd, L.sd, nullptr, nullptr, D, F, h->x, h->x, TL_K_DOWN,
                     L.wd_p)))
         return r;
@@ -605,7 +672,11 @@ int32_t lm_head_rows(tl_handle* h, const float* xrow, int32_t rows, int32_t seq,
         Prof p(h, TL_K_LMHEAD, (double)V * D + V * 4.0 + D * 8.0);
         TL_LAUNCH(h, launch_gemv_fused(h->stream, PRO_RMSNORM, EPI_ARGMAX, g));
     } else {
-        {
+        if (h->racc_res_ws) {
+            if (xrow != h->x) return fail(h, TL_ERR_INTERNAL, "pending K-slice sums for other rows");
+            int32_t r = rows_rmsnorm(h, rows, h->g_final);
+            if (r) return r;
+        } else {
             Prof p(h, TL_K_NORM, (double)rows * D * 9.0);
             TL_LAUNCH(h, launch_rmsnorm_quant(h->stream, xrow, h->g_final, rows, D, c.rms_eps, h->plan, nullptr, h->a8, h->as));
         }
@@ -771,6 +842,12 @@ int32_t decode_graph_launch(tl_handle* h, int32_t seq) {
 // captured once per batch size and replayed.
 int32_t batch_step(tl_handle* h, int32_t n_seqs, int32_t max_t) {
     const tl_config& c = h->cfg;
+    if (!h->racc_clean || h->racc_res_ws) {
+        // an earlier step failed between a K-sliced GEMM and its fold
+        TL_LAUNCH(h, launch_fill_u32(h->stream, (unsigned*)h->racc, (int32_t)h->racc_cap, 0u));
+        h->racc_clean = true;
+        h->racc_res_ws = nullptr;
+    }
     TL_LAUNCH(h, launch_embed_step(h->stream, h->token_cur, h->row_seq, n_seqs, h->cursor, h->row_pos, h->D, c.vocab,
                                    h->emb, h->emb_s, h->x));
     int32_t r;
@@ -880,6 +957,7 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
         (e = dalloc(h, &h->token_cur, (size_t)max_seqs)) || (e = dalloc(h, &h->cursor, (size_t)max_seqs)) ||
         (e = dalloc(h, &h->n_gen, (size_t)max_seqs)) || (e = dalloc(h, &h->eos_id, (size_t)max_seqs)) ||
         (e = dalloc(h, &h->stopped, (size_t)max_seqs)) ||
+        (e = dalloc(h, &h->racc, h->racc_cap = (size_t)std::min(32, max_seqs) * D)) ||
         (e = dalloc(h, &h->tokens_out, (size_t)max_seqs * c.max_pos)) ||
         (e = dalloc(h, &h->logit_out, (size_t)max_seqs * c.max_pos)) ||
         (e = dalloc(h, &h->rope_cos, (size_t)c.max_pos * kHeadDim)) ||
@@ -919,7 +997,8 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
         (e = hipMemsetAsync(h->n_gen, 0, sizeof(int32_t) * max_seqs, h->stream)) ||
         (e = hipMemsetAsync(h->eos_id, 0xFF, sizeof(int32_t) * max_seqs, h->stream)) ||
         (e = hipMemsetAsync(h->stopped, 0, sizeof(int32_t) * max_seqs, h->stream)) ||
-        (e = hipMemsetAsync(h->tile_ctr, 0, sizeof(unsigned) * kSkinnyTiles, h->stream)))
+        (e = hipMemsetAsync(h->tile_ctr, 0, sizeof(unsigned) * kSkinnyTiles, h->stream)) ||
+        (e = hipMemsetAsync(h->racc, 0, sizeof(int32_t) * h->racc_cap, h->stream)))
         return bad(e);
     std::vector<float> cs, sn;
     default_rope(c.max_pos, c.rope_theta, cs, sn);
@@ -941,6 +1020,7 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
     if (const char* env = std::getenv("TL_BATCH_HPW")) h->batch_hpw = std::atoi(env) == 8 ? 8 : 1;
     if (const char* env = std::getenv("TL_GEMM_SMALL")) h->gemm_small = std::atoi(env);
     if (const char* env = std::getenv("TL_GEMM_CFG")) h->gemm_cfg = std::atoi(env);
+    if (const char* env = std::getenv("TL_BATCH_KSLICE")) h->batch_kslice = env[0] != '0';
     if ((e = hipStreamSynchronize(h->stream))) return bad(e);
     *out = h;
     return TL_OK;
