@@ -649,7 +649,21 @@ __global__ __launch_bounds__(kGW * 64) void attention_group_kernel(AttnDecodeArg
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int G = p.n_heads / p.n_kv;
-    const int h0 = blockIdx.x * HPW, g = h0 / G, row = blockIdx.y;
+    // workgroups are dispatched to the 8 XCDs round-robin by linear id: the
+    // G / HPW workgroups of one (row, KV head), which read the same K and V
+    // planes, get linear ids 8 apart so that they run on one XCD and share its
+    // L2 (identity order when the grid is not a multiple of 8)
+    int h0 = blockIdx.x * HPW, row = blockIdx.y;
+    {
+        const int total = gridDim.x * gridDim.y, lin = blockIdx.x + gridDim.x * blockIdx.y;
+        if (total % 8 == 0) {
+            const int q = (lin % 8) * (total / 8) + lin / 8, per = G / HPW;
+            const int unit = q / per;
+            row = unit / p.n_kv;
+            h0 = (unit % p.n_kv) * G + (q % per) * HPW;
+        }
+    }
+    const int g = h0 / G;
     const int D = p.n_heads * kHeadDim, KVD = p.n_kv * kHeadDim, W = D + 2 * KVD;
     const int pos = p.rm.pos[row], seq = p.rm.seq[row];
     if (pos < 0 || pos >= p.kv.max_pos) return;   // a row outside the cache (uniform per workgroup)
