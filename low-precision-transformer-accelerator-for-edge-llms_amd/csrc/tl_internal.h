@@ -142,7 +142,7 @@ hipError_t launch_quantize_weight_rows(hipStream_t s, const float* w, int32_t ro
 hipError_t launch_gemv(hipStream_t s, int epi, const GemvArgs& a);
 constexpr int kSkinnyTiles = 4096;     // output tiles of 32 columns the split small-M GEMM counts
 constexpr int kSkinnyMaxSlices = 8;   // K slices of the small-M GEMM (LDS holds the other 7 partial tiles)
-hipError_t launch_gemm_rows32(hipStream_t s, int epi, const GemmArgs& a);
+hipError_t launch_gemm_rows32(hipStream_t s, int epi, const GemmArgs& a, int32_t waves = 16);
 hipError_t launch_pack_weights(hipStream_t s, const int8_t* w, int32_t n, int32_t k, int8_t* wp);
 
 hipError_t launch_gemm_skinny(hipStream_t s, int epi, const GemmArgs& a, int32_t slices, int32_t* part,

@@ -1465,10 +1465,10 @@ constexpr int kRowsChunks = 12;   // most 32-byte K chunks per wavefront (K <= 1
 // [y (k_split / 32), (y + 1) (k_split / 32)) of K, and the slice's integer
 // sums are added into acc with device-scope atomics (exact: the order of
 // integer additions does not change the sum)
-template <int EPI, int CH, bool PK>
-__global__ __launch_bounds__(1024) void gemm_rows32_kernel(GemmArgs a) {
+template <int EPI, int CH, bool PK, int W = kRowsWaves>
+__global__ __launch_bounds__(W * 64) void gemm_rows32_kernel(GemmArgs a) {
     constexpr int NB = EPI == EPI_GLU ? 2 : 1;
-    extern __shared__ __align__(16) int rows32_lds[];   // [16 waves][NB][16][64]
+    extern __shared__ __align__(16) int rows32_lds[];   // [W waves][NB][16][64]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, col = lane & 31, hi = lane >> 5;
     const int n0 = blockIdx.x * 32;
     const int cps = a.k_split >> 5, c0 = blockIdx.y * cps;
@@ -1485,7 +1485,7 @@ __global__ __launch_bounds__(1024) void gemm_rows32_kernel(GemmArgs a) {
         if (NB == 2) wrow[NB - 1] = a.w2 + o;
     }
     const int64_t wstep = PK ? 1024 : 32;   // bytes between consecutive K chunks
-    const int per = (kch + kRowsWaves - 1) / kRowsWaves;   // consecutive chunks of this wavefront: 4 loads cover a 128-byte line
+    const int per = (kch + W - 1) / W;   // consecutive chunks of this wavefront: 4 loads cover a 128-byte line
     v4i af[CH], bf[NB][CH];
 #pragma unroll
     for (int j = 0; j < CH; j++) {
@@ -1507,71 +1507,97 @@ __global__ __launch_bounds__(1024) void gemm_rows32_kernel(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < 16; i++) rows32_lds[((wave * NB + b) * 16 + i) * 64 + lane] = acc[b][i];
     __syncthreads();
-    // thread t finishes element (register i, lane l) of the 32 x 32 tile
-    const int l = tid & 63, i = tid >> 6;
-    const int m = 8 * (i >> 2) + 4 * (l >> 5) + (i & 3), n = n0 + (l & 31);
-    if (EPI == EPI_ARGMAX) {
-        // dequantized logit -> 64-bit key; the 32 columns of row m are the 32
-        // lanes of this half-wavefront, whose best key is this tile's key of
-        // row m (argmax_tiles_kernel folds the tiles)
-        unsigned long long k = 0;
-        if (m < a.m && n < a.n) {
+    // the tile's 16 x 64 (register i, lane l) elements: wavefront w finishes
+    // registers w, w + W, ... of every lane
+    const int l = lane;
+    for (int i = wave; i < 16; i += W) {
+        const int m = 8 * (i >> 2) + 4 * (l >> 5) + (i & 3), n = n0 + (l & 31);
+        if (EPI == EPI_ARGMAX) {
+            // dequantized logit -> 64-bit key; the 32 columns of row m are the
+            // 32 lanes of this half-wavefront, whose best key is this tile's key
+            // of row m (argmax_tiles_kernel folds the tiles)
+            unsigned long long k = 0;
+            if (m < a.m && n < a.n) {
+                int v = 0;
+#pragma unroll
+                for (int w = 0; w < W; w++) v += rows32_lds[(w * 16 + i) * 64 + l];
+                const float lg = (float)v * deq_mult(a.as[m], a.ws[n]);
+                if (a.y) a.y[(int64_t)m * a.n + n] = lg;
+                k = argmax_key(lg, n);
+            }
+            k = half_max_u64(k);
+            if ((l & 31) == 0 && m < a.m) a.key[(int64_t)blockIdx.x * a.m + m] = k;
+            continue;
+        }
+        if (m >= a.m || n >= a.n) continue;
+        int sum[NB];
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
             int v = 0;
 #pragma unroll
-            for (int w = 0; w < kRowsWaves; w++) v += rows32_lds[(w * 16 + i) * 64 + l];
-            const float lg = (float)v * deq_mult(a.as[m], a.ws[n]);
-            if (a.y) a.y[(int64_t)m * a.n + n] = lg;
-            k = argmax_key(lg, n);
+            for (int w = 0; w < W; w++) v += rows32_lds[((w * NB + b) * 16 + i) * 64 + l];
+            sum[b] = v;
         }
-        k = half_max_u64(k);
-        if ((l & 31) == 0 && m < a.m) a.key[(int64_t)blockIdx.x * a.m + m] = k;
-        return;
-    }
-    if (m >= a.m || n >= a.n) return;
-    int sum[NB];
-#pragma unroll
-    for (int b = 0; b < NB; b++) {
-        int v = 0;
-#pragma unroll
-        for (int w = 0; w < kRowsWaves; w++) v += rows32_lds[((w * NB + b) * 16 + i) * 64 + l];
-        sum[b] = v;
-    }
-    const int64_t idx = (int64_t)m * a.n + n;
-    if (EPI == EPI_RAW) {
-        a.acc[idx] = sum[0];
-        return;
-    }
-    if (EPI == EPI_ACC) {
-        __hip_atomic_fetch_add(a.acc + idx, sum[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return;
-    }
-    const double sx = a.as[m];
-    const float v0 = (float)sum[0] * deq_mult(sx, a.ws[n]);
-    if (EPI == EPI_GLU) {
-        const float up = (float)sum[NB - 1] * deq_mult(sx, a.ws2[n]);
-        a.y[idx] = tl_silu(v0) * up;
-    } else if (EPI == EPI_DEQUANT_RES) {
-        a.y[idx] = a.residual[idx] + v0;
-    } else {
-        a.y[idx] = v0;
+        const int64_t idx = (int64_t)m * a.n + n;
+        if (EPI == EPI_RAW) {
+            a.acc[idx] = sum[0];
+        } else if (EPI == EPI_ACC) {
+            __hip_atomic_fetch_add(a.acc + idx, sum[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            const double sx = a.as[m];
+            const float v0 = (float)sum[0] * deq_mult(sx, a.ws[n]);
+            if (EPI == EPI_GLU) {
+                const float up = (float)sum[NB - 1] * deq_mult(sx, a.ws2[n]);
+                a.y[idx] = tl_silu(v0) * up;
+            } else if (EPI == EPI_DEQUANT_RES) {
+                a.y[idx] = a.residual[idx] + v0;
+            } else {
+                a.y[idx] = v0;
+            }
+        }
     }
 }
 
-static size_t rows32_lds_bytes(int nb) { return (size_t)kRowsWaves * nb * 16 * 64 * sizeof(int); }
+static size_t rows32_lds_bytes(int nb, int w = kRowsWaves) { return (size_t)w * nb * 16 * 64 * sizeof(int); }
+
+// the 4- and 8-wavefront variants on packed weights: 64 / W chunks of 32
+// bytes per wavefront, so a K slice of at most 2048 bytes
+template <int W>
+static hipError_t launch_rows32_w(hipStream_t s, int epi, const GemmArgs& a, dim3 grid) {
+    constexpr int CH = 64 / W;
+    const dim3 block(W * 64);
+    const size_t lds1 = rows32_lds_bytes(1, W), lds2 = rows32_lds_bytes(2, W);
+    switch (epi) {
+        case EPI_DEQUANT: TL_KLAUNCH((gemm_rows32_kernel<EPI_DEQUANT, CH, true, W>), grid, block, lds1, s, a); break;
+        case EPI_DEQUANT_RES: TL_KLAUNCH((gemm_rows32_kernel<EPI_DEQUANT_RES, CH, true, W>), grid, block, lds1, s, a); break;
+        case EPI_GLU: TL_KLAUNCH((gemm_rows32_kernel<EPI_GLU, CH, true, W>), grid, block, lds2, s, a); break;
+        case EPI_RAW: TL_KLAUNCH((gemm_rows32_kernel<EPI_RAW, CH, true, W>), grid, block, lds1, s, a); break;
+        case EPI_ACC: TL_KLAUNCH((gemm_rows32_kernel<EPI_ACC, CH, true, W>), grid, block, lds1, s, a); break;
+        case EPI_ARGMAX: TL_KLAUNCH((gemm_rows32_kernel<EPI_ARGMAX, CH, true, W>), grid, block, lds1, s, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
 
 // M <= 32, K a multiple of 64 and at most 6144; with packed weights (a.wp,
 // and a.wp2 for the GLU) N must be a multiple of 32.  a.k_split (a multiple
-// of 32, 0 = K) slices K over gridDim.y workgroups for EPI_ACC
-hipError_t launch_gemm_rows32(hipStream_t s, int epi, const GemmArgs& args) {
+// of 32, 0 = K) slices K over gridDim.y workgroups for EPI_ACC.  waves = 4 or
+// 8 runs workgroups of that many wavefronts (packed weights, K slice at most
+// 2048 bytes), else 16.
+hipError_t launch_gemm_rows32(hipStream_t s, int epi, const GemmArgs& args, int32_t waves) {
     GemmArgs a = args;
     if (a.m < 1 || a.m > 32 || a.n <= 0 || a.k <= 0 || a.k % 64 || a.k > kRowsWaves * kRowsChunks * 32)
         return hipErrorInvalidValue;
     if (a.k_split <= 0 || a.k_split >= a.k || epi != EPI_ACC) a.k_split = a.k;
     if (a.k_split % 32) return hipErrorInvalidValue;
     if (epi == EPI_ACC && !a.acc) return hipErrorInvalidValue;
+    if (epi == EPI_ARGMAX && !a.key) return hipErrorInvalidValue;
     const bool pk = a.wp != nullptr;
     if (pk && (a.n % 32 || (epi == EPI_GLU && !a.wp2))) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((a.n + 31) / 32), (unsigned)((a.k + a.k_split - 1) / a.k_split)), block(1024);
+    const dim3 grid((unsigned)((a.n + 31) / 32), (unsigned)((a.k + a.k_split - 1) / a.k_split));
+    if (pk && (waves == 4 || waves == 8) && a.k_split <= 64 * 32)
+        return waves == 4 ? launch_rows32_w<4>(s, epi, a, grid) : launch_rows32_w<8>(s, epi, a, grid);
+    const dim3 block(1024);
     const size_t lds1 = rows32_lds_bytes(1), lds2 = rows32_lds_bytes(2);
     const bool shortk = a.k_split <= kRowsWaves * 4 * 32;
 #define TL_R32P(E, C, L)                                                                    \
@@ -1594,7 +1620,7 @@ hipError_t launch_gemm_rows32(hipStream_t s, int epi, const GemmArgs& args) {
         case EPI_RAW: TL_R32(EPI_RAW, lds1); break;
         case EPI_ACC: TL_R32(EPI_ACC, lds1); break;
         case EPI_ARGMAX:
-            if (!a.key || !shortk) return hipErrorInvalidValue;
+            if (!shortk) return hipErrorInvalidValue;
             TL_R32P(EPI_ARGMAX, 4, lds1);
             break;
         default: return hipErrorInvalidValue;

@@ -155,6 +155,8 @@ struct tl_handle {
     bool use_persist = false;             // TL_PERSIST=1 turns on the single-kernel decode
     int batch_hpw = 1;                    // query heads per workgroup of multi-row decode attention (TL_BATCH_HPW)
     int gemm_small = 0;                   // M <= 32 GEMM: 0 one workgroup per tile, 1 split K, 2 16x16x64 tiles (TL_GEMM_SMALL)
+    int rows32_waves = -1;                // wavefronts per workgroup of the packed M <= 32 GEMMs (TL_ROWS32_WAVES;
+                                          // -1: 8 for gate/up, 16 for the others, as measured fastest)
     bool batch_kslice = true;             // batched decode: K-sliced down GEMM folded by the next RMSNorm
                                           // row prologue (TL_BATCH_KSLICE=0 turns it off)
     const float* racc_res_ws = nullptr;   // racc holds a down projection's sums (these weight scales) that
@@ -360,6 +362,14 @@ struct FixedScratch {
     int32_t ctr_cap;      // counters
 };
 
+// wavefronts per workgroup of the packed M <= 32 GEMM: with 8 (8 chunks of
+// 32 bytes each) the gate/up GEMM took 225 against 273 us per batched step at
+// 32 x 2048, while Q|K|V, O and down were 4-12 % slower than with 16
+static int rows32_waves(const tl_handle* h, int epi) {
+    if (h->rows32_waves > 0) return h->rows32_waves;
+    return epi == EPI_GLU ? 8 : 16;
+}
+
 int32_t run_gemm(tl_handle* h, int epi, GemmArgs a, int kclass, const FixedScratch* fx = nullptr) {
     const int nb = epi == EPI_GLU ? 2 : 1;
     const bool prof_ok = fx == nullptr;   // profiling events are allocations
@@ -381,7 +391,7 @@ int32_t run_gemm(tl_handle* h, int epi, GemmArgs a, int kclass, const FixedScrat
         // (measured faster than splitting K over workgroups: the cross-XCD
         // reduction of the partial tiles costs more than the added bandwidth)
         Prof p(h, kclass, bytes, prof_ok);
-        TL_LAUNCH(h, launch_gemm_rows32(h->stream, epi, a));
+        TL_LAUNCH(h, launch_gemm_rows32(h->stream, epi, a, rows32_waves(h, epi)));
         return TL_OK;
     }
     a.wp = a.wp2 = nullptr;
@@ -571,7 +581,7 @@ static int32_t linear_acc(tl_handle* h, int32_t rows, const int8_t* wp, int32_t 
     const double bytes = (double)rows * k + (double)n * k + (double)rows * n * 4.0;
     h->racc_clean = false;
     Prof p(h, kclass, bytes);
-    TL_LAUNCH(h, launch_gemm_rows32(h->stream, EPI_ACC, a));
+    TL_LAUNCH(h, launch_gemm_rows32(h->stream, EPI_ACC, a, rows32_waves(h, EPI_ACC)));
     return TL_OK;
 }
 
@@ -692,7 +702,7 @@ int32_t lm_head_rows(tl_handle* h, const float* xrow, int32_t rows, int32_t seq,
             a.key = (unsigned long long*)h->partials;
             a.y = nullptr;
             Prof p(h, TL_K_LMHEAD, (double)V * D + V * 4.0 + (double)rows * D);
-            TL_LAUNCH(h, launch_gemm_rows32(h->stream, EPI_ARGMAX, a));
+            TL_LAUNCH(h, launch_gemm_rows32(h->stream, EPI_ARGMAX, a, rows32_waves(h, EPI_ARGMAX)));
             TL_LAUNCH(h, launch_argmax_tiles(h->stream, a.key, tiles, rows, keys));
         } else {
             // MFMA GEMM writes logits, a row argmax folds them into keys
@@ -1021,6 +1031,7 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
     if (const char* env = std::getenv("TL_GEMM_SMALL")) h->gemm_small = std::atoi(env);
     if (const char* env = std::getenv("TL_GEMM_CFG")) h->gemm_cfg = std::atoi(env);
     if (const char* env = std::getenv("TL_BATCH_KSLICE")) h->batch_kslice = env[0] != '0';
+    if (const char* env = std::getenv("TL_ROWS32_WAVES")) h->rows32_waves = std::atoi(env);
     if ((e = hipStreamSynchronize(h->stream))) return bad(e);
     *out = h;
     return TL_OK;

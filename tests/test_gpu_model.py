@@ -189,6 +189,35 @@ def test_decode_batch_matches_oracle(small_model):
     eng.close()
 
 
+@pytest.mark.parametrize("waves", ["4", "16"])
+def test_decode_batch_rows32_waves(waves, monkeypatch):
+    """The packed M <= 32 GEMMs with 4 or 16 wavefronts per workgroup
+    (TL_ROWS32_WAVES; by default 8 for gate/up and 16 for the others) give the
+    oracle's batched greedy ids at TinyLlama's head geometry."""
+    monkeypatch.setenv("TL_ROWS32_WAVES", waves)
+    cfg = dict(oracle.TINYLLAMA_CFG, n_layers=2, vocab=512)
+    m = oracle.synthetic_model(cfg, seed=8)
+    B, steps = 5, 3
+    eng = engine_for(m, max_seqs=B)
+    start = np.array([3, 70, 129, 600, 1500], np.int32)
+    toks = np.array([4, 77, 300, 511, 0], np.int32)
+    caches = []
+    for b in range(B):
+        kc, vc = m.new_cache()
+        fill_cache_random(eng, m, b, int(start[b]), seed=500 + b, kc=kc, vc=vc)
+        caches.append((kc, vc))
+    got = eng.decode_batch(toks, start, steps)
+    orc = oracle.Oracle(m)
+    x = np.stack([orc.embed(int(t)) for t in toks]).astype(F32)
+    for s in range(steps):
+        for layer in range(cfg["n_layers"]):
+            orc.decode_rows(layer, start + s, x, caches)
+        want, _ = orc.lm_head_rows(x)
+        assert_bits_equal(got[:, s], want, f"ids of step {s}")
+        x = np.stack([orc.embed(int(t)) for t in want]).astype(F32)
+    eng.close()
+
+
 def test_lm_head_argmax_operator(small_model):
     m = small_model
     eng = engine_for(m)
