@@ -350,10 +350,19 @@ def decode_section(eng, host, args):
     }
     per_step = {k: (CFG["n_layers"] if k != "lm_head" else 1) for k in kbytes}
     bytes_step = sum(kbytes[k] * per_step[k] for k in kbytes)
+    # all decode GEMVs of a step together: their algorithmic bytes over their
+    # summed durations (dispatch, and busy inside the replayed graph)
+    gemv = {"classes": sorted(kbytes), "bytes_per_step": bytes_step}
+    for src, dst in (("dispatch_us", "dispatch"), ("busy_us", "busy")):
+        if all(kernels.get(k, {}).get(src) for k in kbytes):
+            us = sum(kernels[k][src] * per_step[k] for k in kbytes)
+            gbs = sum(kbytes[k] * per_step[k] for k in kbytes) / (us * 1e-6) / 1e9
+            gemv.update({f"{dst}_us_per_step": round(us, 2), f"{dst}_gbs": round(gbs, 1),
+                         f"{dst}_frac": round(gbs / HBM_PEAK_GBS, 4)})
     return dict(prompt=prompt, first=first, toks=toks, dt=dt, kernels=kernels, accounting=accounting,
                 eos_watch={"tok_s": round(args.steps / eos_dt, 2), "vs_no_eos": round(dt / eos_dt, 4),
                            "eos_id": int(never)},
-                bytes_step=bytes_step)
+                bytes_step=bytes_step, gemv=gemv)
 
 
 def main():
@@ -478,6 +487,7 @@ def main():
                      "bytes_per_launch": glu.get("bytes"), "avg_us": glu.get("dispatch_us"),
                      "busy_us": glu.get("busy_us"), "busy_frac": glu.get("busy_frac")},
         "decode_step_hbm_frac": round(d["bytes_step"] / (d["dt"] / args.steps) / 1e9 / HBM_PEAK_GBS, 4),
+        "decode_gemv": d["gemv"],
         "step_accounting": d["accounting"],
         "kernels": kernels,
         "eos_watch": d["eos_watch"],
