@@ -1140,12 +1140,26 @@ __global__ __launch_bounds__(64) void finalize_tokens_kernel(unsigned long long*
     const bool single = n_wg > 0 || nx.x != nullptr;
     const int r = single ? 0 : blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= rows) return;
-    // every lane reads the flag before lane 0 may set it
-    const bool halted = single && nx.stopped != nullptr && *nx.stopped != 0;
+    // every independent load first, so the step pays one memory round trip
+    // before the embedding gather: the stop flag, this row's key and state,
+    // and the first kFinUnroll x 64 workgroup keys.  Every lane reads the flag
+    // and the key before lane 0 may write them.
+    constexpr int kFinUnroll = 16;
+    const int32_t stop_v = (single && nx.stopped != nullptr) ? *nx.stopped : 0;
+    const unsigned long long key_r = keys[r];
+    const int32_t tok_r = token_cur[r], cur_r = cursor[r], gen_r = n_gen[r];
+    const int32_t eos = (single && nx.eos) ? *nx.eos : -1;
+    unsigned long long wk[kFinUnroll];
+#pragma unroll
+    for (int j = 0; j < kFinUnroll; j++) {
+        const int i = threadIdx.x + 64 * j;
+        wk[j] = i < n_wg ? wg_keys[i] : 0ull;
+    }
+    const bool halted = stop_v != 0;
     int32_t tok, cur;
     if (halted) {
-        tok = token_cur[r];
-        cur = cursor[r];
+        tok = tok_r;
+        cur = cur_r;
         if (threadIdx.x == 0) {
             keys[r] = 0ull;
             if (nx.x) *nx.row_pos = cur;
@@ -1153,15 +1167,17 @@ __global__ __launch_bounds__(64) void finalize_tokens_kernel(unsigned long long*
     } else {
         unsigned long long fold = 0;
         if (n_wg > 0) {
-            for (int i = threadIdx.x; i < n_wg; i += 64) fold = max_u64(fold, wg_keys[i]);
+#pragma unroll
+            for (int j = 0; j < kFinUnroll; j++) fold = max_u64(fold, wk[j]);
+            for (int i = threadIdx.x + 64 * kFinUnroll; i < n_wg; i += 64) fold = max_u64(fold, wg_keys[i]);
             fold = wave_max_u64(fold);
         }
-        const unsigned long long k = max_u64(keys[r], fold);   // every lane reads before lane 0 clears
+        const unsigned long long k = max_u64(key_r, fold);
         tok = key_index(k);
-        cur = cursor[r] + advance;
+        cur = cur_r + advance;
         if (!single || threadIdx.x == 0) {
             token_cur[r] = tok;
-            const int32_t i = n_gen[r];
+            const int32_t i = gen_r;
             if (i >= 0 && i < out_stride) {
                 if (tokens_out) tokens_out[(int64_t)r * out_stride + i] = tok;
                 if (best_logit) best_logit[(int64_t)r * out_stride + i] = key_logit(k);
@@ -1170,7 +1186,7 @@ __global__ __launch_bounds__(64) void finalize_tokens_kernel(unsigned long long*
             cursor[r] = cur;
             keys[r] = 0ull;
             if (nx.x) *nx.row_pos = cur;
-            if (single && nx.stopped && nx.eos && *nx.eos >= 0 && tok == *nx.eos) *nx.stopped = 1;
+            if (single && nx.stopped && eos >= 0 && tok == eos) *nx.stopped = 1;
         }
     }
     if (nx.x) {
