@@ -973,7 +973,19 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(AttnTileArgs p) {
     }
     __syncthreads();
 
-    // pass C: INT8 probabilities (zero past each row's last key)
+    // pass C: INT8 probabilities (zero past each row's last key): exponential
+    // / total correctly rounded, from each row's reciprocal and two residual
+    // corrections (e <= 1 <= total keeps e y finite; every total lies in
+    // [1, keys], the quotient's range, which the wave vote confirms)
+    float ty[16], tv[16];
+    bool in_range = true;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        tv[i] = tot[8 * (i >> 2) + 4 * hi + (i & 3)];
+        ty[i] = __fdiv_rn(1.0f, tv[i]);
+        in_range = in_range && fabsf(tv[i]) >= 0x1p-64f && fabsf(tv[i]) <= 0x1p64f;
+    }
+    const bool fast = __all(in_range);
     for (int b = wave; b < nblk; b += 4) {
 #pragma unroll
         for (int half = 0; half < 2; half++) {
@@ -985,7 +997,8 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(AttnTileArgs p) {
                 int8_t pq = 0;
                 if (t <= rpos[i]) {
                     const float e = tl_expf((float)S[i] * rs[i] - m[i]);
-                    float pr = __builtin_rintf(__fdiv_rn(e, tot[r]) * 127.0f);
+                    const float q = fast ? rn_div_fast(e, RnDiv{tv[i], ty[i], true}) : __fdiv_rn(e, tv[i]);
+                    float pr = __builtin_rintf(q * 127.0f);
                     pr = pr < 0.0f ? 0.0f : (pr > 127.0f ? 127.0f : pr);
                     pq = (int8_t)(int)pr;
                 }
@@ -1865,8 +1878,13 @@ __global__ __launch_bounds__(256) void attention_tile_reg_kernel(AttnTileArgs p)
     }
     __syncthreads();
 
-    // pass C: INT8 probabilities, four consecutive keys per 32-bit store
+    // pass C: INT8 probabilities, four consecutive keys per 32-bit store;
+    // exponential / total correctly rounded from the row's reciprocal and two
+    // residual corrections (e <= 1 <= total keeps e y finite; the wave vote
+    // confirms every total lies in the quotient's range)
     const float tr = tot[col];
+    const RnDiv dv{tr, __fdiv_rn(1.0f, tr), true};
+    const bool fast = __all(fabsf(tr) >= 0x1p-64f && fabsf(tr) <= 0x1p64f);
 #pragma unroll
     for (int j = 0; j < NB; j++) {
         const int b = wave + 4 * j;
@@ -1878,7 +1896,8 @@ __global__ __launch_bounds__(256) void attention_tile_reg_kernel(AttnTileArgs p)
                     unsigned word = 0;
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
-                        float pr = __builtin_rintf(__fdiv_rn(sc[j][half][4 * q + r], tr) * 127.0f);
+                        const float e = sc[j][half][4 * q + r];
+                        float pr = __builtin_rintf((fast ? rn_div_fast(e, dv) : __fdiv_rn(e, tr)) * 127.0f);
                         pr = pr < 0.0f ? 0.0f : (pr > 127.0f ? 127.0f : pr);
                         word |= (unsigned)(uint8_t)(int)pr << (8 * r);
                     }
