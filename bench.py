@@ -359,10 +359,32 @@ def decode_section(eng, host, args):
             gbs = sum(kbytes[k] * per_step[k] for k in kbytes) / (us * 1e-6) / 1e9
             gemv.update({f"{dst}_us_per_step": round(us, 2), f"{dst}_gbs": round(gbs, 1),
                          f"{dst}_frac": round(gbs / HBM_PEAK_GBS, 4)})
-    return dict(prompt=prompt, first=first, toks=toks, dt=dt, kernels=kernels, accounting=accounting,
+    margin = lm_head_margin(eng, prompt, first, toks)
+    return dict(prompt=prompt, first=first, toks=toks, dt=dt, kernels=kernels, accounting=accounting, margin=margin,
                 eos_watch={"tok_s": round(args.steps / eos_dt, 2), "vs_no_eos": round(dt / eos_dt, 4),
                            "eos_id": int(never)},
                 bytes_step=bytes_step, gemv=gemv)
+
+
+def lm_head_margin(eng, prompt, first, toks):
+    """Top-1 minus top-2 logit of every greedy choice of the timed run (the
+    prompt's next token and each decode step's), from one untimed prefill of
+    prompt + generated tokens through tl_prefill_logits; prefill rows equal
+    token-by-token decode bit for bit, so each row's argmax must be the token
+    the decode produced."""
+    import torch
+    seq = np.concatenate([prompt, [first], toks[:-1]]).astype(np.int32)
+    n, V = int(seq.size), CFG["vocab"]
+    logits = torch.empty((n, V), dtype=torch.float32, device="cuda")
+    eng.rt.call("tl_prefill_logits", 0, seq, n, logits)
+    rows = logits[prompt.size - 1:].cpu().numpy()
+    top2 = np.partition(rows, V - 2, axis=1)[:, V - 2:]
+    margin = top2[:, 1] - top2[:, 0]
+    want = np.concatenate([[first], toks]).astype(np.int64)
+    return {"choices": int(rows.shape[0]), "min": float(margin.min()), "p01": float(np.quantile(margin, 0.01)),
+            "median": float(np.median(margin)), "argmin_step": int(margin.argmin()) - 1,
+            "exact_ties": int((margin == 0).sum()),
+            "argmax_matches_decode": bool(np.array_equal(rows.argmax(axis=1), want))}
 
 
 def main():
@@ -488,6 +510,7 @@ def main():
                      "busy_us": glu.get("busy_us"), "busy_frac": glu.get("busy_frac")},
         "decode_step_hbm_frac": round(d["bytes_step"] / (d["dt"] / args.steps) / 1e9 / HBM_PEAK_GBS, 4),
         "decode_gemv": d["gemv"],
+        "lm_head_margin": d["margin"],
         "step_accounting": d["accounting"],
         "kernels": kernels,
         "eos_watch": d["eos_watch"],
