@@ -547,11 +547,6 @@ int32_t layer_row1(tl_handle* h, int32_t layer, int32_t max_t) {
     return TL_OK;
 }
 
-// one decoder layer (GI:256-281) for `rows` rows of h->x whose sequence and
-// position are in h->row_seq / h->row_pos; max_t bounds pos + 1 over the rows.
-// decode: every row is a different sequence (its own K/V row is appended by
-// the attention kernel); otherwise the rows are consecutive prompt positions
-// of one sequence (all appended before attention reads them).
 // K slice of a batched-decode GEMM: halve the slice while the 32-column
 // tiles times the slices stay within the 256 CUs (one round of 16-wavefront
 // workgroups) and a slice keeps at least 32 chunks of 32 bytes (two per
@@ -585,6 +580,16 @@ static int32_t linear_acc(tl_handle* h, int32_t rows, const int8_t* wp, int32_t 
     return TL_OK;
 }
 
+// sums a failed batched step left in h->racc (between a K-sliced GEMM and its
+// fold): cleared before anything else uses the buffer
+static int32_t discard_pending_sums(tl_handle* h) {
+    if (h->racc_clean && !h->racc_res_ws) return TL_OK;
+    TL_LAUNCH(h, launch_fill_u32(h->stream, (unsigned*)h->racc, (int32_t)h->racc_cap, 0u));
+    h->racc_clean = true;
+    h->racc_res_ws = nullptr;
+    return TL_OK;
+}
+
 // RMSNorm + quantization of the rows of h->x into h->a8 / h->as, first adding
 // a pending down projection's sums from h->racc (launch_rows_fold)
 static int32_t rows_rmsnorm(tl_handle* h, int32_t rows, const float* g) {
@@ -605,14 +610,19 @@ static int32_t rows_rmsnorm(tl_handle* h, int32_t rows, const float* g) {
     return TL_OK;
 }
 
+// one decoder layer (GI:256-281) for `rows` rows of h->x whose sequence and
+// position are in h->row_seq / h->row_pos; max_t bounds pos + 1 over the rows.
+// decode: every row is a different sequence (its own K/V row is appended by
+// the attention kernel); otherwise the rows are consecutive prompt positions
+// of one sequence (all appended before attention reads them).
 int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, bool decode) {
     if (rows == 1) return layer_row1(h, layer, max_t);
     const tl_config& c = h->cfg;
     const LayerDev& L = h->layers[layer];
     const int D = h->D, F = h->F, KVD = h->KVD, QKV = h->QKV;
     const bool ks = decode && kslice_ok(h, L, rows);
-    if (h->racc_res_ws && !ks) return fail(h, TL_ERR_INTERNAL, "pending K-slice sums outside batched decode");
     int32_t r;
+    if (!ks && (r = discard_pending_sums(h))) return r;
     if ((r = rows_rmsnorm(h, rows, L.g_in))) return r;
     if ((r = linear(h, EPI_DEQUANT, rows, h->a8, h->as, L.wqkv, L.sqkv, nullptr, nullptr, QKV, D, nullptr, h->qkv, TL_K_QKV,
                     L.wqkv_p)))
@@ -682,11 +692,12 @@ int32_t lm_head_rows(tl_handle* h, const float* xrow, int32_t rows, int32_t seq,
         Prof p(h, TL_K_LMHEAD, (double)V * D + V * 4.0 + D * 8.0);
         TL_LAUNCH(h, launch_gemv_fused(h->stream, PRO_RMSNORM, EPI_ARGMAX, g));
     } else {
-        if (h->racc_res_ws) {
-            if (xrow != h->x) return fail(h, TL_ERR_INTERNAL, "pending K-slice sums for other rows");
+        if (h->racc_res_ws && xrow == h->x) {
             int32_t r = rows_rmsnorm(h, rows, h->g_final);
             if (r) return r;
         } else {
+            int32_t r = discard_pending_sums(h);
+            if (r) return r;
             Prof p(h, TL_K_NORM, (double)rows * D * 9.0);
             TL_LAUNCH(h, launch_rmsnorm_quant(h->stream, xrow, h->g_final, rows, D, c.rms_eps, h->plan, nullptr, h->a8, h->as));
         }
@@ -852,15 +863,10 @@ int32_t decode_graph_launch(tl_handle* h, int32_t seq) {
 // captured once per batch size and replayed.
 int32_t batch_step(tl_handle* h, int32_t n_seqs, int32_t max_t) {
     const tl_config& c = h->cfg;
-    if (!h->racc_clean || h->racc_res_ws) {
-        // an earlier step failed between a K-sliced GEMM and its fold
-        TL_LAUNCH(h, launch_fill_u32(h->stream, (unsigned*)h->racc, (int32_t)h->racc_cap, 0u));
-        h->racc_clean = true;
-        h->racc_res_ws = nullptr;
-    }
+    int32_t r;
+    if ((r = discard_pending_sums(h))) return r;
     TL_LAUNCH(h, launch_embed_step(h->stream, h->token_cur, h->row_seq, n_seqs, h->cursor, h->row_pos, h->D, c.vocab,
                                    h->emb, h->emb_s, h->x));
-    int32_t r;
     for (int l = 0; l < c.n_layers; l++)
         if ((r = layer_rows(h, l, n_seqs, max_t, true))) return r;
     return lm_head_rows(h, h->x, n_seqs, 0, 1);
