@@ -169,6 +169,12 @@ struct AttnDecodeArgs {
     double attn_scale;
     float* out;           // [rows][D]
     unsigned long long* ts;   // decode timeline: [waves][2] clock stamps, or null
+    // the grouped kernel may read Q|K|V as the integer sums of a K-sliced GEMM
+    // instead (qkv unused): value i of a row = f32(qacc[i]) f32(qas[row] qws[i]),
+    // the GEMM's DEQUANT epilogue
+    const int32_t* qacc;  // [rows][D + 2 KVD] or null
+    const double* qas;    // [rows]
+    const float* qws;     // [D + 2 KVD]
 };
 
 // NW wavefronts per workgroup; wavefront w takes key blocks w, w + NW, ...
@@ -676,6 +682,10 @@ __global__ __launch_bounds__(kGW * 64) void attention_group_kernel(AttnDecodeArg
     float* bsum = (float*)(p8 + HPW * tpad);              // [HPW][nblk]
     int* accs = (int*)(bsum + HPW * nblk);                // [kGW][HPW][64]
     const float* src = p.qkv + (int64_t)row * W;
+    const int32_t* srci = p.qacc + (int64_t)row * W;
+    const bool sums = p.qacc != nullptr;   // uniform
+    const double qsx = sums ? p.qas[row] : 0.0;
+    auto qkv_at = [&](int i) -> float { return sums ? (float)srci[i] * deq_mult(qsx, p.qws[i]) : src[i]; };
     const int d = lane;
 
     // 0) loads in the order they are needed (loads complete in issue order):
@@ -686,12 +696,12 @@ __global__ __launch_bounds__(kGW * 64) void attention_group_kernel(AttnDecodeArg
     constexpr int kQPer = 4;   // Q elements per thread: D <= 4 x 1024
     float qv[kQPer];
 #pragma unroll
-    for (int j = 0; j < kQPer; j++) qv[j] = src[min(tid + kGW * 64 * j, D - 1)];
+    for (int j = 0; j < kQPer; j++) qv[j] = qkv_at(min(tid + kGW * 64 * j, D - 1));
     float qh = 0.0f, kx = 0.0f, vx = 0.0f;
-    if (wave < HPW) qh = src[(h0 + wave) * kHeadDim + d];
+    if (wave < HPW) qh = qkv_at((h0 + wave) * kHeadDim + d);
     if (wave == HPW) {
-        kx = src[D + g * kHeadDim + d];
-        vx = src[D + KVD + g * kHeadDim + d];
+        kx = qkv_at(D + g * kHeadDim + d);
+        vx = qkv_at(D + KVD + g * kHeadDim + d);
     }
     const float cs = p.cosb[(int64_t)pos * kHeadDim + d];
     const float sn = p.sinb[(int64_t)pos * kHeadDim + d];
@@ -952,17 +962,31 @@ hipError_t launch_gemv_fused(hipStream_t s, int pro, int epi, const GemvArgs& a)
     return hipErrorInvalidValue;
 }
 
+bool attention_decode_grouped(int32_t rows, int32_t n_heads, int32_t n_kv, int32_t max_t, int32_t hpw) {
+    if (rows <= 1 || n_kv <= 0 || n_heads % n_kv || n_heads > 32 * 4) return false;
+    const int G = n_heads / n_kv, D = n_heads * kHeadDim;
+    return G <= kMaxGroupHeads && G % 4 == 0 && max_t <= kGroupMaxKeys && D <= 4 * kGW * 64 &&
+           (hpw == 1 || (hpw == 8 && G == 8));
+}
+
 hipError_t launch_attention_decode(hipStream_t s, const float* qkv, int32_t rows, int32_t n_heads, int32_t n_kv,
                                    RowMap rm, const float* cos, const float* sin, KvGeom kv, int32_t layer,
                                    const float* kv_sk, const float* kv_sv, float* out, int32_t max_t, int32_t hpw,
-                                   unsigned long long* ts) {
+                                   unsigned long long* ts, const QkvSums* sums) {
     if (rows <= 0) return hipSuccess;
     const int G = n_heads / n_kv;
     if (n_heads % n_kv || G > kMaxGroupHeads || n_heads > 32 * 4) return hipErrorInvalidValue;
     const int D = n_heads * kHeadDim, W = D + 2 * n_kv * kHeadDim;
     const int tpad = (max_t + 63) & ~63;
     AttnDecodeArgs p{qkv, n_heads, n_kv, rm, cos, sin, kv, layer, kv_sk, kv_sv, 1.0 / sqrt((double)kHeadDim), out, ts};
-    if (rows > 1 && G % 4 == 0 && max_t <= kGroupMaxKeys && D <= 4 * kGW * 64 && (hpw == 1 || (hpw == 8 && G == 8))) {
+    const bool grouped = attention_decode_grouped(rows, n_heads, n_kv, max_t, hpw);
+    if (sums) {
+        if (!grouped || !sums->acc || !sums->as || !sums->ws) return hipErrorInvalidValue;
+        p.qacc = sums->acc;
+        p.qas = sums->as;
+        p.qws = sums->ws;
+    }
+    if (grouped) {
         // many rows: the grouped kernel, 4 (or 8) query heads per workgroup
         if (hpw == 8)
             TL_KLAUNCH((attention_group_kernel<8>), dim3(n_heads / 8, rows), dim3(kGW * 64), group_lds_bytes(8, tpad),

@@ -113,8 +113,10 @@ struct GemmArgs {
 hipError_t launch_rmsnorm_quant(hipStream_t s, const float* x, const float* g, int32_t rows,
                                 int32_t n, float eps, PwPlan plan, float* y, int8_t* q,
                                 double* scales);
+// zero: optional [rows][zero_n] int32 buffer (zero_n % 4 == 0, 16-byte
+// aligned) each row's workgroup clears after quantizing
 hipError_t launch_quantize_rows(hipStream_t s, const float* x, int32_t rows, int32_t n,
-                                int8_t* q, double* scales);
+                                int8_t* q, double* scales, int32_t* zero = nullptr, int32_t zero_n = 0);
 
 // RMSNorm row prologue that first finishes a K-sliced small-M GEMM with a
 // residual epilogue: its integer sums acc (EPI_ACC, rows x n) are dequantized
@@ -278,10 +280,20 @@ hipError_t persist_occupancy(int32_t d, int32_t f, size_t lds, int* blocks_per_c
 
 hipError_t launch_gemm32(hipStream_t s, int epi, const GemmArgs& a, int32_t splits, int32_t cfg);
 hipError_t launch_gemv_fused(hipStream_t s, int pro, int epi, const GemvArgs& a);
+// Q|K|V rows as the integer sums of a K-sliced GEMM with its dequantization
+// scales (batched decode; the grouped attention kernel only)
+struct QkvSums {
+    const int32_t* acc;   // [rows][D + 2 KVD]
+    const double* as;     // [rows] A-row scales of the GEMM
+    const float* ws;      // [D + 2 KVD] weight scales
+};
+// launch_attention_decode takes the grouped (many-row) kernel for these
+// arguments; the only path that accepts QkvSums
+bool attention_decode_grouped(int32_t rows, int32_t n_heads, int32_t n_kv, int32_t max_t, int32_t hpw);
 hipError_t launch_attention_decode(hipStream_t s, const float* qkv, int32_t rows, int32_t n_heads, int32_t n_kv,
                                    RowMap rm, const float* cos, const float* sin, KvGeom kv, int32_t layer,
                                    const float* kv_sk, const float* kv_sv, float* out, int32_t max_t, int32_t hpw,
-                                   unsigned long long* ts = nullptr);
+                                   unsigned long long* ts = nullptr, const QkvSums* sums = nullptr);
 hipError_t launch_embed_step(hipStream_t s, const int32_t* tok_by_seq, const int32_t* seq_of_row, int32_t rows,
                              const int32_t* cursor, int32_t* row_pos, int32_t d, int32_t vocab, const int8_t* emb,
                              const float* emb_s, float* x);

@@ -86,11 +86,14 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const float* __restr
 // the same two row operations for rows of width n <= 1024 KCH, n % 64 == 0,
 // 16-byte aligned, one workgroup per row: float4 loads, the decode GEMV
 // prologues (identical arithmetic: NumPy pairwise tree, per-row scale), and
-// 16-byte stores of the INT8 row
+// 16-byte stores of the INT8 row.  With `zero`, the workgroup also clears
+// zero_n int32 of its row of that buffer (integer sums that the kernels
+// before it have consumed, zero again for the next K-sliced GEMM).
 template <int PRO, int KCH>
 __global__ __launch_bounds__(kNT) void rows_prologue_kernel(const float* __restrict__ x, const float* __restrict__ g,
                                                            int32_t n, float eps, PwPlan plan, int8_t* __restrict__ q,
-                                                           double* __restrict__ scales) {
+                                                           double* __restrict__ scales, int32_t* __restrict__ zero,
+                                                           int32_t zero_n) {
     __shared__ __align__(16) int8_t xs8[KCH * 1024];
     __shared__ __align__(16) float sq[PRO == PRO_RMSNORM ? KCH * 1024 : 4];
     __shared__ __align__(16) float part[PRO == PRO_RMSNORM ? 8 * 64 : 4];
@@ -111,21 +114,26 @@ __global__ __launch_bounds__(kNT) void rows_prologue_kernel(const float* __restr
     int8_t* qr = q + (int64_t)row * n;
     for (int o = tid * 16; o < n; o += kNT * 16) *(v4i*)(qr + o) = *(const v4i*)(xs8 + o);
     if (tid == 0) scales[row] = xscale;
+    if (zero)
+        for (int i = tid * 4; i < zero_n; i += kNT * 4) *(v4i*)(zero + (int64_t)row * zero_n + i) = (v4i){0, 0, 0, 0};
 }
 
 template <int PRO>
 static hipError_t launch_rows_prologue(hipStream_t s, const float* x, const float* g, int32_t rows, int32_t n,
-                                       float eps, PwPlan plan, int8_t* q, double* scales) {
+                                       float eps, PwPlan plan, int8_t* q, double* scales, int32_t* zero = nullptr,
+                                       int32_t zero_n = 0) {
     const dim3 grid(rows), block(kNT);
+#define TL_RPL(C) TL_KLAUNCH((rows_prologue_kernel<PRO, C>), grid, block, 0, s, x, g, n, eps, plan, q, scales, zero, zero_n)
     switch ((n + 1023) / 1024) {
-        case 1: TL_KLAUNCH((rows_prologue_kernel<PRO, 1>), grid, block, 0, s, x, g, n, eps, plan, q, scales); break;
-        case 2: TL_KLAUNCH((rows_prologue_kernel<PRO, 2>), grid, block, 0, s, x, g, n, eps, plan, q, scales); break;
-        case 3: TL_KLAUNCH((rows_prologue_kernel<PRO, 3>), grid, block, 0, s, x, g, n, eps, plan, q, scales); break;
-        case 4: TL_KLAUNCH((rows_prologue_kernel<PRO, 4>), grid, block, 0, s, x, g, n, eps, plan, q, scales); break;
-        case 5: TL_KLAUNCH((rows_prologue_kernel<PRO, 5>), grid, block, 0, s, x, g, n, eps, plan, q, scales); break;
-        case 6: TL_KLAUNCH((rows_prologue_kernel<PRO, 6>), grid, block, 0, s, x, g, n, eps, plan, q, scales); break;
+        case 1: TL_RPL(1); break;
+        case 2: TL_RPL(2); break;
+        case 3: TL_RPL(3); break;
+        case 4: TL_RPL(4); break;
+        case 5: TL_RPL(5); break;
+        case 6: TL_RPL(6); break;
         default: return hipErrorInvalidValue;
     }
+#undef TL_RPL
     return hipGetLastError();
 }
 
@@ -1384,10 +1392,12 @@ hipError_t launch_rmsnorm_quant(hipStream_t s, const float* x, const float* g, i
 }
 
 hipError_t launch_quantize_rows(hipStream_t s, const float* x, int32_t rows, int32_t n, int8_t* q,
-                                double* scales) {
+                                double* scales, int32_t* zero, int32_t zero_n) {
     if (rows <= 0) return hipSuccess;
+    if (zero && (zero_n <= 0 || zero_n % 4 || (uintptr_t)zero % 16 || !rows_fast_ok(x, nullptr, q, n)))
+        return hipErrorInvalidValue;
     if (rows_fast_ok(x, nullptr, q, n))
-        return launch_rows_prologue<PRO_QUANT>(s, x, nullptr, rows, n, 0.0f, PwPlan{8, 1}, q, scales);
+        return launch_rows_prologue<PRO_QUANT>(s, x, nullptr, rows, n, 0.0f, PwPlan{8, 1}, q, scales, zero, zero_n);
     TL_KLAUNCH(quantize_rows_kernel<false>, dim3(rows), dim3(256), 0, s, x, n, q, (void*)scales);
     return hipGetLastError();
 }

@@ -130,6 +130,10 @@ struct tl_handle {
     int32_t* racc = nullptr;      // [32][D] integer sums of the K-sliced batched-decode down GEMM; zero
                                   // between uses (the fold prologue clears what it read)
     size_t racc_cap = 0;          // int32 elements
+    int32_t* qacc = nullptr;      // [32][QKV] integer sums of the K-sliced batched-decode Q|K|V GEMM, read
+                                  // by the attention kernel; zero between uses (the attention output's
+                                  // quantization clears them)
+    size_t qacc_cap = 0;          // int32 elements
     unsigned* tile_ctr = nullptr;         // [kSkinnyTiles] arrival counters of the small-M GEMM, zero between launches
     size_t partial_cap = 0;       // int32 elements
 
@@ -162,6 +166,9 @@ struct tl_handle {
     const float* racc_res_ws = nullptr;   // racc holds a down projection's sums (these weight scales) that
                                           // the next RMSNorm prologue adds to h->x
     bool racc_clean = true;               // false from an EPI_ACC launch until its fold has run
+    bool qkv_kslice = true;               // batched decode: K-sliced Q|K|V GEMM whose sums the attention
+                                          // kernel dequantizes (TL_BATCH_QKV_KSLICE=0 turns it off)
+    bool qacc_clean = true;               // false from a Q|K|V EPI_ACC launch until qacc is cleared
     bool rows_one_seq = false;            // the uploaded rows are one sequence at rows_pos0 + r
     int32_t rows_seq = 0, rows_pos0 = 0;
     bool persist_ok = false;              // geometry and occupancy allow it
@@ -547,17 +554,17 @@ int32_t layer_row1(tl_handle* h, int32_t layer, int32_t max_t) {
     return TL_OK;
 }
 
-// K slice of a batched-decode GEMM: halve the slice while the 32-column
-// tiles times the slices stay within the 256 CUs (one round of 16-wavefront
-// workgroups) and a slice keeps at least 32 chunks of 32 bytes (two per
-// wavefront).  At TinyLlama's shapes only the down projection (64 tiles,
-// K = 5632) is sliced, in four: O and gate/up measured no faster sliced (the
-// atomic adds and the fold cost what the spread gained; gate/up's 176 tiles
-// leave no room for a second slice in one round)
+// K slice of a batched-decode GEMM: as many slices as keep the 32-column
+// tiles times the slices within the 256 CUs (one round of 16-wavefront
+// workgroups) and at least 16 chunks of 32 bytes (one per wavefront) in a
+// slice.  At TinyLlama's shapes the down projection (64 tiles, K = 5632) is
+// sliced in four and Q|K|V (80 tiles, K = 2048) in three: O and gate/up
+// measured no faster sliced (the atomic adds and the fold cost what the
+// spread gained; gate/up's 176 tiles leave no room for a second slice in one
+// round)
 static int32_t kslice_len(int32_t n, int32_t k) {
     const int tiles = n / 32, kch = k / 32;
-    int s = 1;
-    while (tiles * 2 * s <= 256 && kch / (2 * s) >= 32) s *= 2;
+    const int s = std::max(1, std::min(256 / std::max(tiles, 1), kch / 16));
     return ((kch + s - 1) / s) * 32;
 }
 
@@ -568,25 +575,42 @@ static bool kslice_ok(tl_handle* h, const LayerDev& L, int32_t rows) {
            F % 64 == 0 && D <= 6144 && F <= 6144 && h->plan.n_leaves <= 64 && (size_t)rows * D <= h->racc_cap;
 }
 
-// integer-sum GEMM into h->racc (EPI_ACC), K-sliced
-static int32_t linear_acc(tl_handle* h, int32_t rows, const int8_t* wp, int32_t n, int32_t k, int kclass) {
+// batched decode can also run its Q|K|V GEMM K-sliced, its sums read by the
+// grouped attention kernel
+static bool qkv_kslice_ok(tl_handle* h, const LayerDev& L, int32_t rows, int32_t max_t) {
+    const tl_config& c = h->cfg;
+    const int hpw = c.n_heads / c.n_kv_heads == 8 && h->batch_hpw == 8 ? 8 : 1;
+    return h->qkv_kslice && L.wqkv_p && h->QKV % 32 == 0 && (size_t)rows * h->QKV <= h->qacc_cap &&
+           attention_decode_grouped(rows, c.n_heads, c.n_kv_heads, max_t, hpw);
+}
+
+// integer-sum GEMM into acc (h->racc or h->qacc, zero on entry; EPI_ACC),
+// K-sliced; *clean is set false until the sums are consumed and cleared
+static int32_t linear_acc(tl_handle* h, int32_t rows, const int8_t* wp, int32_t n, int32_t k, int kclass,
+                          int32_t* acc, bool* clean) {
     GemmArgs a{};
-    a.a = h->a8; a.as = h->as; a.wp = wp; a.acc = h->racc;
+    a.a = h->a8; a.as = h->as; a.wp = wp; a.acc = acc;
     a.m = rows; a.n = n; a.k = k; a.k_split = kslice_len(n, k);
     const double bytes = (double)rows * k + (double)n * k + (double)rows * n * 4.0;
-    h->racc_clean = false;
+    *clean = false;
     Prof p(h, kclass, bytes);
     TL_LAUNCH(h, launch_gemm_rows32(h->stream, EPI_ACC, a, rows32_waves(h, EPI_ACC)));
     return TL_OK;
 }
 
-// sums a failed batched step left in h->racc (between a K-sliced GEMM and its
-// fold): cleared before anything else uses the buffer
+// sums a failed batched step left in h->racc or h->qacc (between a K-sliced
+// GEMM and the kernel that consumes and clears them): cleared before anything
+// else uses the buffers
 static int32_t discard_pending_sums(tl_handle* h) {
-    if (h->racc_clean && !h->racc_res_ws) return TL_OK;
-    TL_LAUNCH(h, launch_fill_u32(h->stream, (unsigned*)h->racc, (int32_t)h->racc_cap, 0u));
-    h->racc_clean = true;
-    h->racc_res_ws = nullptr;
+    if (!h->racc_clean || h->racc_res_ws) {
+        TL_LAUNCH(h, launch_fill_u32(h->stream, (unsigned*)h->racc, (int32_t)h->racc_cap, 0u));
+        h->racc_clean = true;
+        h->racc_res_ws = nullptr;
+    }
+    if (!h->qacc_clean) {
+        TL_LAUNCH(h, launch_fill_u32(h->stream, (unsigned*)h->qacc, (int32_t)h->qacc_cap, 0u));
+        h->qacc_clean = true;
+    }
     return TL_OK;
 }
 
@@ -621,18 +645,25 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
     const LayerDev& L = h->layers[layer];
     const int D = h->D, F = h->F, KVD = h->KVD, QKV = h->QKV;
     const bool ks = decode && kslice_ok(h, L, rows);
+    const bool qks = ks && qkv_kslice_ok(h, L, rows, max_t);
     int32_t r;
     if (!ks && (r = discard_pending_sums(h))) return r;
     if ((r = rows_rmsnorm(h, rows, L.g_in))) return r;
-    if ((r = linear(h, EPI_DEQUANT, rows, h->a8, h->as, L.wqkv, L.sqkv, nullptr, nullptr, QKV, D, nullptr, h->qkv, TL_K_QKV,
-                    L.wqkv_p)))
+    if (qks) {
+        // Q|K|V (K = D) K-sliced over the chip: the attention kernel
+        // dequantizes the integer sums it reads from h->qacc
+        if ((r = linear_acc(h, rows, L.wqkv_p, QKV, D, TL_K_QKV, h->qacc, &h->qacc_clean))) return r;
+    } else if ((r = linear(h, EPI_DEQUANT, rows, h->a8, h->as, L.wqkv, L.sqkv, nullptr, nullptr, QKV, D, nullptr, h->qkv,
+                           TL_K_QKV, L.wqkv_p))) {
         return r;
+    }
     if (decode) {
         const int G = c.n_heads / c.n_kv_heads;
+        const QkvSums sums{h->qacc, h->as, L.sqkv};
         Prof p(h, TL_K_ATTN, (double)rows * c.n_kv_heads * (double)max_t * 128.0 + rows * QKV * 4.0);
         TL_LAUNCH(h, launch_attention_decode(h->stream, h->qkv, rows, c.n_heads, c.n_kv_heads, rowmap(h), h->rope_cos,
                                              h->rope_sin, h->kv, layer, h->kv_sk, h->kv_sv, h->att, max_t,
-                                             G == 8 && h->batch_hpw == 8 ? 8 : 1));
+                                             G == 8 && h->batch_hpw == 8 ? 8 : 1, nullptr, qks ? &sums : nullptr));
     } else {
         {
             Prof p(h, TL_K_ATTN, (double)rows * (QKV * 4.0 + D) + (double)rows * KVD * 2.0);
@@ -643,8 +674,11 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
         TL_LAUNCH(h, rows_attention(h, h->q8, h->qs, rows, layer, h->att, max_t));
     }
     {
-        Prof p(h, TL_K_NORM, (double)rows * D * 5.0);
-        TL_LAUNCH(h, launch_quantize_rows(h->stream, h->att, rows, D, h->a8, h->as));
+        // with the Q|K|V sums consumed, this kernel also clears them
+        Prof p(h, TL_K_NORM, (double)rows * D * 5.0 + (qks ? (double)rows * QKV * 4.0 : 0.0));
+        TL_LAUNCH(h, launch_quantize_rows(h->stream, h->att, rows, D, h->a8, h->as, qks ? h->qacc : nullptr,
+                                          qks ? QKV : 0));
+        if (qks) h->qacc_clean = true;
     }
     if ((r = linear(h, EPI_DEQUANT_RES, rows, h->a8, h->as, L.wo, L.so, nullptr, nullptr, D, D, h->x, h->x, TL_K_O,
                     L.wo_p)))
@@ -663,7 +697,7 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
     if (ks) {
         // the down GEMM (K = F) K-sliced over the chip: its integer sums wait
         // in h->racc for the next layer's input RMSNorm, or the final one
-        if ((r = linear_acc(h, rows, L.wd_p, D, F, TL_K_DOWN))) return r;
+        if ((r = linear_acc(h, rows, L.wd_p, D, F, TL_K_DOWN, h->racc, &h->racc_clean))) return r;
         h->racc_res_ws = L.sd;
         return TL_OK;
     }
@@ -974,6 +1008,7 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
         (e = dalloc(h, &h->n_gen, (size_t)max_seqs)) || (e = dalloc(h, &h->eos_id, (size_t)max_seqs)) ||
         (e = dalloc(h, &h->stopped, (size_t)max_seqs)) ||
         (e = dalloc(h, &h->racc, h->racc_cap = (size_t)std::min(32, max_seqs) * D)) ||
+        (e = dalloc(h, &h->qacc, h->qacc_cap = (size_t)std::min(32, max_seqs) * h->QKV)) ||
         (e = dalloc(h, &h->tokens_out, (size_t)max_seqs * c.max_pos)) ||
         (e = dalloc(h, &h->logit_out, (size_t)max_seqs * c.max_pos)) ||
         (e = dalloc(h, &h->rope_cos, (size_t)c.max_pos * kHeadDim)) ||
@@ -1014,7 +1049,8 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
         (e = hipMemsetAsync(h->eos_id, 0xFF, sizeof(int32_t) * max_seqs, h->stream)) ||
         (e = hipMemsetAsync(h->stopped, 0, sizeof(int32_t) * max_seqs, h->stream)) ||
         (e = hipMemsetAsync(h->tile_ctr, 0, sizeof(unsigned) * kSkinnyTiles, h->stream)) ||
-        (e = hipMemsetAsync(h->racc, 0, sizeof(int32_t) * h->racc_cap, h->stream)))
+        (e = hipMemsetAsync(h->racc, 0, sizeof(int32_t) * h->racc_cap, h->stream)) ||
+        (e = hipMemsetAsync(h->qacc, 0, sizeof(int32_t) * h->qacc_cap, h->stream)))
         return bad(e);
     std::vector<float> cs, sn;
     default_rope(c.max_pos, c.rope_theta, cs, sn);
@@ -1037,6 +1073,7 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
     if (const char* env = std::getenv("TL_GEMM_SMALL")) h->gemm_small = std::atoi(env);
     if (const char* env = std::getenv("TL_GEMM_CFG")) h->gemm_cfg = std::atoi(env);
     if (const char* env = std::getenv("TL_BATCH_KSLICE")) h->batch_kslice = env[0] != '0';
+    if (const char* env = std::getenv("TL_BATCH_QKV_KSLICE")) h->qkv_kslice = env[0] != '0';
     if (const char* env = std::getenv("TL_ROWS32_WAVES")) h->rows32_waves = std::atoi(env);
     if ((e = hipStreamSynchronize(h->stream))) return bad(e);
     *out = h;
