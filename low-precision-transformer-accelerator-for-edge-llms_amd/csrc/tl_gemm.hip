@@ -558,4 +558,313 @@ hipError_t launch_gemm32(hipStream_t s, int epi, const GemmArgs& a, int32_t spli
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Prefill GEMMs on packed operands (a.ap, a.wp, a.wp2).  Both operands are
+// stored as 1 KiB MFMA blocks: block (t, c) holds rows [32 t, 32 t + 32) x K
+// bytes [32 c, 32 c + 32), with row 32 t + l % 32's K bytes 32 c + 16 (l / 32)
+// .. +16 at byte 16 l, so a wavefront's fragment load is one coalesced 1 KiB
+// read that hands lane l exactly its MFMA operand.  A's rows are padded to
+// the row tile (128); what the padding rows hold only reaches discarded rows.
+//
+// Why this form (measured at M = 512, TinyLlama shapes): a CU takes in about
+// 33 bytes per clock through its vector loads, whether they land in
+// registers or in LDS (global -> LDS loads), and loads that feed LDS add to
+// the fragment reads out of LDS instead of overlapping them.  So fragments
+// that one wavefront alone uses go straight into its registers, and only
+// operands that several wavefronts share go through LDS.
+// ---------------------------------------------------------------------------
+
+typedef __attribute__((address_space(1))) void PkGlobal;
+typedef __attribute__((address_space(3))) void PkLds;
+
+TL_DEV const int8_t* pk_block(const int8_t* base, int tile, int chunk, int kc) {
+    return base + ((int64_t)tile * kc + chunk) * 1024;
+}
+
+template <int N_>
+TL_DEV void pk_wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N_) : "memory");
+}
+
+// (1) one-matrix GEMMs (DEQUANT, DEQUANT_RES), K a multiple of 512: the 4
+// wavefronts of a workgroup each compute the whole (32 TM) x (32 TN) tile
+// over their own quarter of K, both operands straight into registers
+// kPkSplitPD chunks (of 32 K bytes) ahead, with no LDS and no barrier in the
+// main loop.  The four partial tiles are added through LDS (exact integers)
+// and wavefront w finishes blocks w, w + 4, ... of the tile with the epilogue
+// arithmetic of every other GEMM here.  Tiles: 64 x 64 (TM = TN = 2) for O and
+// down (256 workgroups at M = 512), 32 x 160 (TM = 1, TN = 5) for Q|K|V
+// (N = 2560: 256 workgroups where 64 x 64 needs 320).
+constexpr int kPkSplitPD = 4;
+
+static size_t pk_split_lds_bytes(int tm, int tn) { return (size_t)4 * tm * tn * 16 * 64 * sizeof(int); }
+
+template <int TM, int TN, int EPI>
+__global__ __launch_bounds__(256) void gemm_pk_split_kernel(GemmArgs a) {
+    constexpr int NF = TM + TN, PD = kPkSplitPD, NBLK = TM * TN;
+    extern __shared__ __align__(16) int pk_red[];   // [4 waves][NBLK][16][64]
+    const int kc = a.k >> 5, per = kc >> 2;        // chunks of each wavefront (a multiple of PD)
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int mt0 = blockIdx.y * TM, nt0 = blockIdx.x * TN, c0 = wave * per;
+    const int8_t* ab = a.ap + lane * 16;
+    const int8_t* wb = a.wp + lane * 16;
+    v4i r[PD][NF];
+    auto load = [&](int set, int c) {
+#pragma unroll
+        for (int i = 0; i < TM; i++) r[set][i] = ld16(pk_block(ab, mt0 + i, c, kc));
+#pragma unroll
+        for (int j = 0; j < TN; j++) r[set][TM + j] = ld16(pk_block(wb, nt0 + j, c, kc));
+    };
+    v16i acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = (v16i){};
+    auto mma = [&](int set) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(r[set][i], r[set][TM + j], acc[i][j], 0, 0, 0);
+    };
+    // register set u holds chunks u, u + PD, ...: the loop body reloads each
+    // set right after its MFMAs, unconditionally (the last PD chunks are
+    // peeled), so every wait is for the oldest set only
+#pragma unroll
+    for (int u = 0; u < PD; u++) load(u, c0 + u);
+    for (int c = PD; c < per; c += PD) {
+#pragma unroll
+        for (int u = 0; u < PD; u++) {
+            mma(u);
+            load(u, c0 + c + u);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < PD; u++) mma(u);
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) pk_red[((wave * NBLK + i * TN + j) * 16 + e) * 64 + lane] = acc[i][j][e];
+    __syncthreads();
+    // block b: lane l, register e is output row 8 (e / 4) + 4 (l / 32) + e % 4,
+    // column l % 32; all of a block's loads before its stores (y may be the
+    // residual, updated in place)
+    for (int b = wave; b < NBLK; b += 4) {
+        const int i = b / TN, j = b % TN;
+        const int n = (nt0 + j) * 32 + (lane & 31);
+        const int rb = (mt0 + i) * 32 + 4 * (lane >> 5);
+        const float sw = a.ws[n];
+        double sx[16];
+        float res[EPI == EPI_DEQUANT_RES ? 16 : 1];
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const int m = min(rb + 8 * (e >> 2) + (e & 3), a.m - 1);
+            sx[e] = a.as[m];
+            if (EPI == EPI_DEQUANT_RES) res[e] = a.residual[(int64_t)m * a.n + n];
+        }
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            int sum = 0;
+#pragma unroll
+            for (int w = 0; w < 4; w++) sum += pk_red[((w * NBLK + b) * 16 + e) * 64 + lane];
+            const int m = rb + 8 * (e >> 2) + (e & 3);
+            const float v = (float)sum * deq_mult(sx[e], sw);
+            if (m < a.m) a.y[(int64_t)m * a.n + n] = EPI == EPI_DEQUANT_RES ? res[e] + v : v;
+        }
+    }
+}
+
+// (2) the GLU GEMM (gate and up), K a multiple of 256: 128 x (32 TN) output
+// tiles of each matrix, 4 x 1 wavefronts.  Wavefront w owns rows
+// [32 w, 32 w + 32) of the tile: its A fragments are its own and go straight
+// into registers two 128-byte K stages ahead.  The 8 TN weight blocks of a
+// stage (2 matrices x TN column tiles x 4 K chunks) are shared by the 4
+// wavefronts and arrive by global -> LDS loads (2 TN per wavefront) in a ring
+// of three stage buffers with one barrier per stage: stage k + 2 is loaded
+// into the buffer stage k - 1 used.  __syncthreads would wait for every
+// global -> LDS load in flight (they count as LDS writes to its fence), so the
+// barrier is a bare s_barrier after an explicit wait for this wavefront's
+// loads of the stage.  The SiLU-GLU epilogue runs on the wavefront's own
+// accumulators.
+constexpr int kPkGluStages = 3;
+
+static size_t pk_glu_lds_bytes(int tn) { return (size_t)kPkGluStages * 8 * tn * 1024; }
+
+// the stage's 8 TN weight fragments (block (s TN + j) 4 + q at byte 1024 x
+// block from addr) by one asm block that ends in its own LDS wait: the
+// compiler would otherwise make every LDS read wait for all global -> LDS
+// loads in flight, as it cannot tell the ring's buffers apart.  `keep` are
+// registers that must not be reused for the results (the addresses of the
+// global -> LDS loads just issued).
+template <int TN>
+TL_DEV void pk_lds_frags(v4i* bq, uint32_t addr, const int8_t* const* keep) {
+    if constexpr (TN == 1) {
+        asm volatile(
+            "ds_read_b128 %0, %8\n\tds_read_b128 %1, %8 offset:1024\n\t"
+            "ds_read_b128 %2, %8 offset:2048\n\tds_read_b128 %3, %8 offset:3072\n\t"
+            "ds_read_b128 %4, %8 offset:4096\n\tds_read_b128 %5, %8 offset:5120\n\t"
+            "ds_read_b128 %6, %8 offset:6144\n\tds_read_b128 %7, %8 offset:7168\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(bq[0]), "=&v"(bq[1]), "=&v"(bq[2]), "=&v"(bq[3]), "=&v"(bq[4]), "=&v"(bq[5]), "=&v"(bq[6]),
+              "=&v"(bq[7])
+            : "v"(addr), "v"(keep[0]), "v"(keep[1]));
+    } else {
+        asm volatile(
+            "ds_read_b128 %0, %16\n\tds_read_b128 %1, %16 offset:1024\n\t"
+            "ds_read_b128 %2, %16 offset:2048\n\tds_read_b128 %3, %16 offset:3072\n\t"
+            "ds_read_b128 %4, %16 offset:4096\n\tds_read_b128 %5, %16 offset:5120\n\t"
+            "ds_read_b128 %6, %16 offset:6144\n\tds_read_b128 %7, %16 offset:7168\n\t"
+            "ds_read_b128 %8, %16 offset:8192\n\tds_read_b128 %9, %16 offset:9216\n\t"
+            "ds_read_b128 %10, %16 offset:10240\n\tds_read_b128 %11, %16 offset:11264\n\t"
+            "ds_read_b128 %12, %16 offset:12288\n\tds_read_b128 %13, %16 offset:13312\n\t"
+            "ds_read_b128 %14, %16 offset:14336\n\tds_read_b128 %15, %16 offset:15360\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(bq[0]), "=&v"(bq[1]), "=&v"(bq[2]), "=&v"(bq[3]), "=&v"(bq[4]), "=&v"(bq[5]), "=&v"(bq[6]),
+              "=&v"(bq[7]), "=&v"(bq[8]), "=&v"(bq[9]), "=&v"(bq[10]), "=&v"(bq[11]), "=&v"(bq[12]),
+              "=&v"(bq[13]), "=&v"(bq[14]), "=&v"(bq[15])
+            : "v"(addr), "v"(keep[0]), "v"(keep[1]), "v"(keep[2]), "v"(keep[3]));
+    }
+}
+
+template <int TN>
+__global__ __launch_bounds__(256) void gemm_pk_glu_kernel(GemmArgs a) {
+    constexpr int NB = 2, BB = 8 * TN, PWB = BB / 4, NS = kPkGluStages;
+    extern __shared__ __align__(16) int8_t pk_glu_lds[];   // [NS][BB][1024]
+    const int kc = a.k >> 5, nk = a.k >> 7;                 // 128-byte stages, an even count >= 2
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int mt = blockIdx.y * 4 + wave, nt0 = blockIdx.x * TN;
+    const int8_t* ab = a.ap + lane * 16;
+    v4i ra[2][4];
+    auto a_load = [&](int set, int stage) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) ra[set][q] = ld16(pk_block(ab, mt, stage * 4 + q, kc));
+    };
+    const int8_t* src[PWB];   // this stage's global -> LDS sources
+#pragma unroll
+    for (int j = 0; j < PWB; j++) src[j] = a.wp;
+    auto b_issue = [&](int stage, int buf) {
+#pragma unroll
+        for (int j = 0; j < PWB; j++) {
+            const int b = wave * PWB + j, mat = b / (TN * 4), bb = b % (TN * 4);
+            src[j] = pk_block(mat ? a.wp2 : a.wp, nt0 + bb / 4, stage * 4 + bb % 4, kc) + lane * 16;
+            __builtin_amdgcn_global_load_lds((PkGlobal*)src[j], (PkLds*)(pk_glu_lds + (buf * BB + b) * 1024), 16, 0, 0);
+        }
+    };
+    v16i acc[NB][TN];
+#pragma unroll
+    for (int s = 0; s < NB; s++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[s][j] = (v16i){};
+    auto compute = [&](int kk, int u) {
+        v4i bq[BB];
+        pk_lds_frags<TN>(bq, (uint32_t)(uintptr_t)(pk_glu_lds + (kk % NS) * BB * 1024 + lane * 16), src);
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+            for (int s = 0; s < NB; s++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    acc[s][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ra[u][q], bq[(s * TN + j) * 4 + q], acc[s][j], 0, 0, 0);
+    };
+    b_issue(0, 0);
+    b_issue(1, 1);
+    a_load(0, 0);
+    a_load(1, 1);
+    // stage kk: this wavefront's loads of the stage (issued two stages back)
+    // are done when at most stage kk + 1's (PWB weight + 4 A loads) remain;
+    // after the barrier every wavefront's are, and every wavefront is past
+    // stage kk - 1, whose buffer then takes stage kk + 2
+    for (int k = 0; k < nk - 2; k += 2) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int kk = k + u;
+            pk_wait_vm<PWB + 4>();
+            asm volatile("s_barrier" ::: "memory");
+            b_issue(kk + 2, (kk + 2) % NS);
+            compute(kk, u);
+            a_load(u, kk + 2);
+        }
+    }
+    pk_wait_vm<PWB + 4>();
+    asm volatile("s_barrier" ::: "memory");
+    compute(nk - 2, 0);
+    pk_wait_vm<0>();
+    asm volatile("s_barrier" ::: "memory");
+    compute(nk - 1, 1);
+    const int rb = mt * 32 + 4 * (lane >> 5);
+    double sx[16];
+#pragma unroll
+    for (int e = 0; e < 16; e++) sx[e] = a.as[min(rb + 8 * (e >> 2) + (e & 3), a.m - 1)];
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        const int n = (nt0 + j) * 32 + (lane & 31);
+        const float sg = a.ws[n], su = a.ws2[n];
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const int m = rb + 8 * (e >> 2) + (e & 3);
+            const float gt = (float)acc[0][j][e] * deq_mult(sx[e], sg);
+            const float up = (float)acc[1][j][e] * deq_mult(sx[e], su);
+            if (m < a.m) a.y[(int64_t)m * a.n + n] = tl_silu(gt) * up;
+        }
+    }
+}
+
+// tile of the one-matrix packed GEMM: 32 x 160 when N is a multiple of 160
+// and that covers the chip in fewer rounds of 256 workgroups than 64 x 64
+static bool pk_split_narrow(int32_t m, int32_t n) {
+    if (n % 160) return false;
+    const int64_t t22 = (int64_t)((m + 63) / 64) * (n / 64), t15 = (int64_t)((m + 31) / 32) * (n / 160);
+    return n % 64 != 0 || (t15 + 255) / 256 < (t22 + 255) / 256;
+}
+
+bool gemm_pk_supported(int epi, int32_t m, int32_t n, int32_t k) {
+    if (m < 1 || n < 1 || k < 1) return false;
+    if (epi == EPI_GLU) return n % 64 == 0 && k % 256 == 0;   // both tile widths
+    if (epi != EPI_DEQUANT && epi != EPI_DEQUANT_RES) return false;
+    return k % 512 == 0 && (n % 64 == 0 || pk_split_narrow(m, n));
+}
+
+int32_t gemm_pk_row_pad() { return 128; }
+
+hipError_t launch_gemm_pk(hipStream_t s, int epi, const GemmArgs& a, int32_t glu_tn) {
+    if (a.m <= 0) return hipSuccess;
+    if (!a.ap || !a.wp || !gemm_pk_supported(epi, a.m, a.n, a.k) || (epi == EPI_GLU && !a.wp2))
+        return hipErrorInvalidValue;
+    const dim3 block(256);
+    if (epi == EPI_GLU) {
+        if (glu_tn == 1)
+            TL_KLAUNCH(gemm_pk_glu_kernel<1>, dim3(a.n / 32, (a.m + 127) / 128), block, pk_glu_lds_bytes(1), s, a);
+        else TL_KLAUNCH(gemm_pk_glu_kernel<2>, dim3(a.n / 64, (a.m + 127) / 128), block, pk_glu_lds_bytes(2), s, a);
+        return hipGetLastError();
+    }
+    const bool res = epi == EPI_DEQUANT_RES;
+    if (pk_split_narrow(a.m, a.n)) {
+        const dim3 grid(a.n / 160, (a.m + 31) / 32);
+        if (res) TL_KLAUNCH((gemm_pk_split_kernel<1, 5, EPI_DEQUANT_RES>), grid, block, pk_split_lds_bytes(1, 5), s, a);
+        else TL_KLAUNCH((gemm_pk_split_kernel<1, 5, EPI_DEQUANT>), grid, block, pk_split_lds_bytes(1, 5), s, a);
+    } else {
+        const dim3 grid(a.n / 64, (a.m + 63) / 64);
+        if (res) TL_KLAUNCH((gemm_pk_split_kernel<2, 2, EPI_DEQUANT_RES>), grid, block, pk_split_lds_bytes(2, 2), s, a);
+        else TL_KLAUNCH((gemm_pk_split_kernel<2, 2, EPI_DEQUANT>), grid, block, pk_split_lds_bytes(2, 2), s, a);
+    }
+    return hipGetLastError();
+}
+
+hipError_t init_gemm_pk_kernels() {
+    const void* fns[] = {(const void*)gemm_pk_split_kernel<1, 5, EPI_DEQUANT>,
+                         (const void*)gemm_pk_split_kernel<1, 5, EPI_DEQUANT_RES>,
+                         (const void*)gemm_pk_split_kernel<2, 2, EPI_DEQUANT>,
+                         (const void*)gemm_pk_split_kernel<2, 2, EPI_DEQUANT_RES>, (const void*)gemm_pk_glu_kernel<1>,
+                         (const void*)gemm_pk_glu_kernel<2>};
+    const size_t bytes[] = {pk_split_lds_bytes(1, 5), pk_split_lds_bytes(1, 5), pk_split_lds_bytes(2, 2),
+                            pk_split_lds_bytes(2, 2), pk_glu_lds_bytes(1), pk_glu_lds_bytes(2)};
+    for (int i = 0; i < 6; i++) {
+        const hipError_t e = hipFuncSetAttribute(fns[i], hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes[i]);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 }  // namespace tl

@@ -107,16 +107,21 @@ struct GemmArgs {
     const int8_t* wp;         // packed copy of w (MFMA operand blocks, pack_weights_kernel) or null
     const int8_t* wp2;        // packed copy of w2
     unsigned long long* key;  // EPI_ARGMAX: [N / 32 tiles][M] best key of each tile and row
+    const int8_t* ap;         // A in MFMA operand blocks (rows padded to gemm_pk_row_pad()) for
+                              // launch_gemm_pk, or null
 };
 
 // ---- launchers (tl_kernels.hip) ------------------------------------------
+// packed: q is written in the packed GEMM operand layout (launch_gemm_pk)
+// instead of row-major; needs n % 64 == 0 and n <= 6144 (else invalid value)
 hipError_t launch_rmsnorm_quant(hipStream_t s, const float* x, const float* g, int32_t rows,
                                 int32_t n, float eps, PwPlan plan, float* y, int8_t* q,
-                                double* scales);
+                                double* scales, bool packed = false);
 // zero: optional [rows][zero_n] int32 buffer (zero_n % 4 == 0, 16-byte
 // aligned) each row's workgroup clears after quantizing
 hipError_t launch_quantize_rows(hipStream_t s, const float* x, int32_t rows, int32_t n,
-                                int8_t* q, double* scales, int32_t* zero = nullptr, int32_t zero_n = 0);
+                                int8_t* q, double* scales, int32_t* zero = nullptr, int32_t zero_n = 0,
+                                bool packed = false);
 
 // RMSNorm row prologue that first finishes a K-sliced small-M GEMM with a
 // residual epilogue: its integer sums acc (EPI_ACC, rows x n) are dequantized
@@ -279,6 +284,15 @@ hipError_t launch_requant_q16(hipStream_t s, const int32_t* acc, const uint32_t*
 hipError_t persist_occupancy(int32_t d, int32_t f, size_t lds, int* blocks_per_cu);
 
 hipError_t launch_gemm32(hipStream_t s, int epi, const GemmArgs& a, int32_t splits, int32_t cfg);
+// prefill GEMM on packed A (a.ap) and packed weights (a.wp, a.wp2): DEQUANT,
+// DEQUANT_RES or GLU where gemm_pk_supported(); packed A holds row r's 16-byte
+// piece p (K bytes [16 p, 16 p + 16)) at byte ((r / 32) (K / 32) + p / 2) 1024 +
+// ((p % 2) 32 + r % 32) 16, rows padded to a multiple of gemm_pk_row_pad()
+bool gemm_pk_supported(int epi, int32_t m, int32_t n, int32_t k);
+int32_t gemm_pk_row_pad();
+// glu_tn: GLU output tiles of 128 x 32 (1) or 128 x 64 (2) columns of each matrix
+hipError_t launch_gemm_pk(hipStream_t s, int epi, const GemmArgs& a, int32_t glu_tn);
+hipError_t init_gemm_pk_kernels();
 hipError_t launch_gemv_fused(hipStream_t s, int pro, int epi, const GemvArgs& a);
 // Q|K|V rows as the integer sums of a K-sliced GEMM with its dequantization
 // scales (batched decode; the grouped attention kernel only)

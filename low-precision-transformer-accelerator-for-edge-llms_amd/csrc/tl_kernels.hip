@@ -86,14 +86,16 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const float* __restr
 // the same two row operations for rows of width n <= 1024 KCH, n % 64 == 0,
 // 16-byte aligned, one workgroup per row: float4 loads, the decode GEMV
 // prologues (identical arithmetic: NumPy pairwise tree, per-row scale), and
-// 16-byte stores of the INT8 row.  With `zero`, the workgroup also clears
-// zero_n int32 of its row of that buffer (integer sums that the kernels
-// before it have consumed, zero again for the next K-sliced GEMM).
+// 16-byte stores of the INT8 row (row-major, or with pk in the packed GEMM
+// operand layout: piece p of row r at ((r / 32) (n / 32) + p / 2) 1024 +
+// ((p % 2) 32 + r % 32) 16).  With `zero`, the workgroup also clears zero_n
+// int32 of its row of that buffer (integer sums that the kernels before it
+// have consumed, zero again for the next K-sliced GEMM).
 template <int PRO, int KCH>
 __global__ __launch_bounds__(kNT) void rows_prologue_kernel(const float* __restrict__ x, const float* __restrict__ g,
                                                            int32_t n, float eps, PwPlan plan, int8_t* __restrict__ q,
                                                            double* __restrict__ scales, int32_t* __restrict__ zero,
-                                                           int32_t zero_n) {
+                                                           int32_t zero_n, int32_t pk) {
     __shared__ __align__(16) int8_t xs8[KCH * 1024];
     __shared__ __align__(16) float sq[PRO == PRO_RMSNORM ? KCH * 1024 : 4];
     __shared__ __align__(16) float part[PRO == PRO_RMSNORM ? 8 * 64 : 4];
@@ -111,8 +113,14 @@ __global__ __launch_bounds__(kNT) void rows_prologue_kernel(const float* __restr
     }
     if (PRO == PRO_QUANT) prologue_quant<KCH>(xv, n, xs8, red, &xscale);
     else prologue_rmsnorm<KCH>(xv, gv, n, eps, plan, sq, part, xs8, red, &xscale);
-    int8_t* qr = q + (int64_t)row * n;
-    for (int o = tid * 16; o < n; o += kNT * 16) *(v4i*)(qr + o) = *(const v4i*)(xs8 + o);
+    if (pk) {
+        int8_t* qt = q + (int64_t)(row >> 5) * (n >> 5) * 1024 + (row & 31) * 16;
+        for (int o = tid * 16; o < n; o += kNT * 16)
+            *(v4i*)(qt + (o >> 5) * 1024 + ((o >> 4) & 1) * 512) = *(const v4i*)(xs8 + o);
+    } else {
+        int8_t* qr = q + (int64_t)row * n;
+        for (int o = tid * 16; o < n; o += kNT * 16) *(v4i*)(qr + o) = *(const v4i*)(xs8 + o);
+    }
     if (tid == 0) scales[row] = xscale;
     if (zero)
         for (int i = tid * 4; i < zero_n; i += kNT * 4) *(v4i*)(zero + (int64_t)row * zero_n + i) = (v4i){0, 0, 0, 0};
@@ -121,9 +129,10 @@ __global__ __launch_bounds__(kNT) void rows_prologue_kernel(const float* __restr
 template <int PRO>
 static hipError_t launch_rows_prologue(hipStream_t s, const float* x, const float* g, int32_t rows, int32_t n,
                                        float eps, PwPlan plan, int8_t* q, double* scales, int32_t* zero = nullptr,
-                                       int32_t zero_n = 0) {
+                                       int32_t zero_n = 0, bool packed = false) {
     const dim3 grid(rows), block(kNT);
-#define TL_RPL(C) TL_KLAUNCH((rows_prologue_kernel<PRO, C>), grid, block, 0, s, x, g, n, eps, plan, q, scales, zero, zero_n)
+    const int32_t pk = packed ? 1 : 0;
+#define TL_RPL(C) TL_KLAUNCH((rows_prologue_kernel<PRO, C>), grid, block, 0, s, x, g, n, eps, plan, q, scales, zero, zero_n, pk)
     switch ((n + 1023) / 1024) {
         case 1: TL_RPL(1); break;
         case 2: TL_RPL(2); break;
@@ -1382,22 +1391,24 @@ static inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b)
 
 hipError_t launch_rmsnorm_quant(hipStream_t s, const float* x, const float* g, int32_t rows,
                                 int32_t n, float eps, PwPlan plan, float* y, int8_t* q,
-                                double* scales) {
+                                double* scales, bool packed) {
     if (rows <= 0) return hipSuccess;
     if (!y && plan.n_leaves <= 64 && rows_fast_ok(x, g, q, n))
-        return launch_rows_prologue<PRO_RMSNORM>(s, x, g, rows, n, eps, plan, q, scales);
+        return launch_rows_prologue<PRO_RMSNORM>(s, x, g, rows, n, eps, plan, q, scales, nullptr, 0, packed);
+    if (packed) return hipErrorInvalidValue;
     const size_t lds = sizeof(float) * ((size_t)2 * n + 10 * (size_t)plan.n_leaves + 16);
     TL_KLAUNCH(rmsnorm_quant_kernel, dim3(rows), dim3(256), lds, s, x, g, n, eps, plan, y, q, scales);
     return hipGetLastError();
 }
 
 hipError_t launch_quantize_rows(hipStream_t s, const float* x, int32_t rows, int32_t n, int8_t* q,
-                                double* scales, int32_t* zero, int32_t zero_n) {
+                                double* scales, int32_t* zero, int32_t zero_n, bool packed) {
     if (rows <= 0) return hipSuccess;
-    if (zero && (zero_n <= 0 || zero_n % 4 || (uintptr_t)zero % 16 || !rows_fast_ok(x, nullptr, q, n)))
-        return hipErrorInvalidValue;
+    if ((zero || packed) && !rows_fast_ok(x, nullptr, q, n)) return hipErrorInvalidValue;
+    if (zero && (zero_n <= 0 || zero_n % 4 || (uintptr_t)zero % 16)) return hipErrorInvalidValue;
     if (rows_fast_ok(x, nullptr, q, n))
-        return launch_rows_prologue<PRO_QUANT>(s, x, nullptr, rows, n, 0.0f, PwPlan{8, 1}, q, scales, zero, zero_n);
+        return launch_rows_prologue<PRO_QUANT>(s, x, nullptr, rows, n, 0.0f, PwPlan{8, 1}, q, scales, zero, zero_n,
+                                               packed);
     TL_KLAUNCH(quantize_rows_kernel<false>, dim3(rows), dim3(256), 0, s, x, n, q, (void*)scales);
     return hipGetLastError();
 }

@@ -184,6 +184,9 @@ struct tl_handle {
     unsigned* perr = nullptr;
     int32_t* pstatus = nullptr;
     int gemm_cfg = -1;                    // < 0: choose the MFMA tile configuration per shape
+    bool prefill_pk = true;               // prefill GEMMs on packed A and weights (launch_gemm_pk) where the
+                                          // shapes allow (TL_PREFILL_PACKED=0 turns it off)
+    int pk_glu_tn = 1;                    // their GLU tile: 128 x 32 (1) or 128 x 64 (2) columns (TL_PK_GLU_TN)
     std::vector<hipGraphExec_t> graphs;   // captured batch-1 decode step per sequence
     std::vector<hipGraphExec_t> batch_graphs;   // captured batched decode step, by batch size
 
@@ -381,6 +384,12 @@ int32_t run_gemm(tl_handle* h, int epi, GemmArgs a, int kclass, const FixedScrat
     const int nb = epi == EPI_GLU ? 2 : 1;
     const bool prof_ok = fx == nullptr;   // profiling events are allocations
     const double bytes = (double)a.m * a.k + (double)nb * a.n * a.k + (double)a.m * a.n * 4.0;
+    if (a.ap) {
+        // A was written in the packed operand layout for this GEMM
+        Prof p(h, kclass, bytes, prof_ok);
+        TL_LAUNCH(h, launch_gemm_pk(h->stream, epi, a, h->pk_glu_tn));
+        return TL_OK;
+    }
     if (a.m >= 64) {
         // 32x32x32 MFMA tiles: the 64 x 64 block-tiled kernel with 128-byte K
         // stages (cfg 8) measured fastest at M = 512; K not a multiple of 128
@@ -457,7 +466,7 @@ int32_t run_gemm(tl_handle* h, int epi, GemmArgs a, int kclass, const FixedScrat
 int32_t linear(tl_handle* h, int epi, int rows, const int8_t* x8, const double* xs, const int8_t* w,
                const float* ws, const int8_t* w2, const float* ws2, int32_t n, int32_t k,
                const float* residual, float* y, int kclass, const int8_t* wp = nullptr,
-               const int8_t* wp2 = nullptr) {
+               const int8_t* wp2 = nullptr, bool a_packed = false) {
     if (rows == 1) {
         GemvArgs g{};
         g.w = w; g.w2 = w2; g.ws = ws; g.ws2 = ws2; g.x = x8; g.xs = xs;
@@ -470,6 +479,7 @@ int32_t linear(tl_handle* h, int epi, int rows, const int8_t* x8, const double* 
     GemmArgs a{};
     a.a = x8; a.w = w; a.w2 = w2; a.as = xs; a.ws = ws; a.ws2 = ws2;
     a.residual = residual; a.y = y; a.m = rows; a.n = n; a.k = k; a.wp = wp; a.wp2 = wp2;
+    a.ap = a_packed ? x8 : nullptr;
     // multi-row GEMMs keep their role's class (Q|K|V, O, gate/up, down, LM head)
     return run_gemm(h, epi, a, kclass);
 }
@@ -614,9 +624,20 @@ static int32_t discard_pending_sums(tl_handle* h) {
     return TL_OK;
 }
 
-// RMSNorm + quantization of the rows of h->x into h->a8 / h->as, first adding
-// a pending down projection's sums from h->racc (launch_rows_fold)
-static int32_t rows_rmsnorm(tl_handle* h, int32_t rows, const float* g) {
+// prefill rows of this layer run their four GEMMs on packed operands: the
+// row kernels then write h->a8 in the packed layout those GEMMs read
+static bool prefill_packed(const tl_handle* h, const LayerDev& L, int32_t rows) {
+    const int D = h->D, F = h->F, QKV = h->QKV;
+    return h->prefill_pk && h->gemm_cfg < 0 && rows >= 64 && L.wqkv_p && L.wo_p && L.wg_p && L.wu_p && L.wd_p &&
+           D % 64 == 0 && F % 64 == 0 && D <= 6144 && F <= 6144 && h->plan.n_leaves <= 64 &&
+           gemm_pk_supported(EPI_DEQUANT, rows, QKV, D) && gemm_pk_supported(EPI_DEQUANT_RES, rows, D, D) &&
+           gemm_pk_supported(EPI_GLU, rows, F, D) && gemm_pk_supported(EPI_DEQUANT_RES, rows, D, F);
+}
+
+// RMSNorm + quantization of the rows of h->x into h->a8 / h->as (in the packed
+// GEMM operand layout with pk), first adding a pending down projection's sums
+// from h->racc (launch_rows_fold)
+static int32_t rows_rmsnorm(tl_handle* h, int32_t rows, const float* g, bool pk = false) {
     if (h->racc_res_ws) {
         FoldArgs f{};
         f.x = h->x; f.acc = h->racc; f.as = h->as; f.ws = h->racc_res_ws; f.g = g;
@@ -630,7 +651,8 @@ static int32_t rows_rmsnorm(tl_handle* h, int32_t rows, const float* g) {
         return TL_OK;
     }
     Prof p(h, TL_K_NORM, (double)rows * h->D * 9.0);
-    TL_LAUNCH(h, launch_rmsnorm_quant(h->stream, h->x, g, rows, h->D, h->cfg.rms_eps, h->plan, nullptr, h->a8, h->as));
+    TL_LAUNCH(h, launch_rmsnorm_quant(h->stream, h->x, g, rows, h->D, h->cfg.rms_eps, h->plan, nullptr, h->a8, h->as,
+                                      pk));
     return TL_OK;
 }
 
@@ -646,15 +668,16 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
     const int D = h->D, F = h->F, KVD = h->KVD, QKV = h->QKV;
     const bool ks = decode && kslice_ok(h, L, rows);
     const bool qks = ks && qkv_kslice_ok(h, L, rows, max_t);
+    const bool pk = !decode && prefill_packed(h, L, rows);   // h->a8 in the packed GEMM operand layout
     int32_t r;
     if (!ks && (r = discard_pending_sums(h))) return r;
-    if ((r = rows_rmsnorm(h, rows, L.g_in))) return r;
+    if ((r = rows_rmsnorm(h, rows, L.g_in, pk))) return r;
     if (qks) {
         // Q|K|V (K = D) K-sliced over the chip: the attention kernel
         // dequantizes the integer sums it reads from h->qacc
         if ((r = linear_acc(h, rows, L.wqkv_p, QKV, D, TL_K_QKV, h->qacc, &h->qacc_clean))) return r;
     } else if ((r = linear(h, EPI_DEQUANT, rows, h->a8, h->as, L.wqkv, L.sqkv, nullptr, nullptr, QKV, D, nullptr, h->qkv,
-                           TL_K_QKV, L.wqkv_p))) {
+                           TL_K_QKV, L.wqkv_p, nullptr, pk))) {
         return r;
     }
     if (decode) {
@@ -677,22 +700,23 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
         // with the Q|K|V sums consumed, this kernel also clears them
         Prof p(h, TL_K_NORM, (double)rows * D * 5.0 + (qks ? (double)rows * QKV * 4.0 : 0.0));
         TL_LAUNCH(h, launch_quantize_rows(h->stream, h->att, rows, D, h->a8, h->as, qks ? h->qacc : nullptr,
-                                          qks ? QKV : 0));
+                                          qks ? QKV : 0, pk));
         if (qks) h->qacc_clean = true;
     }
     if ((r = linear(h, EPI_DEQUANT_RES, rows, h->a8, h->as, L.wo, L.so, nullptr, nullptr, D, D, h->x, h->x, TL_K_O,
-                    L.wo_p)))
+                    L.wo_p, nullptr, pk)))
         return r;
     {
         Prof p(h, TL_K_NORM, (double)rows * D * 9.0);
-        TL_LAUNCH(h, launch_rmsnorm_quant(h->stream, h->x, L.g_post, rows, D, c.rms_eps, h->plan, nullptr, h->a8, h->as));
+        TL_LAUNCH(h, launch_rmsnorm_quant(h->stream, h->x, L.g_post, rows, D, c.rms_eps, h->plan, nullptr, h->a8, h->as,
+                                          pk));
     }
     if ((r = linear(h, EPI_GLU, rows, h->a8, h->as, L.wg, L.sg, L.wu, L.su, F, D, nullptr, h->hid, TL_K_GLU, L.wg_p,
-                    L.wu_p)))
+                    L.wu_p, pk)))
         return r;
     {
         Prof p(h, TL_K_NORM, (double)rows * F * 5.0);
-        TL_LAUNCH(h, launch_quantize_rows(h->stream, h->hid, rows, F, h->a8, h->as));
+        TL_LAUNCH(h, launch_quantize_rows(h->stream, h->hid, rows, F, h->a8, h->as, nullptr, 0, pk));
     }
     if (ks) {
         // the down GEMM (K = F) K-sliced over the chip: its integer sums wait
@@ -702,7 +726,7 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
         return TL_OK;
     }
     if ((r = linear(h, EPI_DEQUANT_RES, rows, h->a8, h->as, L.wd, L.sd, nullptr, nullptr, D, F, h->x, h->x, TL_K_DOWN,
-                    L.wd_p)))
+                    L.wd_p, nullptr, pk)))
         return r;
     return TL_OK;
 }
@@ -997,7 +1021,7 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
     const int R = h->max_rows, D = h->D, F = h->F;
     const int KF = std::max(D, F);
     if ((e = dalloc(h, &h->x, (size_t)R * D)) || (e = dalloc(h, &h->qkv, (size_t)R * h->QKV)) ||
-        (e = dalloc(h, &h->a8, (size_t)R * KF)) || (e = dalloc(h, &h->as, (size_t)R)) ||
+        (e = dalloc(h, &h->a8, (size_t)((R + gemm_pk_row_pad() - 1) / gemm_pk_row_pad()) * gemm_pk_row_pad() * KF)) || (e = dalloc(h, &h->as, (size_t)R)) ||
         (e = dalloc(h, &h->q8, (size_t)R * D)) || (e = dalloc(h, &h->qs, (size_t)R)) ||
         (e = dalloc(h, &h->att, (size_t)R * D)) || (e = dalloc(h, &h->hid, (size_t)R * F)) ||
         (e = dalloc(h, &h->logits, (size_t)max_seqs * c.vocab)) || (e = dalloc(h, &h->row_seq, (size_t)R)) || (e = dalloc(h, &h->tile_ctr, (size_t)kSkinnyTiles)) ||
@@ -1066,12 +1090,15 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
     if ((e = init_kernels())) return bad(e);
     if ((e = init_decode_kernels())) return bad(e);
     if ((e = init_prefill_kernels())) return bad(e);
+    if ((e = init_gemm_pk_kernels())) return bad(e);
     if ((e = init_skinny_kernels())) return bad(e);
     if (const char* env = std::getenv("TL_NO_GRAPHS")) h->use_graphs = env[0] == '0';
     if (const char* env = std::getenv("TL_PERSIST")) h->use_persist = env[0] == '1';
     if (const char* env = std::getenv("TL_BATCH_HPW")) h->batch_hpw = std::atoi(env) == 8 ? 8 : 1;
     if (const char* env = std::getenv("TL_GEMM_SMALL")) h->gemm_small = std::atoi(env);
     if (const char* env = std::getenv("TL_GEMM_CFG")) h->gemm_cfg = std::atoi(env);
+    if (const char* env = std::getenv("TL_PREFILL_PACKED")) h->prefill_pk = env[0] != '0';
+    if (const char* env = std::getenv("TL_PK_GLU_TN")) h->pk_glu_tn = std::atoi(env) == 2 ? 2 : 1;
     if (const char* env = std::getenv("TL_BATCH_KSLICE")) h->batch_kslice = env[0] != '0';
     if (const char* env = std::getenv("TL_BATCH_QKV_KSLICE")) h->qkv_kslice = env[0] != '0';
     if (const char* env = std::getenv("TL_ROWS32_WAVES")) h->rows32_waves = std::atoi(env);

@@ -405,6 +405,35 @@ def test_prefill_512_tinyllama_shape():
     eng.close()
 
 
+@pytest.mark.parametrize("packed", ["1", "0"], ids=["packed_operands", "row_major"])
+@pytest.mark.parametrize("n", [64, 100, 300])
+def test_prefill_lengths_tinyllama_shape(n, packed, monkeypatch):
+    """Prefills whose length is not a multiple of the GEMM row tiles (the
+    packed-operand GEMMs pad A to 128 rows; TL_PREFILL_PACKED=0 runs the
+    row-major kernels) on a 2-layer TinyLlama-shape model: next token, its
+    logit and every K/V row equal token-by-token decode in the oracle."""
+    monkeypatch.setenv("TL_PREFILL_PACKED", packed)
+    cfg = dict(oracle.TINYLLAMA_CFG, n_layers=2, vocab=4096)
+    m = oracle.synthetic_model(cfg, seed=40 + n)
+    prompt = np.random.default_rng(n).integers(0, cfg["vocab"], n).astype(np.int32)
+    eng = engine_for(m)
+    tok, lg = eng.prefill(prompt)
+    orc = oracle.Oracle(m)
+    kc, vc = m.new_cache()
+    x = None
+    for i, t in enumerate(prompt):
+        x = orc.embed(int(t))
+        for layer in range(cfg["n_layers"]):
+            x = orc.decode_row(layer, i, x, kc, vc)
+    assert (tok, lg) == orc.lm_head(x)
+    for layer in range(cfg["n_layers"]):
+        for g in range(cfg["n_kv_heads"]):
+            k, v = eng.kv_read(0, layer, g, 0, n)
+            assert_bits_equal(k, kc[layer, g, :n], f"K layer {layer} head {g}")
+            assert_bits_equal(v, vc[layer, g, :n], f"V layer {layer} head {g}")
+    eng.close()
+
+
 @DECODE_PATHS
 def test_generate_tinyllama_shape_matches_oracle(persist, monkeypatch):
     """Greedy generation on a 2-layer TinyLlama-shape model (hidden 2048, FFN
