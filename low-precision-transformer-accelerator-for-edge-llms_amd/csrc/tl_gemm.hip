@@ -586,6 +586,13 @@ TL_DEV void pk_wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N_) : "memory");
 }
 
+// the same wait, taking the four registers of an asm-issued fragment load as
+// operands: whatever reads them is ordered after the wait
+template <int N_>
+TL_DEV void pk_wait_regs(v4i* r) {
+    asm volatile("s_waitcnt vmcnt(%4)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]) : "n"(N_));
+}
+
 // (1) one-matrix GEMMs (DEQUANT, DEQUANT_RES), K a multiple of 512: the 4
 // wavefronts of a workgroup each compute the whole (32 TM) x (32 TN) tile
 // over their own quarter of K, both operands straight into registers
@@ -736,10 +743,20 @@ __global__ __launch_bounds__(256) void gemm_pk_glu_kernel(GemmArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int mt = blockIdx.y * 4 + wave, nt0 = blockIdx.x * TN;
     const int8_t* ab = a.ap + lane * 16;
+    // The A fragment loads are issued from inline asm and waited for by
+    // explicit vmcnt counts that follow the issue order below: the compiler,
+    // seeing register loads and global -> LDS loads in flight together, would
+    // wait for all of them before each stage's MFMAs.  A wait takes the
+    // registers it guards as operands, so nothing reads them before it; the
+    // LDS fragment reads are asm too, so the compiler has no LDS read to
+    // order after the global -> LDS loads.
     v4i ra[2][4];
     auto a_load = [&](int set, int stage) {
 #pragma unroll
-        for (int q = 0; q < 4; q++) ra[set][q] = ld16(pk_block(ab, mt, stage * 4 + q, kc));
+        for (int q = 0; q < 4; q++)
+            asm volatile("global_load_dwordx4 %0, %1, off"
+                         : "=v"(ra[set][q])
+                         : "v"(pk_block(ab, mt, stage * 4 + q, kc)));
     };
     const int8_t* src[PWB];   // this stage's global -> LDS sources
 #pragma unroll
@@ -768,30 +785,37 @@ __global__ __launch_bounds__(256) void gemm_pk_glu_kernel(GemmArgs a) {
                 for (int j = 0; j < TN; j++)
                     acc[s][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ra[u][q], bq[(s * TN + j) * 4 + q], acc[s][j], 0, 0, 0);
     };
+    // issue order: B(0) A(0) B(1) A(1), then per stage kk: B(kk + 2) ... A(kk + 2).
+    // Stage kk: B(kk) is done when at most A(kk), B(kk + 1), A(kk + 1) remain
+    // (PWB + 8); after the barrier every wavefront's is, and every wavefront
+    // is past stage kk - 1, whose buffer takes B(kk + 2); A(kk) is done when
+    // at most B(kk + 1), A(kk + 1), B(kk + 2) remain (2 PWB + 4).
     b_issue(0, 0);
-    b_issue(1, 1);
     a_load(0, 0);
+    b_issue(1, 1);
     a_load(1, 1);
-    // stage kk: this wavefront's loads of the stage (issued two stages back)
-    // are done when at most stage kk + 1's (PWB weight + 4 A loads) remain;
-    // after the barrier every wavefront's are, and every wavefront is past
-    // stage kk - 1, whose buffer then takes stage kk + 2
     for (int k = 0; k < nk - 2; k += 2) {
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             const int kk = k + u;
-            pk_wait_vm<PWB + 4>();
+            pk_wait_vm<PWB + 8>();
             asm volatile("s_barrier" ::: "memory");
             b_issue(kk + 2, (kk + 2) % NS);
+            pk_wait_regs<2 * PWB + 4>(ra[u]);
             compute(kk, u);
             a_load(u, kk + 2);
         }
     }
-    pk_wait_vm<PWB + 4>();
+    // the last two stages issue nothing: B(nk - 2) waits on A(nk - 2),
+    // B(nk - 1), A(nk - 1); A(nk - 2) on B(nk - 1), A(nk - 1); B(nk - 1) on
+    // A(nk - 1); A(nk - 1) on nothing
+    pk_wait_vm<PWB + 8>();
     asm volatile("s_barrier" ::: "memory");
+    pk_wait_regs<PWB + 4>(ra[0]);
     compute(nk - 2, 0);
-    pk_wait_vm<0>();
+    pk_wait_vm<4>();
     asm volatile("s_barrier" ::: "memory");
+    pk_wait_regs<0>(ra[1]);
     compute(nk - 1, 1);
     const int rb = mt * 32 + 4 * (lane >> 5);
     double sx[16];
