@@ -601,14 +601,125 @@ TL_DEV void pk_wait_regs(v4i* r) {
 // and wavefront w finishes blocks w, w + 4, ... of the tile with the epilogue
 // arithmetic of every other GEMM here.  Tiles: 64 x 64 (TM = TN = 2) for O and
 // down (256 workgroups at M = 512), 32 x 160 (TM = 1, TN = 5) for Q|K|V
-// (N = 2560: 256 workgroups where 64 x 64 needs 320).
+// (N = 2560: 256 workgroups where 64 x 64 needs 320); 64 x 64 for the
+// prefill Q|K|V with qkv_post's work in the epilogue (EPI_QKV_ROPE, one head
+// per tile).  The epilogue's operands are loaded right after the first
+// operand loads, so they arrive during the main loop.
 constexpr int kPkSplitPD = 4;
 
 static size_t pk_split_lds_bytes(int tm, int tn) { return (size_t)4 * tm * tn * 16 * 64 * sizeof(int); }
 
+// EPI_QKV_ROPE epilogue of a 64 x 64 tile (one head of Q, K or V): wavefront
+// w takes accumulator registers 8 (w % 2) .. 8 (w % 2) + 7 (8 rows per lane) of
+// row block w / 2 in both column blocks, so a lane holds dimensions d and
+// d + 32 of its rows.  The
+// arithmetic is qkv_post_kernel's: x = f32(acc) f32(sx sw), rotated
+// x_d c_d + (-x_{d+32}) s_d and x_{d+32} c_{d+32} + x_d s_{d+32} (two products
+// and a sum, no fused multiply-add), K and V bytes sat(rne(x / s)).  Its
+// operands (row scales, positions, sequences, cos / sin) are loaded before
+// the LDS reduction (qkv_rope_operands, qkv_rope_tables).
+struct QkvRopeOps {   // the 8 registers (rows) of the wavefront's row block
+    double sx[8];
+    int pos[8], seq[8];
+    float c0[8], s0[8], c1[8], s1[8];
+    float sw0, sw1, sc;
+    int region, g, n0, rb, e0, i;
+};
+
+TL_DEV void qkv_rope_operands(const GemmArgs& a, const QkvRopeArgs& f, int mt0, int nt0, int wave, int lane,
+                              QkvRopeOps& o) {
+    constexpr int NE = 8;
+    const int d = lane & 31, D = f.n_heads * kHeadDim, KVD = f.n_kv * kHeadDim;
+    o.i = wave >> 1;
+    o.e0 = (wave & 1) * 8;
+    o.n0 = nt0 * 32;
+    o.region = o.n0 < D ? 0 : (o.n0 < D + KVD ? 1 : 2);   // Q, K, V (uniform)
+    o.g = o.region == 1 ? (o.n0 - D) >> 6 : (o.n0 - D - KVD) >> 6;
+    o.rb = (mt0 + o.i) * 32 + 4 * (lane >> 5);
+    o.sw0 = a.ws[o.n0 + d];
+    o.sw1 = a.ws[o.n0 + 32 + d];
+    o.sc = o.region == 1 ? f.kv_sk[f.layer * f.n_kv + o.g] : (o.region == 2 ? f.kv_sv[f.layer * f.n_kv + o.g] : 1.0f);
+#pragma unroll
+    for (int ee = 0; ee < NE; ee++) {
+        const int e = o.e0 + ee, m = min(o.rb + 8 * (e >> 2) + (e & 3), a.m - 1);
+        o.sx[ee] = a.as[m];
+        o.pos[ee] = f.rm.pos[m];
+        o.seq[ee] = f.rm.seq[m];
+    }
+}
+
+// the cos / sin entries of the rows' positions (after qkv_rope_operands)
+TL_DEV void qkv_rope_tables(const QkvRopeArgs& f, int lane, QkvRopeOps& o) {
+    constexpr int NE = 8;
+    const int d = lane & 31;
+    if (o.region != 2) {
+#pragma unroll
+        for (int ee = 0; ee < NE; ee++) {
+            const int64_t t = (int64_t)min(max(o.pos[ee], 0), f.kv.max_pos - 1) * kHeadDim;
+            o.c0[ee] = f.cosb[t + d];
+            o.s0[ee] = f.sinb[t + d];
+            o.c1[ee] = f.cosb[t + d + 32];
+            o.s1[ee] = f.sinb[t + d + 32];
+        }
+    }
+}
+
+TL_DEV void qkv_rope_epilogue(const GemmArgs& a, const QkvRopeArgs& f, const QkvRopeOps& o, const int* red,
+                              int lane) {
+    constexpr int NBLK = 4, NE = 8;
+    const int d = lane & 31, D = f.n_heads * kHeadDim;
+#pragma unroll
+    for (int ee = 0; ee < NE; ee++) {
+        const int e = o.e0 + ee, m = o.rb + 8 * (e >> 2) + (e & 3);
+        int a0 = 0, a1 = 0;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            a0 += red[((w * NBLK + o.i * 2) * 16 + e) * 64 + lane];
+            a1 += red[((w * NBLK + o.i * 2 + 1) * 16 + e) * 64 + lane];
+        }
+        const float lo = (float)a0 * deq_mult(o.sx[ee], o.sw0), hi = (float)a1 * deq_mult(o.sx[ee], o.sw1);
+        const int pos = o.pos[ee];
+        const bool valid = m < a.m && pos >= 0 && pos < f.kv.max_pos;   // uniform per half-wavefront
+        if (o.region == 2) {
+            if (valid) {
+                const int64_t pl = f.kv.plane(o.seq[ee], f.layer, o.g);
+                f.kv.v[pl + KvGeom::v_off(pos, d)] = sat_i8(__builtin_rintf(__fdiv_rn(lo, o.sc)));
+                f.kv.v[pl + KvGeom::v_off(pos, d + 32)] = sat_i8(__builtin_rintf(__fdiv_rn(hi, o.sc)));
+            }
+            continue;
+        }
+        const float rlo = (lo * o.c0[ee]) + ((-hi) * o.s0[ee]);
+        const float rhi = (hi * o.c1[ee]) + (lo * o.s1[ee]);
+        if (o.region == 1) {
+            if (valid) {
+                const int64_t pl = f.kv.plane(o.seq[ee], f.layer, o.g);
+                f.kv.k[pl + KvGeom::k_off(pos, d)] = sat_i8(__builtin_rintf(__fdiv_rn(rlo, o.sc)));
+                f.kv.k[pl + KvGeom::k_off(pos, d + 32)] = sat_i8(__builtin_rintf(__fdiv_rn(rhi, o.sc)));
+            }
+            continue;
+        }
+        if (m < a.m) {
+            f.q_out[(int64_t)m * D + o.n0 + d] = rlo;
+            f.q_out[(int64_t)m * D + o.n0 + d + 32] = rhi;
+        }
+        const float mx = half_max_f32(valid ? fmaxf(fabsf(rlo), fabsf(rhi)) : 0.0f);   // the row's 32 lanes
+        if (d == 0 && valid) atomicMax(f.q_max + (int64_t)m * 4, __float_as_uint(mx));
+    }
+}
+
+// operands of the DEQUANT(_RES) epilogue of the blocks wavefront w finishes
+// (w, w + 4, ...: NBW at most), loaded before the main loop
+template <int NBW, bool RES>
+struct SplitOps {
+    double sx[NBW][16];
+    float res[NBW][RES ? 16 : 1];
+    float sw[NBW];
+};
+
 template <int TM, int TN, int EPI>
-__global__ __launch_bounds__(256) void gemm_pk_split_kernel(GemmArgs a) {
-    constexpr int NF = TM + TN, PD = kPkSplitPD, NBLK = TM * TN;
+__global__ __launch_bounds__(256) void gemm_pk_split_kernel(GemmArgs a, QkvRopeArgs f) {
+    constexpr int NF = TM + TN, PD = kPkSplitPD, NBLK = TM * TN, NBW = (NBLK + 3) / 4;
+    constexpr bool RES = EPI == EPI_DEQUANT_RES;
     extern __shared__ __align__(16) int pk_red[];   // [4 waves][NBLK][16][64]
     const int kc = a.k >> 5, per = kc >> 2;        // chunks of each wavefront (a multiple of PD)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -648,37 +759,58 @@ __global__ __launch_bounds__(256) void gemm_pk_split_kernel(GemmArgs a) {
     }
 #pragma unroll
     for (int u = 0; u < PD; u++) mma(u);
+    // the epilogue's operands go out now (vector-memory waits complete in
+    // issue order, so earlier they would hold up the main loop) and arrive
+    // while the partial tiles pass through LDS.  Block b, lane l, register e
+    // is output row 8 (e / 4) + 4 (l / 32) + e % 4, column l % 32.
+    QkvRopeOps qo;
+    SplitOps<NBW, RES> so;
+    if constexpr (EPI == EPI_QKV_ROPE) {
+        static_assert(TM == 2 && TN == 2, "one 64-row x one-head tile");
+        qkv_rope_operands(a, f, mt0, nt0, wave, lane, qo);
+    } else {
+#pragma unroll
+        for (int bw = 0; bw < NBW; bw++) {
+            const int b = min(wave + 4 * bw, NBLK - 1);
+            const int i = b / TN, j = b % TN, n = (nt0 + j) * 32 + (lane & 31);
+            const int rb = (mt0 + i) * 32 + 4 * (lane >> 5);
+            so.sw[bw] = a.ws[n];
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int m = min(rb + 8 * (e >> 2) + (e & 3), a.m - 1);
+                so.sx[bw][e] = a.as[m];
+                if constexpr (RES) so.res[bw][e] = a.residual[(int64_t)m * a.n + n];
+            }
+        }
+    }
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++)
 #pragma unroll
             for (int e = 0; e < 16; e++) pk_red[((wave * NBLK + i * TN + j) * 16 + e) * 64 + lane] = acc[i][j][e];
+    if constexpr (EPI == EPI_QKV_ROPE) qkv_rope_tables(f, lane, qo);
     __syncthreads();
-    // block b: lane l, register e is output row 8 (e / 4) + 4 (l / 32) + e % 4,
-    // column l % 32; all of a block's loads before its stores (y may be the
-    // residual, updated in place)
-    for (int b = wave; b < NBLK; b += 4) {
-        const int i = b / TN, j = b % TN;
-        const int n = (nt0 + j) * 32 + (lane & 31);
-        const int rb = (mt0 + i) * 32 + 4 * (lane >> 5);
-        const float sw = a.ws[n];
-        double sx[16];
-        float res[EPI == EPI_DEQUANT_RES ? 16 : 1];
+    if constexpr (EPI == EPI_QKV_ROPE) {
+        qkv_rope_epilogue(a, f, qo, pk_red, lane);
+        return;
+    }
+    // wavefront w finishes blocks w, w + 4, ... (y may be the residual, read
+    // above and written here in place)
 #pragma unroll
-        for (int e = 0; e < 16; e++) {
-            const int m = min(rb + 8 * (e >> 2) + (e & 3), a.m - 1);
-            sx[e] = a.as[m];
-            if (EPI == EPI_DEQUANT_RES) res[e] = a.residual[(int64_t)m * a.n + n];
-        }
+    for (int bw = 0; bw < NBW; bw++) {
+        const int b = wave + 4 * bw;
+        if (b >= NBLK) break;
+        const int i = b / TN, j = b % TN, n = (nt0 + j) * 32 + (lane & 31);
+        const int rb = (mt0 + i) * 32 + 4 * (lane >> 5);
 #pragma unroll
         for (int e = 0; e < 16; e++) {
             int sum = 0;
 #pragma unroll
             for (int w = 0; w < 4; w++) sum += pk_red[((w * NBLK + b) * 16 + e) * 64 + lane];
             const int m = rb + 8 * (e >> 2) + (e & 3);
-            const float v = (float)sum * deq_mult(sx[e], sw);
-            if (m < a.m) a.y[(int64_t)m * a.n + n] = EPI == EPI_DEQUANT_RES ? res[e] + v : v;
+            const float v = (float)sum * deq_mult(so.sx[bw][e], so.sw[bw]);
+            if (m < a.m) a.y[(int64_t)m * a.n + n] = RES ? so.res[bw][RES ? e : 0] + v : v;
         }
     }
 }
@@ -857,6 +989,7 @@ hipError_t launch_gemm_pk(hipStream_t s, int epi, const GemmArgs& a, int32_t glu
     if (!a.ap || !a.wp || !gemm_pk_supported(epi, a.m, a.n, a.k) || (epi == EPI_GLU && !a.wp2))
         return hipErrorInvalidValue;
     const dim3 block(256);
+    const QkvRopeArgs f{};
     if (epi == EPI_GLU) {
         if (glu_tn == 1)
             TL_KLAUNCH(gemm_pk_glu_kernel<1>, dim3(a.n / 32, (a.m + 127) / 128), block, pk_glu_lds_bytes(1), s, a);
@@ -866,13 +999,24 @@ hipError_t launch_gemm_pk(hipStream_t s, int epi, const GemmArgs& a, int32_t glu
     const bool res = epi == EPI_DEQUANT_RES;
     if (pk_split_narrow(a.m, a.n)) {
         const dim3 grid(a.n / 160, (a.m + 31) / 32);
-        if (res) TL_KLAUNCH((gemm_pk_split_kernel<1, 5, EPI_DEQUANT_RES>), grid, block, pk_split_lds_bytes(1, 5), s, a);
-        else TL_KLAUNCH((gemm_pk_split_kernel<1, 5, EPI_DEQUANT>), grid, block, pk_split_lds_bytes(1, 5), s, a);
+        if (res) TL_KLAUNCH((gemm_pk_split_kernel<1, 5, EPI_DEQUANT_RES>), grid, block, pk_split_lds_bytes(1, 5), s, a, f);
+        else TL_KLAUNCH((gemm_pk_split_kernel<1, 5, EPI_DEQUANT>), grid, block, pk_split_lds_bytes(1, 5), s, a, f);
     } else {
         const dim3 grid(a.n / 64, (a.m + 63) / 64);
-        if (res) TL_KLAUNCH((gemm_pk_split_kernel<2, 2, EPI_DEQUANT_RES>), grid, block, pk_split_lds_bytes(2, 2), s, a);
-        else TL_KLAUNCH((gemm_pk_split_kernel<2, 2, EPI_DEQUANT>), grid, block, pk_split_lds_bytes(2, 2), s, a);
+        if (res) TL_KLAUNCH((gemm_pk_split_kernel<2, 2, EPI_DEQUANT_RES>), grid, block, pk_split_lds_bytes(2, 2), s, a, f);
+        else TL_KLAUNCH((gemm_pk_split_kernel<2, 2, EPI_DEQUANT>), grid, block, pk_split_lds_bytes(2, 2), s, a, f);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_pk_qkv(hipStream_t s, const GemmArgs& a, const QkvRopeArgs& f) {
+    if (a.m <= 0) return hipSuccess;
+    const int D = f.n_heads * kHeadDim, KVD = f.n_kv * kHeadDim;
+    if (!a.ap || !a.wp || !f.q_out || !f.q_max || f.n_heads <= 0 || f.n_kv <= 0 || a.n != D + 2 * KVD ||
+        a.k % 512 || a.n % 64)
+        return hipErrorInvalidValue;
+    TL_KLAUNCH((gemm_pk_split_kernel<2, 2, EPI_QKV_ROPE>), dim3(a.n / 64, (a.m + 63) / 64), dim3(256),
+               pk_split_lds_bytes(2, 2), s, a, f);
     return hipGetLastError();
 }
 
@@ -881,10 +1025,11 @@ hipError_t init_gemm_pk_kernels() {
                          (const void*)gemm_pk_split_kernel<1, 5, EPI_DEQUANT_RES>,
                          (const void*)gemm_pk_split_kernel<2, 2, EPI_DEQUANT>,
                          (const void*)gemm_pk_split_kernel<2, 2, EPI_DEQUANT_RES>, (const void*)gemm_pk_glu_kernel<1>,
-                         (const void*)gemm_pk_glu_kernel<2>};
+                         (const void*)gemm_pk_glu_kernel<2>, (const void*)gemm_pk_split_kernel<2, 2, EPI_QKV_ROPE>};
     const size_t bytes[] = {pk_split_lds_bytes(1, 5), pk_split_lds_bytes(1, 5), pk_split_lds_bytes(2, 2),
-                            pk_split_lds_bytes(2, 2), pk_glu_lds_bytes(1), pk_glu_lds_bytes(2)};
-    for (int i = 0; i < 6; i++) {
+                            pk_split_lds_bytes(2, 2), pk_glu_lds_bytes(1), pk_glu_lds_bytes(2),
+                            pk_split_lds_bytes(2, 2)};
+    for (int i = 0; i < 7; i++) {
         const hipError_t e = hipFuncSetAttribute(fns[i], hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes[i]);
         if (e != hipSuccess) return e;
     }

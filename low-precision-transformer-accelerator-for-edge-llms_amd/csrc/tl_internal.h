@@ -60,6 +60,8 @@ enum GemvEpi : int {
     EPI_RAW = 5,          // acc only
     EPI_ACC = 6,          // acc[m][n] += the K slice's sum (integer atomic add; the row prologue that
                           // follows folds the sums and clears them)
+    EPI_QKV_ROPE = 7,     // prefill Q|K|V: dequantize, RoPE on Q and K, K / V quantized into the cache,
+                          // rotated Q out in float32 with its row maximum (launch_gemm_pk_qkv)
 };
 
 // activation prologue of the fused decode GEMV
@@ -161,9 +163,13 @@ hipError_t launch_qkv_post(hipStream_t s, const float* qkv, int32_t rows, int32_
                            KvGeom kv, int32_t layer, const float* kv_sk, const float* kv_sv,
                            int8_t* q8, double* q_scale, float* q_rot_out, bool append_kv = true);
 constexpr int kTileMaxKeys = 4096;   // context limit of launch_attention_tiles (LDS)
+// qf / qmax (optional, instead of q8 / q_scale): rotated Q rows in float32
+// ([rows][D]) and their maxima max|q| as float bits ([rows][4], element 0),
+// quantized by the kernel exactly as qkv_post quantizes them
 hipError_t launch_attention_tiles(hipStream_t s, const int8_t* q8, const double* q_scale, int32_t rows,
                                   int32_t n_heads, int32_t n_kv_heads, int32_t seq, int32_t pos0, KvGeom kv,
-                                  int32_t layer, const float* kv_sk, const float* kv_sv, float* out);
+                                  int32_t layer, const float* kv_sk, const float* kv_sv, float* out,
+                                  const float* qf = nullptr, const unsigned* qmax = nullptr);
 // Optional debug outputs of row 0 (the decode-step capture): INT32 scores and
 // INT8 probabilities of keys key0 .. key0 + n_keys - 1 per query head
 // ([n_heads][n_keys]) and the f32 score scale per query head.
@@ -289,6 +295,23 @@ hipError_t launch_gemm32(hipStream_t s, int epi, const GemmArgs& a, int32_t spli
 // piece p (K bytes [16 p, 16 p + 16)) at byte ((r / 32) (K / 32) + p / 2) 1024 +
 // ((p % 2) 32 + r % 32) 16, rows padded to a multiple of gemm_pk_row_pad()
 bool gemm_pk_supported(int epi, int32_t m, int32_t n, int32_t k);
+// the prefill Q|K|V GEMM with qkv_post's work in its epilogue (EPI_QKV_ROPE):
+// RoPE on Q and K at each row's position, K and V quantized with the static
+// per-head scales into the cache, rotated Q written to q_out ([M][D] float32)
+// and max|q| of each row folded into q_max[4 row] (float bits, atomic max;
+// zero beforehand).  Needs N = D + 2 KVD with D, KVD multiples of 64.
+struct QkvRopeArgs {
+    const float* cosb;
+    const float* sinb;
+    RowMap rm;
+    KvGeom kv;
+    int32_t layer, n_heads, n_kv;
+    const float* kv_sk;
+    const float* kv_sv;
+    float* q_out;
+    unsigned* q_max;
+};
+hipError_t launch_gemm_pk_qkv(hipStream_t s, const GemmArgs& a, const QkvRopeArgs& f);
 int32_t gemm_pk_row_pad();
 // glu_tn: GLU output tiles of 128 x 32 (1) or 128 x 64 (2) columns of each matrix
 hipError_t launch_gemm_pk(hipStream_t s, int epi, const GemmArgs& a, int32_t glu_tn);

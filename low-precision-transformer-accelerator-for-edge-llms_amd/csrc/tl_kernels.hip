@@ -896,10 +896,67 @@ struct AttnTileArgs {
     const float* kv_sv;
     double attn_scale;
     float* out;              // [rows][D]
+    const float* qf;         // or rotated Q in float32 [rows][D], quantized here
+    const unsigned* qmax;    // with qf: max|q| of each row as float bits [rows][4]
 };
+
+// Q fragments of a tile lane (row r, head h, K halves hi * 16 .. + 16 and
+// 32 + hi * 16 .. + 16), in three steps around the workgroup barrier that
+// follows the K and V loads.  From q8 the fragments are loaded directly.
+// From float32 Q the workgroup quantizes the tile once: thread t takes row
+// t / 8, dimensions 8 (t % 8) .. + 8, at the row's scale exactly as
+// qkv_post_kernel does (quant_scale of the row maximum, the correctly rounded
+// division of rn_div_prep / quant4; the fast form only when every lane's
+// divisor allows it, both give RN(q / s)), into a 32 x 64 byte LDS tile that
+// every wavefront then reads its fragments from.
+struct TileQ {
+    v4i qa0, qa1;
+    float4 x0, x1;
+    unsigned mx;
+};
+
+TL_DEV void tile_q_load(const AttnTileArgs& p, int r0, int nr, int h, int col, int hi, TileQ& q) {
+    const int D = p.n_heads * kHeadDim;
+    if (!p.qf) {
+        const int8_t* qrow = p.q8 + (int64_t)(r0 + min(col, nr - 1)) * D + h * kHeadDim + hi * 16;
+        q.qa0 = ld16(qrow);
+        q.qa1 = ld16(qrow + 32);
+        return;
+    }
+    const int r = r0 + min((int)threadIdx.x >> 3, nr - 1);   // rows past the tile's last: a stand-in, never stored
+    const float4* qr = (const float4*)(p.qf + (int64_t)r * D + h * kHeadDim + (threadIdx.x & 7) * 8);
+    q.x0 = qr[0];
+    q.x1 = qr[1];
+    q.mx = p.qmax[(int64_t)r * 4];
+}
+
+// before the barrier: quantize this thread's 8 values into qs8 ([32][64])
+TL_DEV void tile_q_quantize(const AttnTileArgs& p, TileQ& q, int8_t* qs8) {
+    if (!p.qf) return;
+    RnDiv dq;
+    dq.b = (float)quant_scale(__uint_as_float(q.mx));
+    dq.y = __fdiv_rn(1.0f, dq.b);
+    dq.fast = __all(fabsf(dq.b) >= 0x1p-64f && fabsf(dq.b) <= 0x1p64f);
+    const unsigned u0 = dq.fast ? quant4<true>(q.x0, dq) : quant4<false>(q.x0, dq);
+    const unsigned u1 = dq.fast ? quant4<true>(q.x1, dq) : quant4<false>(q.x1, dq);
+    *(uint2*)(qs8 + threadIdx.x * 8) = make_uint2(u0, u1);
+}
+
+// after the barrier: the lane's fragments out of qs8
+TL_DEV void tile_q_frags(const AttnTileArgs& p, const int8_t* qs8, int col, int hi, TileQ& q) {
+    if (!p.qf) return;
+    q.qa0 = *(const v4i*)(qs8 + col * 64 + hi * 16);
+    q.qa1 = *(const v4i*)(qs8 + col * 64 + 32 + hi * 16);
+}
+
+// the row's Q scale (GI:36-42) for the score dequantization
+TL_DEV double tile_q_scale(const AttnTileArgs& p, int r) {
+    return p.qf ? quant_scale(__uint_as_float(p.qmax[(int64_t)r * 4])) : p.q_scale[r];
+}
 
 __global__ __launch_bounds__(256) void attention_tile_kernel(AttnTileArgs p) {
     extern __shared__ __align__(16) int8_t tile_lds[];
+    __shared__ __align__(16) int8_t qs8[32 * 64];   // Q quantized by the workgroup (float32 Q input)
     __shared__ float scl[32], mrow[32], tot[32];
     __shared__ float wmax[4][32];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -920,11 +977,14 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(AttnTileArgs p) {
     const float sk = p.kv_sk[p.layer * p.n_kv + g], sv = p.kv_sv[p.layer * p.n_kv + g];
 
     // Q fragments (rows past the tile's last read a stand-in, never stored)
-    const int8_t* qrow = p.q8 + (int64_t)(r0 + min(col, nr - 1)) * D + h * kHeadDim + hi * 16;
-    const v4i qa0 = ld16(qrow), qa1 = ld16(qrow + 32);
-    if (tid < 32) scl[tid] = (float)((p.q_scale[r0 + min(tid, nr - 1)] * (double)sk) * p.attn_scale);
+    TileQ tq;
+    tile_q_load(p, r0, nr, h, col, hi, tq);
+    if (tid < 32) scl[tid] = (float)((tile_q_scale(p, r0 + min(tid, nr - 1)) * (double)sk) * p.attn_scale);
     for (int e = tid; e < 32 * 64; e += 256) accs[e] = 0;
+    tile_q_quantize(p, tq, qs8);
     __syncthreads();
+    tile_q_frags(p, qs8, col, hi, tq);
+    const v4i qa0 = tq.qa0, qa1 = tq.qa1;
     float rs[16];
     int rpos[16];
 #pragma unroll
@@ -1793,6 +1853,7 @@ hipError_t init_prefill_kernels() {
 template <int NB>
 __global__ __launch_bounds__(256) void attention_tile_reg_kernel(AttnTileArgs p) {
     extern __shared__ __align__(16) int8_t tile_lds[];
+    __shared__ __align__(16) int8_t qs8[32 * 64];   // Q quantized by the workgroup (float32 Q input)
     __shared__ float scl[32], tot[32];
     __shared__ float wmax[4][32];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1815,8 +1876,8 @@ __global__ __launch_bounds__(256) void attention_tile_reg_kernel(AttnTileArgs p)
     // every load first: Q, then K of this wavefront's blocks b = wave + 4 j
     // (two 32-key tiles each), then V of its 32-key chunks c = wave + 4 j
     // (block indices clamped inside the plane; surplus copies unused)
-    const int8_t* qrow = p.q8 + (int64_t)(r0 + min(col, nr - 1)) * D + h * kHeadDim + hi * 16;
-    const v4i qa0 = ld16(qrow), qa1 = ld16(qrow + 32);
+    TileQ tq;
+    tile_q_load(p, r0, nr, h, col, hi, tq);
     v4i kf[NB][2][2], vf[2 * NB][2];
 #pragma unroll
     for (int j = 0; j < NB; j++)
@@ -1834,9 +1895,12 @@ __global__ __launch_bounds__(256) void attention_tile_reg_kernel(AttnTileArgs p)
         vf[j][0] = ld16(vb);
         vf[j][1] = ld16(vb + 512);
     }
-    if (tid < 32) scl[tid] = (float)((p.q_scale[r0 + min(tid, nr - 1)] * (double)sk) * p.attn_scale);
+    if (tid < 32) scl[tid] = (float)((tile_q_scale(p, r0 + min(tid, nr - 1)) * (double)sk) * p.attn_scale);
     for (int e = tid; e < 32 * 64; e += 256) accs[e] = 0;
+    tile_q_quantize(p, tq, qs8);   // float32 Q quantized while the K and V loads are in flight
     __syncthreads();
+    tile_q_frags(p, qs8, col, hi, tq);
+    const v4i qa0 = tq.qa0, qa1 = tq.qa1;
     const float rs = scl[col];
     const int rpos = pos_first + col;
 
@@ -1956,14 +2020,16 @@ __global__ __launch_bounds__(256) void attention_tile_reg_kernel(AttnTileArgs p)
 // rows of one sequence at positions pos0 .. pos0 + rows - 1
 hipError_t launch_attention_tiles(hipStream_t s, const int8_t* q8, const double* q_scale, int32_t rows,
                                   int32_t n_heads, int32_t n_kv_heads, int32_t seq, int32_t pos0, KvGeom kv,
-                                  int32_t layer, const float* kv_sk, const float* kv_sv, float* out) {
+                                  int32_t layer, const float* kv_sk, const float* kv_sv, float* out,
+                                  const float* qf, const unsigned* qmax) {
     if (rows <= 0) return hipSuccess;
-    if (n_heads % n_kv_heads || pos0 < 0 || pos0 + rows > kv.max_pos || pos0 + rows > kTileMaxKeys)
+    if (n_heads % n_kv_heads || pos0 < 0 || pos0 + rows > kv.max_pos || pos0 + rows > kTileMaxKeys ||
+        (qf && !qmax) || (!qf && (!q8 || !q_scale)))
         return hipErrorInvalidValue;
     const int tpad = (pos0 + rows + 63) & ~63;
     const size_t lds = tile_lds_bytes(tpad);
     AttnTileArgs a{q8, q_scale, n_heads, n_kv_heads, rows, seq, pos0, layer, kv, kv_sk, kv_sv,
-                   1.0 / sqrt((double)kHeadDim), out};
+                   1.0 / sqrt((double)kHeadDim), out, qf, qmax};
     const dim3 grid(n_heads, (rows + 31) / 32), block(256);
     if (tpad <= 256) TL_KLAUNCH(attention_tile_reg_kernel<1>, grid, block, lds, s, a);
     else if (tpad <= 512) TL_KLAUNCH(attention_tile_reg_kernel<2>, grid, block, lds, s, a);

@@ -134,6 +134,9 @@ struct tl_handle {
                                   // by the attention kernel; zero between uses (the attention output's
                                   // quantization clears them)
     size_t qacc_cap = 0;          // int32 elements
+    unsigned* qmax = nullptr;     // [max_rows][4] prefill: max|q| of each rotated Q row (float bits, element 0)
+                                  // from the fused Q|K|V GEMM; zero between uses (the attention output's
+                                  // quantization clears them)
     unsigned* tile_ctr = nullptr;         // [kSkinnyTiles] arrival counters of the small-M GEMM, zero between launches
     size_t partial_cap = 0;       // int32 elements
 
@@ -169,6 +172,10 @@ struct tl_handle {
     bool qkv_kslice = true;               // batched decode: K-sliced Q|K|V GEMM whose sums the attention
                                           // kernel dequantizes (TL_BATCH_QKV_KSLICE=0 turns it off)
     bool qacc_clean = true;               // false from a Q|K|V EPI_ACC launch until qacc is cleared
+    bool qkv_fuse = true;                 // prefill on packed operands: qkv_post's work in the Q|K|V GEMM
+                                          // epilogue and Q quantized by the attention kernel
+                                          // (TL_PREFILL_QKV_FUSE=0 turns it off)
+    bool qmax_clean = true;               // false from a fused Q|K|V GEMM until qmax is cleared
     bool rows_one_seq = false;            // the uploaded rows are one sequence at rows_pos0 + r
     int32_t rows_seq = 0, rows_pos0 = 0;
     bool persist_ok = false;              // geometry and occupancy allow it
@@ -621,6 +628,10 @@ static int32_t discard_pending_sums(tl_handle* h) {
         TL_LAUNCH(h, launch_fill_u32(h->stream, (unsigned*)h->qacc, (int32_t)h->qacc_cap, 0u));
         h->qacc_clean = true;
     }
+    if (!h->qmax_clean) {
+        TL_LAUNCH(h, launch_fill_u32(h->stream, h->qmax, 4 * h->max_rows, 0u));
+        h->qmax_clean = true;
+    }
     return TL_OK;
 }
 
@@ -669,6 +680,10 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
     const bool ks = decode && kslice_ok(h, L, rows);
     const bool qks = ks && qkv_kslice_ok(h, L, rows, max_t);
     const bool pk = !decode && prefill_packed(h, L, rows);   // h->a8 in the packed GEMM operand layout
+    // prefill tiles on packed operands: qkv_post's work in the Q|K|V GEMM
+    // epilogue, rotated Q in h->qkv ([rows][D]) quantized by the attention tiles
+    const bool fq = pk && h->qkv_fuse && h->rows_one_seq && h->rows_pos0 + rows <= kTileMaxKeys && D % 64 == 0 &&
+                    KVD % 64 == 0;
     int32_t r;
     if (!ks && (r = discard_pending_sums(h))) return r;
     if ((r = rows_rmsnorm(h, rows, L.g_in, pk))) return r;
@@ -676,6 +691,14 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
         // Q|K|V (K = D) K-sliced over the chip: the attention kernel
         // dequantizes the integer sums it reads from h->qacc
         if ((r = linear_acc(h, rows, L.wqkv_p, QKV, D, TL_K_QKV, h->qacc, &h->qacc_clean))) return r;
+    } else if (fq) {
+        GemmArgs a{};
+        a.ap = h->a8; a.wp = L.wqkv_p; a.as = h->as; a.ws = L.sqkv; a.m = rows; a.n = QKV; a.k = D;
+        const QkvRopeArgs f{h->rope_cos, h->rope_sin, rowmap(h), h->kv, layer, c.n_heads, c.n_kv_heads,
+                            h->kv_sk, h->kv_sv, h->qkv, h->qmax};
+        h->qmax_clean = false;
+        Prof p(h, TL_K_QKV, (double)rows * D + (double)QKV * D + (double)rows * (D * 4.0 + KVD * 2.0));
+        TL_LAUNCH(h, launch_gemm_pk_qkv(h->stream, a, f));
     } else if ((r = linear(h, EPI_DEQUANT, rows, h->a8, h->as, L.wqkv, L.sqkv, nullptr, nullptr, QKV, D, nullptr, h->qkv,
                            TL_K_QKV, L.wqkv_p, nullptr, pk))) {
         return r;
@@ -687,6 +710,10 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
         TL_LAUNCH(h, launch_attention_decode(h->stream, h->qkv, rows, c.n_heads, c.n_kv_heads, rowmap(h), h->rope_cos,
                                              h->rope_sin, h->kv, layer, h->kv_sk, h->kv_sv, h->att, max_t,
                                              G == 8 && h->batch_hpw == 8 ? 8 : 1, nullptr, qks ? &sums : nullptr));
+    } else if (fq) {
+        Prof p(h, TL_K_ATTN, (double)rows * c.n_kv_heads * (double)max_t * 128.0 + rows * D * 8.0);
+        TL_LAUNCH(h, launch_attention_tiles(h->stream, nullptr, nullptr, rows, c.n_heads, c.n_kv_heads, h->rows_seq,
+                                            h->rows_pos0, h->kv, layer, h->kv_sk, h->kv_sv, h->att, h->qkv, h->qmax));
     } else {
         {
             Prof p(h, TL_K_ATTN, (double)rows * (QKV * 4.0 + D) + (double)rows * KVD * 2.0);
@@ -697,11 +724,13 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
         TL_LAUNCH(h, rows_attention(h, h->q8, h->qs, rows, layer, h->att, max_t));
     }
     {
-        // with the Q|K|V sums consumed, this kernel also clears them
+        // with the Q|K|V sums (or the Q row maxima) consumed, this kernel also
+        // clears them
+        int32_t* zero = qks ? h->qacc : (fq ? (int32_t*)h->qmax : nullptr);
         Prof p(h, TL_K_NORM, (double)rows * D * 5.0 + (qks ? (double)rows * QKV * 4.0 : 0.0));
-        TL_LAUNCH(h, launch_quantize_rows(h->stream, h->att, rows, D, h->a8, h->as, qks ? h->qacc : nullptr,
-                                          qks ? QKV : 0, pk));
+        TL_LAUNCH(h, launch_quantize_rows(h->stream, h->att, rows, D, h->a8, h->as, zero, qks ? QKV : (fq ? 4 : 0), pk));
         if (qks) h->qacc_clean = true;
+        if (fq) h->qmax_clean = true;
     }
     if ((r = linear(h, EPI_DEQUANT_RES, rows, h->a8, h->as, L.wo, L.so, nullptr, nullptr, D, D, h->x, h->x, TL_K_O,
                     L.wo_p, nullptr, pk)))
@@ -1033,6 +1062,7 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
         (e = dalloc(h, &h->stopped, (size_t)max_seqs)) ||
         (e = dalloc(h, &h->racc, h->racc_cap = (size_t)std::min(32, max_seqs) * D)) ||
         (e = dalloc(h, &h->qacc, h->qacc_cap = (size_t)std::min(32, max_seqs) * h->QKV)) ||
+        (e = dalloc(h, &h->qmax, (size_t)4 * R)) ||
         (e = dalloc(h, &h->tokens_out, (size_t)max_seqs * c.max_pos)) ||
         (e = dalloc(h, &h->logit_out, (size_t)max_seqs * c.max_pos)) ||
         (e = dalloc(h, &h->rope_cos, (size_t)c.max_pos * kHeadDim)) ||
@@ -1074,7 +1104,8 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
         (e = hipMemsetAsync(h->stopped, 0, sizeof(int32_t) * max_seqs, h->stream)) ||
         (e = hipMemsetAsync(h->tile_ctr, 0, sizeof(unsigned) * kSkinnyTiles, h->stream)) ||
         (e = hipMemsetAsync(h->racc, 0, sizeof(int32_t) * h->racc_cap, h->stream)) ||
-        (e = hipMemsetAsync(h->qacc, 0, sizeof(int32_t) * h->qacc_cap, h->stream)))
+        (e = hipMemsetAsync(h->qacc, 0, sizeof(int32_t) * h->qacc_cap, h->stream)) ||
+        (e = hipMemsetAsync(h->qmax, 0, sizeof(unsigned) * 4 * R, h->stream)))
         return bad(e);
     std::vector<float> cs, sn;
     default_rope(c.max_pos, c.rope_theta, cs, sn);
@@ -1099,6 +1130,7 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
     if (const char* env = std::getenv("TL_GEMM_CFG")) h->gemm_cfg = std::atoi(env);
     if (const char* env = std::getenv("TL_PREFILL_PACKED")) h->prefill_pk = env[0] != '0';
     if (const char* env = std::getenv("TL_PK_GLU_TN")) h->pk_glu_tn = std::atoi(env) == 2 ? 2 : 1;
+    if (const char* env = std::getenv("TL_PREFILL_QKV_FUSE")) h->qkv_fuse = env[0] != '0';
     if (const char* env = std::getenv("TL_BATCH_KSLICE")) h->batch_kslice = env[0] != '0';
     if (const char* env = std::getenv("TL_BATCH_QKV_KSLICE")) h->qkv_kslice = env[0] != '0';
     if (const char* env = std::getenv("TL_ROWS32_WAVES")) h->rows32_waves = std::atoi(env);

@@ -405,14 +405,19 @@ def test_prefill_512_tinyllama_shape():
     eng.close()
 
 
-@pytest.mark.parametrize("packed", ["1", "0"], ids=["packed_operands", "row_major"])
+@pytest.mark.parametrize("packed,fuse", [("1", "1"), ("1", "0"), ("0", "1")],
+                         ids=["packed_fused_qkv", "packed", "row_major"])
 @pytest.mark.parametrize("n", [64, 100, 300])
-def test_prefill_lengths_tinyllama_shape(n, packed, monkeypatch):
+def test_prefill_lengths_tinyllama_shape(n, packed, fuse, monkeypatch):
     """Prefills whose length is not a multiple of the GEMM row tiles (the
     packed-operand GEMMs pad A to 128 rows; TL_PREFILL_PACKED=0 runs the
-    row-major kernels) on a 2-layer TinyLlama-shape model: next token, its
-    logit and every K/V row equal token-by-token decode in the oracle."""
+    row-major kernels; by default the packed Q|K|V GEMM also rotates,
+    quantizes and appends K/V and leaves Q for the attention tiles to
+    quantize, TL_PREFILL_QKV_FUSE=0 keeps qkv_post) on a 2-layer
+    TinyLlama-shape model: next token, its logit and every K/V row equal
+    token-by-token decode in the oracle."""
     monkeypatch.setenv("TL_PREFILL_PACKED", packed)
+    monkeypatch.setenv("TL_PREFILL_QKV_FUSE", fuse)
     cfg = dict(oracle.TINYLLAMA_CFG, n_layers=2, vocab=4096)
     m = oracle.synthetic_model(cfg, seed=40 + n)
     prompt = np.random.default_rng(n).integers(0, cfg["vocab"], n).astype(np.int32)
