@@ -703,7 +703,7 @@ TL_DEV void qkv_rope_epilogue(const GemmArgs& a, const QkvRopeArgs& f, const Qkv
             f.q_out[(int64_t)m * D + o.n0 + d + 32] = rhi;
         }
         const float mx = half_max_f32(valid ? fmaxf(fabsf(rlo), fabsf(rhi)) : 0.0f);   // the row's 32 lanes
-        if (d == 0 && valid) atomicMax(f.q_max + (int64_t)m * 4, __float_as_uint(mx));
+        if (d == 0 && valid) atomicMax(f.q_max + (int64_t)m * kQmaxStride, __float_as_uint(mx));
     }
 }
 

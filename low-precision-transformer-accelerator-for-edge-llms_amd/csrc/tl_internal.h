@@ -164,7 +164,8 @@ hipError_t launch_qkv_post(hipStream_t s, const float* qkv, int32_t rows, int32_
                            int8_t* q8, double* q_scale, float* q_rot_out, bool append_kv = true);
 constexpr int kTileMaxKeys = 4096;   // context limit of launch_attention_tiles (LDS)
 // qf / qmax (optional, instead of q8 / q_scale): rotated Q rows in float32
-// ([rows][D]) and their maxima max|q| as float bits ([rows][4], element 0),
+// ([rows][D]) and their maxima max|q| as float bits ([rows][kQmaxStride],
+// element 0),
 // quantized by the kernel exactly as qkv_post quantizes them
 hipError_t launch_attention_tiles(hipStream_t s, const int8_t* q8, const double* q_scale, int32_t rows,
                                   int32_t n_heads, int32_t n_kv_heads, int32_t seq, int32_t pos0, KvGeom kv,
@@ -298,8 +299,12 @@ bool gemm_pk_supported(int epi, int32_t m, int32_t n, int32_t k);
 // the prefill Q|K|V GEMM with qkv_post's work in its epilogue (EPI_QKV_ROPE):
 // RoPE on Q and K at each row's position, K and V quantized with the static
 // per-head scales into the cache, rotated Q written to q_out ([M][D] float32)
-// and max|q| of each row folded into q_max[4 row] (float bits, atomic max;
-// zero beforehand).  Needs N = D + 2 KVD with D, KVD multiples of 64.
+// and max|q| of each row folded into q_max[kQmaxStride row] (float bits,
+// atomic max; zero beforehand).  Needs N = D + 2 KVD with D, KVD multiples
+// of 64.  One 128-byte line per row: the 32 heads' atomics on a row then
+// share a line with no other row's (4-byte rows took the GEMM from 13.5 to
+// 15.5 us, 16-byte rows measured 13.3-13.7 us).
+constexpr int kQmaxStride = 32;
 struct QkvRopeArgs {
     const float* cosb;
     const float* sinb;

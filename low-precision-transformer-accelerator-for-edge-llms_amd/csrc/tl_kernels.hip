@@ -897,7 +897,7 @@ struct AttnTileArgs {
     double attn_scale;
     float* out;              // [rows][D]
     const float* qf;         // or rotated Q in float32 [rows][D], quantized here
-    const unsigned* qmax;    // with qf: max|q| of each row as float bits [rows][4]
+    const unsigned* qmax;    // with qf: max|q| of each row as float bits [rows][kQmaxStride]
 };
 
 // Q fragments of a tile lane (row r, head h, K halves hi * 16 .. + 16 and
@@ -927,7 +927,7 @@ TL_DEV void tile_q_load(const AttnTileArgs& p, int r0, int nr, int h, int col, i
     const float4* qr = (const float4*)(p.qf + (int64_t)r * D + h * kHeadDim + (threadIdx.x & 7) * 8);
     q.x0 = qr[0];
     q.x1 = qr[1];
-    q.mx = p.qmax[(int64_t)r * 4];
+    q.mx = p.qmax[(int64_t)r * kQmaxStride];
 }
 
 // before the barrier: quantize this thread's 8 values into qs8 ([32][64])
@@ -951,7 +951,7 @@ TL_DEV void tile_q_frags(const AttnTileArgs& p, const int8_t* qs8, int col, int 
 
 // the row's Q scale (GI:36-42) for the score dequantization
 TL_DEV double tile_q_scale(const AttnTileArgs& p, int r) {
-    return p.qf ? quant_scale(__uint_as_float(p.qmax[(int64_t)r * 4])) : p.q_scale[r];
+    return p.qf ? quant_scale(__uint_as_float(p.qmax[(int64_t)r * kQmaxStride])) : p.q_scale[r];
 }
 
 __global__ __launch_bounds__(256) void attention_tile_kernel(AttnTileArgs p) {

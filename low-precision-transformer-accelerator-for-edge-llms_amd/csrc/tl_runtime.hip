@@ -134,7 +134,7 @@ struct tl_handle {
                                   // by the attention kernel; zero between uses (the attention output's
                                   // quantization clears them)
     size_t qacc_cap = 0;          // int32 elements
-    unsigned* qmax = nullptr;     // [max_rows][4] prefill: max|q| of each rotated Q row (float bits, element 0)
+    unsigned* qmax = nullptr;     // [max_rows][kQmaxStride] prefill: max|q| of each rotated Q row (float bits, element 0)
                                   // from the fused Q|K|V GEMM; zero between uses (the attention output's
                                   // quantization clears them)
     unsigned* tile_ctr = nullptr;         // [kSkinnyTiles] arrival counters of the small-M GEMM, zero between launches
@@ -629,7 +629,7 @@ static int32_t discard_pending_sums(tl_handle* h) {
         h->qacc_clean = true;
     }
     if (!h->qmax_clean) {
-        TL_LAUNCH(h, launch_fill_u32(h->stream, h->qmax, 4 * h->max_rows, 0u));
+        TL_LAUNCH(h, launch_fill_u32(h->stream, h->qmax, kQmaxStride * h->max_rows, 0u));
         h->qmax_clean = true;
     }
     return TL_OK;
@@ -728,7 +728,8 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
         // clears them
         int32_t* zero = qks ? h->qacc : (fq ? (int32_t*)h->qmax : nullptr);
         Prof p(h, TL_K_NORM, (double)rows * D * 5.0 + (qks ? (double)rows * QKV * 4.0 : 0.0));
-        TL_LAUNCH(h, launch_quantize_rows(h->stream, h->att, rows, D, h->a8, h->as, zero, qks ? QKV : (fq ? 4 : 0), pk));
+        TL_LAUNCH(h, launch_quantize_rows(h->stream, h->att, rows, D, h->a8, h->as, zero,
+                                          qks ? QKV : (fq ? kQmaxStride : 0), pk));
         if (qks) h->qacc_clean = true;
         if (fq) h->qmax_clean = true;
     }
@@ -1062,7 +1063,7 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
         (e = dalloc(h, &h->stopped, (size_t)max_seqs)) ||
         (e = dalloc(h, &h->racc, h->racc_cap = (size_t)std::min(32, max_seqs) * D)) ||
         (e = dalloc(h, &h->qacc, h->qacc_cap = (size_t)std::min(32, max_seqs) * h->QKV)) ||
-        (e = dalloc(h, &h->qmax, (size_t)4 * R)) ||
+        (e = dalloc(h, &h->qmax, (size_t)kQmaxStride * R)) ||
         (e = dalloc(h, &h->tokens_out, (size_t)max_seqs * c.max_pos)) ||
         (e = dalloc(h, &h->logit_out, (size_t)max_seqs * c.max_pos)) ||
         (e = dalloc(h, &h->rope_cos, (size_t)c.max_pos * kHeadDim)) ||
@@ -1105,7 +1106,7 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
         (e = hipMemsetAsync(h->tile_ctr, 0, sizeof(unsigned) * kSkinnyTiles, h->stream)) ||
         (e = hipMemsetAsync(h->racc, 0, sizeof(int32_t) * h->racc_cap, h->stream)) ||
         (e = hipMemsetAsync(h->qacc, 0, sizeof(int32_t) * h->qacc_cap, h->stream)) ||
-        (e = hipMemsetAsync(h->qmax, 0, sizeof(unsigned) * 4 * R, h->stream)))
+        (e = hipMemsetAsync(h->qmax, 0, sizeof(unsigned) * kQmaxStride * R, h->stream)))
         return bad(e);
     std::vector<float> cs, sn;
     default_rope(c.max_pos, c.rope_theta, cs, sn);
