@@ -439,6 +439,36 @@ def test_prefill_lengths_tinyllama_shape(n, packed, fuse, monkeypatch):
     eng.close()
 
 
+@pytest.mark.parametrize("fuse", ["1", "0"], ids=["fused_qkv", "qkv_post"])
+def test_prefill_packed_other_geometry(fuse, monkeypatch):
+    """The packed-operand prefill GEMMs at a second geometry (hidden 1024,
+    FFN 3072, 16 query / 4 KV heads: Q|K|V N = 1536, one 64-row tile per
+    head, the 32 x 160 split tile not taken) with 200 rows: next token, its
+    logit and every K/V row equal token-by-token decode in the oracle."""
+    monkeypatch.setenv("TL_PREFILL_QKV_FUSE", fuse)
+    cfg = dict(oracle.TINYLLAMA_CFG, hidden=1024, intermediate=3072, n_heads=16, n_kv_heads=4, n_layers=2,
+               vocab=2048, max_pos=512)
+    m = oracle.synthetic_model(cfg, seed=77)
+    n = 200
+    prompt = np.random.default_rng(77).integers(0, cfg["vocab"], n).astype(np.int32)
+    eng = engine_for(m)
+    tok, lg = eng.prefill(prompt)
+    orc = oracle.Oracle(m)
+    kc, vc = m.new_cache()
+    x = None
+    for i, t in enumerate(prompt):
+        x = orc.embed(int(t))
+        for layer in range(cfg["n_layers"]):
+            x = orc.decode_row(layer, i, x, kc, vc)
+    assert (tok, lg) == orc.lm_head(x)
+    for layer in range(cfg["n_layers"]):
+        for g in range(cfg["n_kv_heads"]):
+            k, v = eng.kv_read(0, layer, g, 0, n)
+            assert_bits_equal(k, kc[layer, g, :n], f"K layer {layer} head {g}")
+            assert_bits_equal(v, vc[layer, g, :n], f"V layer {layer} head {g}")
+    eng.close()
+
+
 @DECODE_PATHS
 def test_generate_tinyllama_shape_matches_oracle(persist, monkeypatch):
     """Greedy generation on a 2-layer TinyLlama-shape model (hidden 2048, FFN
