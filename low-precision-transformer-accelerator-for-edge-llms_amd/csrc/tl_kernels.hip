@@ -1874,23 +1874,29 @@ __global__ __launch_bounds__(256) void attention_tile_reg_kernel(AttnTileArgs p)
     const float sk = p.kv_sk[p.layer * p.n_kv + g], sv = p.kv_sv[p.layer * p.n_kv + g];
 
     // every load first: Q, then K of this wavefront's blocks b = wave + 4 j
-    // (two 32-key tiles each), then V of its 32-key chunks c = wave + 4 j
-    // (block indices clamped inside the plane; surplus copies unused)
+    // (two 32-key tiles each), then V of its 32-key chunks c = wave + 4 j.
+    // Blocks and chunks past the tile's keys (b >= nblk, c >= tpad / 32: a
+    // short causal tile) are skipped here and in every pass below -- each
+    // test is uniform per wavefront -- so a short tile costs less than the
+    // longest instead of the same.
     TileQ tq;
     tile_q_load(p, r0, nr, h, col, hi, tq);
     v4i kf[NB][2][2], vf[2 * NB][2];
 #pragma unroll
-    for (int j = 0; j < NB; j++)
+    for (int j = 0; j < NB; j++) {
+        if (wave + 4 * j >= nblk) continue;
 #pragma unroll
         for (int half = 0; half < 2; half++) {
-            const int t = min(64 * (wave + 4 * j), tpad - 64) + 32 * half + col;
+            const int t = 64 * (wave + 4 * j) + 32 * half + col;
             const int8_t* kb = kp + (int64_t)(t >> 6) * 4096 + hi * 1024 + (t & 63) * 16;
             kf[j][half][0] = ld16(kb);
             kf[j][half][1] = ld16(kb + 2048);
         }
+    }
 #pragma unroll
     for (int j = 0; j < 2 * NB; j++) {
-        const int kc = min(wave + 4 * j, tpad / 32 - 1);
+        const int kc = wave + 4 * j;
+        if (kc >= tpad / 32) continue;
         const int8_t* vb = vp + (int64_t)(kc * 2 + hi) * 1024 + col * 16;
         vf[j][0] = ld16(vb);
         vf[j][1] = ld16(vb + 512);
@@ -1908,22 +1914,23 @@ __global__ __launch_bounds__(256) void attention_tile_reg_kernel(AttnTileArgs p)
     float sc[NB][2][16];
     float mx = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < NB; j++)
+    for (int j = 0; j < NB; j++) {
+        if (wave + 4 * j >= nblk) continue;
 #pragma unroll
         for (int half = 0; half < 2; half++) {
             v16i acc = {};
             acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[j][half][0], qa0, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[j][half][1], qa1, acc, 0, 0, 0);
             const int t0 = 64 * (wave + 4 * j) + 32 * half + 4 * hi;
-            const bool blk = wave + 4 * j < nblk;
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const float v = (float)acc[i] * rs;
                 sc[j][half][i] = v;
                 const int t = t0 + 8 * (i >> 2) + (i & 3);
-                mx = (blk && t <= rpos) ? fmaxf(mx, v) : mx;
+                mx = t <= rpos ? fmaxf(mx, v) : mx;
             }
         }
+    }
     mx = fmaxf(mx, lane_xor<32>(mx));
     if (hi == 0) wmax[wave][col] = mx;
     __syncthreads();
@@ -1933,6 +1940,7 @@ __global__ __launch_bounds__(256) void attention_tile_reg_kernel(AttnTileArgs p)
 #pragma unroll
     for (int j = 0; j < NB; j++) {
         const int b = wave + 4 * j;
+        if (b >= nblk) continue;
         const int t0 = 64 * b + 4 * hi;
 #pragma unroll
         for (int half = 0; half < 2; half++)
@@ -1954,7 +1962,7 @@ __global__ __launch_bounds__(256) void attention_tile_reg_kernel(AttnTileArgs p)
 #pragma unroll
         for (int r = 0; r < 4; r++) d[r] = pair_sum<32>(c[r]);      // distance 4
         const float f = (d[0] + d[2]) + (d[1] + d[3]);                        // distances 2, 1
-        if (hi == 0 && b < nblk) bsum[col * nblk + b] = f;
+        if (hi == 0) bsum[col * nblk + b] = f;
     }
     __syncthreads();
     if (tid < 32) {
