@@ -561,8 +561,8 @@ __global__ __launch_bounds__(256) void attention_row_kernel(AttnDecodeArgs p) {
     for (int b = wave; b < nblk; b += NW) {
         const int t = b * 64 + lane;
         float e = 0.0f;
-        if (t < T) {
-            e = tl_expf(s_buf[t] - m);
+        if (t < T) {   // x - max <= 0: tl_expf_nonpos is tl_expf there
+            e = tl_expf_nonpos(s_buf[t] - m);
             s_buf[t] = e;
         }
         const float bs = wave_butterfly_sum(e);
@@ -572,7 +572,8 @@ __global__ __launch_bounds__(256) void attention_row_kernel(AttnDecodeArgs p) {
     const float tot = ordered_sum_aligned(bsum, nblk);   // bsum: 16-byte aligned, 16 bytes of slack
 
     // 5) INT8 probabilities of this wavefront's keys (exponential / total,
-    //    correctly rounded: e <= 1 <= total keeps e y finite), then P . V over
+    //    correctly rounded: e <= 1 <= total keeps e y finite; e <= total, so
+    //    rne(127 e / total) lies in [0, 127] with no clamp), then P . V over
     //    the same keys (lane <-> dimension; this row's V is v8 of lane d)
     const RnDiv dt = rn_div_prep(tot);
     auto probs = [&](auto fast) {
@@ -581,9 +582,7 @@ __global__ __launch_bounds__(256) void attention_row_kernel(AttnDecodeArgs p) {
             int8_t pq = 0;
             if (t < T) {
                 const float q = decltype(fast)::value ? rn_div_fast(s_buf[t], dt) : __fdiv_rn(s_buf[t], tot);
-                float pr = __builtin_rintf(q * 127.0f);
-                pr = pr < 0.0f ? 0.0f : (pr > 127.0f ? 127.0f : pr);
-                pq = (int8_t)(int)pr;
+                pq = (int8_t)(int)__builtin_rintf(q * 127.0f);
             }
             p8[t] = pq;
         }
@@ -804,8 +803,8 @@ __global__ __launch_bounds__(kGW * 64) void attention_group_kernel(AttnDecodeArg
 #pragma unroll
             for (int h = 0; h < HPW; h++) {
                 float e = 0.0f;
-                if (t < T) {
-                    e = tl_expf(s_buf[h * tpad + t] - mh[h]);
+                if (t < T) {   // x - max <= 0: tl_expf_nonpos is tl_expf there
+                    e = tl_expf_nonpos(s_buf[h * tpad + t] - mh[h]);
                     s_buf[h * tpad + t] = e;
                 }
                 const float bs = wave_butterfly_sum(e);
@@ -819,24 +818,40 @@ __global__ __launch_bounds__(kGW * 64) void attention_group_kernel(AttnDecodeArg
     }
     __syncthreads();
 
-    // 4) INT8 probabilities (zero past the last key)
+    // 4) INT8 probabilities (zero past the last key): exponential / total
+    //    correctly rounded from each head's reciprocal and two residual
+    //    corrections (e <= 1 <= total keeps e y finite).  A float sum of
+    //    nonnegative terms is never below any of them, so e <= total and
+    //    rne(127 e / total) lies in [0, 127]: the probability clip needs no
+    //    clamp.
+    RnDiv dt[HPW];
+    bool fast = true;
 #pragma unroll
-    for (int i = 0; i < kGKB; i++) {
-        const int b = wave + kGW * i;
-        if (b < nblk) {
-            const int t = b * 64 + lane;
+    for (int h = 0; h < HPW; h++) {
+        dt[h] = rn_div_prep(toth[h]);
+        fast = fast && dt[h].fast;
+    }
+    auto probs = [&](auto fst) {
 #pragma unroll
-            for (int h = 0; h < HPW; h++) {
-                int8_t pq = 0;
-                if (t < T) {
-                    float pr = __builtin_rintf(__fdiv_rn(s_buf[h * tpad + t], toth[h]) * 127.0f);
-                    pr = pr < 0.0f ? 0.0f : (pr > 127.0f ? 127.0f : pr);
-                    pq = (int8_t)(int)pr;
+        for (int i = 0; i < kGKB; i++) {
+            const int b = wave + kGW * i;
+            if (b < nblk) {
+                const int t = b * 64 + lane;
+#pragma unroll
+                for (int h = 0; h < HPW; h++) {
+                    int8_t pq = 0;
+                    if (t < T) {
+                        const float e = s_buf[h * tpad + t];
+                        const float q = decltype(fst)::value ? rn_div_fast(e, dt[h]) : __fdiv_rn(e, dt[h].b);
+                        pq = (int8_t)(int)__builtin_rintf(q * 127.0f);
+                    }
+                    p8[h * tpad + t] = pq;
                 }
-                p8[h * tpad + t] = pq;
             }
         }
-    }
+    };
+    if (fast) probs(std::true_type{});
+    else probs(std::false_type{});
     __syncthreads();
 
     // 5) P . V (lane <-> dimension) over this wavefront's value groups; the

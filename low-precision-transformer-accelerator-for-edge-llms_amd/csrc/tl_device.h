@@ -68,6 +68,31 @@ TL_DEV float tl_expf_sel(float x) {
     return x >= -80.0f ? e : 0.0f;
 }
 
+// tl_expf for x <= 0 (a softmax argument: a score minus its row's maximum),
+// the same value in fewer instructions: such x never reach the upper clamp;
+// below -80 the select returns 0 whatever the reduction gave, so the lower
+// clamp is not needed either; and from -80 to 0, k = rint(x log2e) lies in
+// [-116, 0], where p 2^k is a normal float, so ldexp(p, k) equals the
+// product with 2^k exactly.
+TL_DEV float tl_expf_nonpos(float x) {
+    const float log2e = 0x1.715476p+0f;
+    const float c1 = 0x1.63p-1f;
+    const float c2 = -0x1.bd0106p-13f;
+    const float kf = __builtin_rintf(x * log2e);
+    float r = __builtin_fmaf(-kf, c1, x);
+    r = __builtin_fmaf(-kf, c2, r);
+    float p = 0x1.a01a02p-13f;
+    p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+    p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const float e = __builtin_amdgcn_ldexpf(p, (int)kf);
+    return x >= -80.0f ? e : 0.0f;
+}
+
 // SiLU, TL:159-161: x / (1 + exp(-clip(x, -60, 60)))
 TL_DEV float tl_silu(float x) {
     float c = x < -60.0f ? -60.0f : (x > 60.0f ? 60.0f : x);

@@ -1922,12 +1922,21 @@ __global__ __launch_bounds__(256) void attention_tile_reg_kernel(AttnTileArgs p)
             acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[j][half][0], qa0, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[j][half][1], qa1, acc, 0, 0, 0);
             const int t0 = 64 * (wave + 4 * j) + 32 * half + 4 * hi;
+            if (64 * (wave + 4 * j) + 63 <= pos_first) {   // every row sees the whole block
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const float v = (float)acc[i] * rs;
-                sc[j][half][i] = v;
-                const int t = t0 + 8 * (i >> 2) + (i & 3);
-                mx = t <= rpos ? fmaxf(mx, v) : mx;
+                for (int i = 0; i < 16; i++) {
+                    const float v = (float)acc[i] * rs;
+                    sc[j][half][i] = v;
+                    mx = fmaxf(mx, v);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const float v = (float)acc[i] * rs;
+                    sc[j][half][i] = v;
+                    const int t = t0 + 8 * (i >> 2) + (i & 3);
+                    mx = t <= rpos ? fmaxf(mx, v) : mx;
+                }
             }
         }
     }
@@ -1942,13 +1951,21 @@ __global__ __launch_bounds__(256) void attention_tile_reg_kernel(AttnTileArgs p)
         const int b = wave + 4 * j;
         if (b >= nblk) continue;
         const int t0 = 64 * b + 4 * hi;
+        // x - m <= 0 for every key a row sees: tl_expf_nonpos is tl_expf there
+        if (64 * b + 63 <= pos_first) {
 #pragma unroll
-        for (int half = 0; half < 2; half++)
+            for (int half = 0; half < 2; half++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int t = t0 + 32 * half + 8 * (i >> 2) + (i & 3);
-                sc[j][half][i] = t <= rpos ? tl_expf_sel(sc[j][half][i] - m) : 0.0f;
-            }
+                for (int i = 0; i < 16; i++) sc[j][half][i] = tl_expf_nonpos(sc[j][half][i] - m);
+        } else {
+#pragma unroll
+            for (int half = 0; half < 2; half++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int t = t0 + 32 * half + 8 * (i >> 2) + (i & 3);
+                    sc[j][half][i] = t <= rpos ? tl_expf_nonpos(sc[j][half][i] - m) : 0.0f;
+                }
+        }
         float a[16];
 #pragma unroll
         for (int i = 0; i < 16; i++) a[i] = sc[j][0][i] + sc[j][1][i];      // distance 32
@@ -1974,7 +1991,10 @@ __global__ __launch_bounds__(256) void attention_tile_reg_kernel(AttnTileArgs p)
     // pass C: INT8 probabilities, four consecutive keys per 32-bit store;
     // exponential / total correctly rounded from the row's reciprocal and two
     // residual corrections (e <= 1 <= total keeps e y finite; the wave vote
-    // confirms every total lies in the quotient's range)
+    // confirms every total lies in the quotient's range).  A float sum of
+    // nonnegative terms is never below any of them, so 0 <= e <= total and
+    // rne(127 e / total) already lies in [0, 127]: the probability clip holds
+    // without a clamp, and the byte is packed straight from the float.
     const float tr = tot[col];
     const RnDiv dv{tr, __fdiv_rn(1.0f, tr), true};
     const bool fast = __all(fabsf(tr) >= 0x1p-64f && fabsf(tr) <= 0x1p64f);
@@ -1990,9 +2010,8 @@ __global__ __launch_bounds__(256) void attention_tile_reg_kernel(AttnTileArgs p)
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
                         const float e = sc[j][half][4 * q + r];
-                        float pr = __builtin_rintf((fast ? rn_div_fast(e, dv) : __fdiv_rn(e, tr)) * 127.0f);
-                        pr = pr < 0.0f ? 0.0f : (pr > 127.0f ? 127.0f : pr);
-                        word |= (unsigned)(uint8_t)(int)pr << (8 * r);
+                        const float pr = __builtin_rintf((fast ? rn_div_fast(e, dv) : __fdiv_rn(e, tr)) * 127.0f);
+                        word = __builtin_amdgcn_cvt_pk_u8_f32(pr, r, word);
                     }
                     *(unsigned*)(p8 + col * tpad + 64 * b + 32 * half + 8 * q + 4 * hi) = word;
                 }
