@@ -58,6 +58,50 @@ def test_decode_layer_tinyllama_shape(layer_model):
     eng.close()
 
 
+def test_decode_sharp_softmax_matches_oracle():
+    """Decode attention with K/V scales of 1-3 (scores spread over hundreds,
+    so most exponentials fall past the cut-off at -80): the batch-1 decode
+    layer output and batched decode of three sequences over two layers equal
+    the oracle bit for bit; the second layer's K/V rows are built from the
+    first layer's attention output."""
+    cfg = dict(oracle.TINYLLAMA_CFG, n_layers=2, vocab=512)
+    m = oracle.synthetic_model(cfg, seed=31, kv_range=(1.0, 3.0))
+    orc = oracle.Oracle(m)
+    eng = engine_for(m)
+    kc, vc = m.new_cache()
+    fill_cache_random(eng, m, 0, 700, seed=8, kc=kc, vc=vc)
+    x = np.random.default_rng(9).standard_normal(2048).astype(F32)
+    xd = dev(x)
+    eng.decode_layer(xd, layer=0, pos=700)
+    assert_bits_equal(host(xd), orc.decode_row(0, 700, x, kc, vc), "batch-1 layer output")
+    eng.close()
+    B, steps = 3, 2
+    eng = engine_for(m, max_seqs=B)
+    start = np.array([100, 640, 1500], np.int32)
+    toks = np.array([3, 77, 400], np.int32)
+    caches = []
+    for b in range(B):
+        kc, vc = m.new_cache()
+        fill_cache_random(eng, m, b, int(start[b]), seed=40 + b, kc=kc, vc=vc)
+        caches.append((kc, vc))
+    got = eng.decode_batch(toks, start, steps)
+    for b in range(B):
+        kc, vc = caches[b]
+        tok = int(toks[b])
+        for s in range(steps):
+            x = orc.embed(tok)
+            for layer in range(cfg["n_layers"]):
+                x = orc.decode_row(layer, int(start[b]) + s, x, kc, vc)
+            tok, _ = orc.lm_head(x)
+            assert got[b, s] == tok, f"seq {b} step {s}"
+        for layer in range(cfg["n_layers"]):
+            for g in range(4):
+                k, v = eng.kv_read(b, layer, g, 0, int(start[b]) + steps)
+                assert_bits_equal(k, kc[layer, g, :int(start[b]) + steps], f"K seq {b} layer {layer}")
+                assert_bits_equal(v, vc[layer, g, :int(start[b]) + steps], f"V seq {b} layer {layer}")
+    eng.close()
+
+
 # ---- small models: generation, prefill == decode, batched decode -------------------
 
 @pytest.fixture(scope="module")
@@ -496,14 +540,17 @@ def test_generate_tinyllama_shape_matches_oracle(persist, monkeypatch):
 
 # ---- causal attention of a block of rows (prefill tiles) ----------------------------
 
-@pytest.mark.parametrize("shape,pos0,rows", [
-    ("tinyllama", 0, 1), ("tinyllama", 0, 77), ("tinyllama", 130, 64), ("tinyllama", 1900, 100),
-    ("small", 5, 33), ("small", 0, 256), ("small", 96, 160)])
-def test_attention_rows_match_oracle(shape, pos0, rows):
+@pytest.mark.parametrize("shape,pos0,rows,sharp", [
+    ("tinyllama", 0, 1, False), ("tinyllama", 0, 77, False), ("tinyllama", 130, 64, False),
+    ("tinyllama", 1900, 100, False), ("small", 5, 33, False), ("small", 0, 256, False),
+    ("small", 96, 160, False), ("tinyllama", 0, 512, True), ("small", 96, 160, True)])
+def test_attention_rows_match_oracle(shape, pos0, rows, sharp):
     """tl_attention over rows at positions pos0 .. pos0 + rows - 1 of one
     sequence (the prefill path: INT8 MFMA tiles of 32 rows, partial last
     tiles, tiles that start mid-context) equals the oracle's per-row GQA
-    attention over the same INT8 cache, bit for bit."""
+    attention over the same INT8 cache, bit for bit.  With `sharp`, Q scales
+    of 0.5-2 put most of each row's scores more than 80 below its maximum,
+    where the exponential is 0 by the cut-off rather than by the polynomial."""
     base = oracle.TINYLLAMA_CFG if shape == "tinyllama" else oracle.SMALL_CFG
     cfg = dict(base, n_layers=1, vocab=64)
     from lpta.engine import Engine
@@ -522,7 +569,12 @@ def test_attention_rows_match_oracle(shape, pos0, rows):
         vc[0, g, :n] = rng.integers(-127, 128, (n, 64))
         eng.kv_write(0, 0, g, 0, kc[0, g, :n], vc[0, g, :n])
     q8 = rng.integers(-127, 128, (rows, D)).astype(np.int8)
-    qs = rng.uniform(0.005, 0.05, rows)
+    qs = rng.uniform(0.5, 2.0, rows) if sharp else rng.uniform(0.005, 0.05, rows)
+    if sharp:   # the regime is reached: keys below max - 80 in the last row of head 0
+        r = rows - 1
+        s = (kc[0, 0, :pos0 + rows].astype(np.int64) @ q8[r, :64].astype(np.int64)).astype(F32)
+        s = s * F32(qs[r] * float(sk[0, 0]) * 0.125)
+        assert np.count_nonzero(s - s.max() < -80) > (pos0 + rows) // 2
     out = dev(np.zeros((rows, D), F32))
     eng.rt.call("tl_attention", 0, 0, pos0, rows, dev(q8), dev(qs), out)
     got = host(out)
