@@ -603,8 +603,8 @@ TL_DEV void pk_wait_regs(v4i* r) {
 // down (256 workgroups at M = 512), 32 x 160 (TM = 1, TN = 5) for Q|K|V
 // (N = 2560: 256 workgroups where 64 x 64 needs 320); 64 x 64 for the
 // prefill Q|K|V with qkv_post's work in the epilogue (EPI_QKV_ROPE, one head
-// per tile).  The epilogue's operands are loaded right after the first
-// operand loads, so they arrive during the main loop.
+// per tile).  The epilogue's operands are loaded behind the last operand
+// loads, so they arrive during the last MFMAs.
 constexpr int kPkSplitPD = 4;
 
 static size_t pk_split_lds_bytes(int tm, int tn) { return (size_t)4 * tm * tn * 16 * 64 * sizeof(int); }
@@ -668,16 +668,22 @@ TL_DEV void qkv_rope_epilogue(const GemmArgs& a, const QkvRopeArgs& f, const Qkv
                               int lane) {
     constexpr int NBLK = 4, NE = 8;
     const int d = lane & 31, D = f.n_heads * kHeadDim;
+    int a0[NE], a1[NE];   // every partial sum first: the LDS reads overlap
+#pragma unroll
+    for (int ee = 0; ee < NE; ee++) {
+        const int e = o.e0 + ee;
+        a0[ee] = 0;
+        a1[ee] = 0;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            a0[ee] += red[((w * NBLK + o.i * 2) * 16 + e) * 64 + lane];
+            a1[ee] += red[((w * NBLK + o.i * 2 + 1) * 16 + e) * 64 + lane];
+        }
+    }
 #pragma unroll
     for (int ee = 0; ee < NE; ee++) {
         const int e = o.e0 + ee, m = o.rb + 8 * (e >> 2) + (e & 3);
-        int a0 = 0, a1 = 0;
-#pragma unroll
-        for (int w = 0; w < 4; w++) {
-            a0 += red[((w * NBLK + o.i * 2) * 16 + e) * 64 + lane];
-            a1 += red[((w * NBLK + o.i * 2 + 1) * 16 + e) * 64 + lane];
-        }
-        const float lo = (float)a0 * deq_mult(o.sx[ee], o.sw0), hi = (float)a1 * deq_mult(o.sx[ee], o.sw1);
+        const float lo = (float)a0[ee] * deq_mult(o.sx[ee], o.sw0), hi = (float)a1[ee] * deq_mult(o.sx[ee], o.sw1);
         const int pos = o.pos[ee];
         const bool valid = m < a.m && pos >= 0 && pos < f.kv.max_pos;   // uniform per half-wavefront
         if (o.region == 2) {
@@ -750,19 +756,26 @@ __global__ __launch_bounds__(256) void gemm_pk_split_kernel(GemmArgs a, QkvRopeA
     // peeled), so every wait is for the oldest set only
 #pragma unroll
     for (int u = 0; u < PD; u++) load(u, c0 + u);
-    for (int c = PD; c < per; c += PD) {
+    int c = PD;
+    for (; c < per - PD; c += PD) {
 #pragma unroll
         for (int u = 0; u < PD; u++) {
             mma(u);
             load(u, c0 + c + u);
         }
     }
+    if (c < per) {   // the last reloads
 #pragma unroll
-    for (int u = 0; u < PD; u++) mma(u);
-    // the epilogue's operands go out now (vector-memory waits complete in
-    // issue order, so earlier they would hold up the main loop) and arrive
-    // while the partial tiles pass through LDS.  Block b, lane l, register e
-    // is output row 8 (e / 4) + 4 (l / 32) + e % 4, column l % 32.
+        for (int u = 0; u < PD; u++) {
+            mma(u);
+            load(u, c0 + c + u);
+        }
+    }
+    // the epilogue's operands go out behind the last operand loads: their
+    // latency passes under the last PD sets of MFMAs instead of after them
+    // (vector-memory waits complete in issue order, so issued earlier they
+    // would hold up the main loop's waits).  Block b, lane l, register e is
+    // output row 8 (e / 4) + 4 (l / 32) + e % 4, column l % 32.
     QkvRopeOps qo;
     SplitOps<NBW, RES> so;
     if constexpr (EPI == EPI_QKV_ROPE) {
@@ -784,6 +797,8 @@ __global__ __launch_bounds__(256) void gemm_pk_split_kernel(GemmArgs a, QkvRopeA
         }
     }
 #pragma unroll
+    for (int u = 0; u < PD; u++) mma(u);
+#pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++)
@@ -796,20 +811,26 @@ __global__ __launch_bounds__(256) void gemm_pk_split_kernel(GemmArgs a, QkvRopeA
         return;
     }
     // wavefront w finishes blocks w, w + 4, ... (y may be the residual, read
-    // above and written here in place)
+    // above and written here in place).  Every partial sum is read before
+    // any store, outside the row test, so the LDS reads overlap instead of
+    // paying one LDS round trip per element.
 #pragma unroll
     for (int bw = 0; bw < NBW; bw++) {
         const int b = wave + 4 * bw;
         if (b >= NBLK) break;
         const int i = b / TN, j = b % TN, n = (nt0 + j) * 32 + (lane & 31);
         const int rb = (mt0 + i) * 32 + 4 * (lane >> 5);
+        int sum[16];
 #pragma unroll
         for (int e = 0; e < 16; e++) {
-            int sum = 0;
+            sum[e] = 0;
 #pragma unroll
-            for (int w = 0; w < 4; w++) sum += pk_red[((w * NBLK + b) * 16 + e) * 64 + lane];
+            for (int w = 0; w < 4; w++) sum[e] += pk_red[((w * NBLK + b) * 16 + e) * 64 + lane];
+        }
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
             const int m = rb + 8 * (e >> 2) + (e & 3);
-            const float v = (float)sum * deq_mult(so.sx[bw][e], so.sw[bw]);
+            const float v = (float)sum[e] * deq_mult(so.sx[bw][e], so.sw[bw]);
             if (m < a.m) a.y[(int64_t)m * a.n + n] = RES ? so.res[bw][RES ? e : 0] + v : v;
         }
     }

@@ -1596,6 +1596,25 @@ __global__ __launch_bounds__(W * 64) void gemm_rows32_kernel(GemmArgs a) {
     }
     const int64_t wstep = PK ? 1024 : 32;   // bytes between consecutive K chunks
     const int per = (kch + W - 1) / W;   // consecutive chunks of this wavefront: 4 loads cover a 128-byte line
+    // the epilogue's operands of this wavefront's output elements (registers
+    // i = wave + W ii of every lane: row 8 (i / 4) + 4 (l / 32) + i % 4,
+    // column n0 + l % 32) are requested first, so they arrive with the first
+    // weight loads instead of after the LDS fold (indices clamped in range;
+    // out-of-range elements are not stored)
+    constexpr int NI = 16 / W;
+    double esx[NI];
+    float eres[NI], esw = 0.0f, esw2 = 0.0f;
+    if constexpr (EPI != EPI_RAW && EPI != EPI_ACC) {
+        const int en = min(n0 + col, a.n - 1);
+        esw = a.ws[en];
+        if constexpr (EPI == EPI_GLU) esw2 = a.ws2[en];
+#pragma unroll
+        for (int ii = 0; ii < NI; ii++) {
+            const int i = wave + W * ii, mc = min(8 * (i >> 2) + 4 * hi + (i & 3), a.m - 1);
+            esx[ii] = a.as[mc];
+            if constexpr (EPI == EPI_DEQUANT_RES) eres[ii] = a.residual[(int64_t)mc * a.n + en];
+        }
+    }
     v4i af[CH], bf[NB][CH];
 #pragma unroll
     for (int j = 0; j < CH; j++) {
@@ -1620,7 +1639,9 @@ __global__ __launch_bounds__(W * 64) void gemm_rows32_kernel(GemmArgs a) {
     // the tile's 16 x 64 (register i, lane l) elements: wavefront w finishes
     // registers w, w + W, ... of every lane
     const int l = lane;
-    for (int i = wave; i < 16; i += W) {
+#pragma unroll
+    for (int ii = 0; ii < NI; ii++) {
+        const int i = wave + W * ii;
         const int m = 8 * (i >> 2) + 4 * (l >> 5) + (i & 3), n = n0 + (l & 31);
         if (EPI == EPI_ARGMAX) {
             // dequantized logit -> 64-bit key; the 32 columns of row m are the
@@ -1631,7 +1652,7 @@ __global__ __launch_bounds__(W * 64) void gemm_rows32_kernel(GemmArgs a) {
                 int v = 0;
 #pragma unroll
                 for (int w = 0; w < W; w++) v += rows32_lds[(w * 16 + i) * 64 + l];
-                const float lg = (float)v * deq_mult(a.as[m], a.ws[n]);
+                const float lg = (float)v * deq_mult(esx[ii], esw);
                 if (a.y) a.y[(int64_t)m * a.n + n] = lg;
                 k = argmax_key(lg, n);
             }
@@ -1654,13 +1675,13 @@ __global__ __launch_bounds__(W * 64) void gemm_rows32_kernel(GemmArgs a) {
         } else if (EPI == EPI_ACC) {
             __hip_atomic_fetch_add(a.acc + idx, sum[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         } else {
-            const double sx = a.as[m];
-            const float v0 = (float)sum[0] * deq_mult(sx, a.ws[n]);
+            const double sx = esx[ii];
+            const float v0 = (float)sum[0] * deq_mult(sx, esw);
             if (EPI == EPI_GLU) {
-                const float up = (float)sum[NB - 1] * deq_mult(sx, a.ws2[n]);
+                const float up = (float)sum[NB - 1] * deq_mult(sx, esw2);
                 a.y[idx] = tl_silu(v0) * up;
             } else if (EPI == EPI_DEQUANT_RES) {
-                a.y[idx] = a.residual[idx] + v0;
+                a.y[idx] = eres[ii] + v0;
             } else {
                 a.y[idx] = v0;
             }
