@@ -483,14 +483,19 @@ def test_prefill_lengths_tinyllama_shape(n, packed, fuse, monkeypatch):
     eng.close()
 
 
+@pytest.mark.parametrize("geom", [(1024, 3072, 16, 4), (512, 1536, 8, 2)], ids=["hidden1024", "hidden512"])
 @pytest.mark.parametrize("fuse", ["1", "0"], ids=["fused_qkv", "qkv_post"])
-def test_prefill_packed_other_geometry(fuse, monkeypatch):
-    """The packed-operand prefill GEMMs at a second geometry (hidden 1024,
-    FFN 3072, 16 query / 4 KV heads: Q|K|V N = 1536, one 64-row tile per
-    head, the 32 x 160 split tile not taken) with 200 rows: next token, its
-    logit and every K/V row equal token-by-token decode in the oracle."""
+def test_prefill_packed_other_geometry(fuse, geom, monkeypatch):
+    """The packed-operand prefill GEMMs at two more geometries with 200 rows:
+    hidden 1024, FFN 3072, 16 query / 4 KV heads (Q|K|V N = 1536, one 64-row
+    tile per head, the 32 x 160 split tile not taken) and hidden 512, FFN
+    1536, 8 / 2 heads (K = 512: each wavefront's quarter of K is the four
+    register sets loaded before the main loop, which then never runs).  Next
+    token, its logit and every K/V row equal token-by-token decode in the
+    oracle."""
     monkeypatch.setenv("TL_PREFILL_QKV_FUSE", fuse)
-    cfg = dict(oracle.TINYLLAMA_CFG, hidden=1024, intermediate=3072, n_heads=16, n_kv_heads=4, n_layers=2,
+    hidden, ffn, nh, nkv = geom
+    cfg = dict(oracle.TINYLLAMA_CFG, hidden=hidden, intermediate=ffn, n_heads=nh, n_kv_heads=nkv, n_layers=2,
                vocab=2048, max_pos=512)
     m = oracle.synthetic_model(cfg, seed=77)
     n = 200
