@@ -175,6 +175,7 @@ struct AttnDecodeArgs {
     const int32_t* qacc;  // [rows][D + 2 KVD] or null
     const double* qas;    // [rows]
     const float* qws;     // [D + 2 KVD]
+    float* out_max;       // attention_group_kernel: [rows][n_heads] max |output| of each head, or null
 };
 
 // NW wavefronts per workgroup; wavefront w takes key blocks w, w + NW, ...
@@ -879,11 +880,16 @@ __global__ __launch_bounds__(kGW * 64) void attention_group_kernel(AttnDecodeArg
 #pragma unroll
     for (int h = 0; h < HPW; h++) accs[(wave * HPW + h) * 64 + lane] = o[h];
     __syncthreads();
-    if (tid < HPW * 64) {
+    if (tid < HPW * 64) {   // wavefront h: head h0 + h
         const int h = tid >> 6, dd = tid & 63;
         int O = 0;
         for (int w = 0; w < kGW; w++) O += accs[(w * HPW + h) * 64 + dd];
-        p.out[(int64_t)row * D + (int64_t)(h0 + h) * kHeadDim + dd] = (float)O * deq_mult(1.0 / 127.0, sv);
+        const float v = (float)O * deq_mult(1.0 / 127.0, sv);
+        p.out[(int64_t)row * D + (int64_t)(h0 + h) * kHeadDim + dd] = v;
+        if (p.out_max) {   // the head's part of the maximum the O projection quantizes the row at
+            const float m = wave_max_f32(fabsf(v));
+            if (dd == 0) p.out_max[(int64_t)row * p.n_heads + h0 + h] = m;
+        }
     }
 }
 
@@ -987,7 +993,7 @@ bool attention_decode_grouped(int32_t rows, int32_t n_heads, int32_t n_kv, int32
 hipError_t launch_attention_decode(hipStream_t s, const float* qkv, int32_t rows, int32_t n_heads, int32_t n_kv,
                                    RowMap rm, const float* cos, const float* sin, KvGeom kv, int32_t layer,
                                    const float* kv_sk, const float* kv_sv, float* out, int32_t max_t, int32_t hpw,
-                                   unsigned long long* ts, const QkvSums* sums) {
+                                   unsigned long long* ts, const QkvSums* sums, float* out_max) {
     if (rows <= 0) return hipSuccess;
     const int G = n_heads / n_kv;
     if (n_heads % n_kv || G > kMaxGroupHeads || n_heads > 32 * 4) return hipErrorInvalidValue;
@@ -995,6 +1001,8 @@ hipError_t launch_attention_decode(hipStream_t s, const float* qkv, int32_t rows
     const int tpad = (max_t + 63) & ~63;
     AttnDecodeArgs p{qkv, n_heads, n_kv, rm, cos, sin, kv, layer, kv_sk, kv_sv, 1.0 / sqrt((double)kHeadDim), out, ts};
     const bool grouped = attention_decode_grouped(rows, n_heads, n_kv, max_t, hpw);
+    if (out_max && !grouped) return hipErrorInvalidValue;
+    p.out_max = out_max;
     if (sums) {
         if (!grouped || !sums->acc || !sums->as || !sums->ws) return hipErrorInvalidValue;
         p.qacc = sums->acc;

@@ -62,6 +62,7 @@ enum GemvEpi : int {
                           // follows folds the sums and clears them)
     EPI_QKV_ROPE = 7,     // prefill Q|K|V: dequantize, RoPE on Q and K, K / V quantized into the cache,
                           // rotated Q out in float32 with its row maximum (launch_gemm_pk_qkv)
+    EPI_ACC_F32 = 8,      // EPI_ACC with a float32 A that gemm_rows32 quantizes itself (GemmArgs::af)
 };
 
 // activation prologue of the fused decode GEMV
@@ -111,6 +112,14 @@ struct GemmArgs {
     unsigned long long* key;  // EPI_ARGMAX: [N / 32 tiles][M] best key of each tile and row
     const int8_t* ap;         // A in MFMA operand blocks (rows padded to gemm_pk_row_pad()) for
                               // launch_gemm_pk, or null
+    // gemm_rows32 EPI_ACC_F32 only: A is the float32 [M][K] row-major
+    // matrix quantized per row here (quantize_int8, GI:36-42) at the maximum
+    // of the amax_n (a multiple of 4, at most 32) values amax[row][..], the
+    // row's parts' max |x|; the row scales go to as_out (a and as unused)
+    const float* af;
+    const float* amax;
+    int32_t amax_n;
+    double* as_out;
 };
 
 // ---- launchers (tl_kernels.hip) ------------------------------------------
@@ -142,6 +151,8 @@ struct FoldArgs {
     PwPlan plan;
     int8_t* q;            // [rows][n]
     double* scales;       // [rows]
+    int32_t* zero;        // or null: [rows][zero_n] int32 the kernel also clears (consumed integer sums)
+    int32_t zero_n;
 };
 hipError_t launch_rows_fold(hipStream_t s, const FoldArgs& f);
 hipError_t launch_quantize_tensor(hipStream_t s, const float* x, int64_t n, int8_t* q,
@@ -332,10 +343,12 @@ struct QkvSums {
 // launch_attention_decode takes the grouped (many-row) kernel for these
 // arguments; the only path that accepts QkvSums
 bool attention_decode_grouped(int32_t rows, int32_t n_heads, int32_t n_kv, int32_t max_t, int32_t hpw);
+// out_max (the grouped kernel only): [rows][n_heads] max |output| of each head
 hipError_t launch_attention_decode(hipStream_t s, const float* qkv, int32_t rows, int32_t n_heads, int32_t n_kv,
                                    RowMap rm, const float* cos, const float* sin, KvGeom kv, int32_t layer,
                                    const float* kv_sk, const float* kv_sv, float* out, int32_t max_t, int32_t hpw,
-                                   unsigned long long* ts = nullptr, const QkvSums* sums = nullptr);
+                                   unsigned long long* ts = nullptr, const QkvSums* sums = nullptr,
+                                   float* out_max = nullptr);
 hipError_t launch_embed_step(hipStream_t s, const int32_t* tok_by_seq, const int32_t* seq_of_row, int32_t rows,
                              const int32_t* cursor, int32_t* row_pos, int32_t d, int32_t vocab, const int8_t* emb,
                              const float* emb_s, float* x);

@@ -191,6 +191,8 @@ __global__ __launch_bounds__(kNT) void rows_fold_kernel(FoldArgs f) {
     int8_t* qr = f.q + ro;
     for (int o = tid * 16; o < n; o += kNT * 16) *(v4i*)(qr + o) = *(const v4i*)(xs8 + o);
     if (tid == 0) f.scales[row] = xscale;
+    if (f.zero)
+        for (int i = tid * 4; i < f.zero_n; i += kNT * 4) *(v4i*)(f.zero + (int64_t)row * f.zero_n + i) = (v4i){0, 0, 0, 0};
 }
 
 hipError_t launch_rows_fold(hipStream_t s, const FoldArgs& f) {
@@ -199,6 +201,7 @@ hipError_t launch_rows_fold(hipStream_t s, const FoldArgs& f) {
     if (f.n <= 0 || f.n % 64 || f.n > 6 * 1024 || bits % 16 || !f.x || !f.acc || !f.as || !f.ws || !f.g || !f.q ||
         !f.scales || f.plan.n_leaves > 64)
         return hipErrorInvalidValue;
+    if (f.zero && (f.zero_n <= 0 || f.zero_n % 4 || (uintptr_t)f.zero % 16)) return hipErrorInvalidValue;
     const dim3 grid(f.rows), block(kNT);
     switch ((f.n + 1023) / 1024) {
         case 1: TL_KLAUNCH(rows_fold_kernel<1>, grid, block, 0, s, f); break;
@@ -1604,7 +1607,7 @@ __global__ __launch_bounds__(W * 64) void gemm_rows32_kernel(GemmArgs a) {
     constexpr int NI = 16 / W;
     double esx[NI];
     float eres[NI], esw = 0.0f, esw2 = 0.0f;
-    if constexpr (EPI != EPI_RAW && EPI != EPI_ACC) {
+    if constexpr (EPI != EPI_RAW && EPI != EPI_ACC && EPI != EPI_ACC_F32) {
         const int en = min(n0 + col, a.n - 1);
         esw = a.ws[en];
         if constexpr (EPI == EPI_GLU) esw2 = a.ws2[en];
@@ -1616,12 +1619,51 @@ __global__ __launch_bounds__(W * 64) void gemm_rows32_kernel(GemmArgs a) {
         }
     }
     v4i af[CH], bf[NB][CH];
+    if constexpr (EPI == EPI_ACC_F32) {
+        // a float32 A (a.af; one 32-byte K chunk per wavefront,
+        // which the launcher checks): this lane's 16 values of its row are
+        // requested first, then the weights, then quantized as
+        // quantize_rows_kernel does, at the row maximum
+        const int rq = min(col, a.m - 1), cc = min(wave * per, kch - 1);
+        // the row's amax_n maxima: float4 2 q + hi of this lane (clamped;
+        // max is idempotent), the other half-wavefront's in the lane l ^ 32
+        const float4* m4 = (const float4*)(a.amax + (int64_t)rq * a.amax_n);
+        float4 mv[4];
 #pragma unroll
-    for (int j = 0; j < CH; j++) {
-        const int cc = min(wave * per + min(j, per - 1), kch - 1);
-        af[j] = ld16(arow + (int64_t)cc * 32);
+        for (int q = 0; q < 4; q++) mv[q] = m4[min(2 * q + hi, (a.amax_n >> 2) - 1)];
+        const float4* f4 = (const float4*)(a.af + (int64_t)rq * a.k + (int64_t)(c0 + cc) * 32 + hi * 16);
+        float4 fv[4];
 #pragma unroll
-        for (int b = 0; b < NB; b++) bf[b][j] = ld_nt16(wrow[b] + (int64_t)cc * wstep);
+        for (int w = 0; w < 4; w++) fv[w] = f4[w];
+        float mx = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; q++) mx = fmaxf(fmaxf(fmaxf(mx, mv[q].x), fmaxf(mv[q].y, mv[q].z)), mv[q].w);
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+#pragma unroll
+        for (int j = 0; j < CH; j++) {
+            const int ccj = min(wave * per + min(j, per - 1), kch - 1);
+#pragma unroll
+            for (int b = 0; b < NB; b++) bf[b][j] = ld_nt16(wrow[b] + (int64_t)ccj * wstep);
+        }
+        const double s = quant_scale(mx);
+        if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0 && hi == 0 && col < a.m) a.as_out[col] = s;
+        RnDiv dv;
+        dv.b = (float)s;
+        dv.y = __fdiv_rn(1.0f, dv.b);
+        dv.fast = __all(fabsf(dv.b) >= 0x1p-64f && fabsf(dv.b) <= 0x1p64f);
+        // |x| <= max |x| = 127 b (1 + 2^-24) keeps every x y finite
+#pragma unroll
+        for (int w = 0; w < 4; w++) af[0][w] = (int)(dv.fast ? quant4<true>(fv[w], dv) : quant4<false>(fv[w], dv));
+#pragma unroll
+        for (int j = 1; j < CH; j++) af[j] = (v4i){0, 0, 0, 0};   // unused (one chunk)
+    } else {
+#pragma unroll
+        for (int j = 0; j < CH; j++) {
+            const int cc = min(wave * per + min(j, per - 1), kch - 1);
+            af[j] = ld16(arow + (int64_t)cc * 32);
+#pragma unroll
+            for (int b = 0; b < NB; b++) bf[b][j] = ld_nt16(wrow[b] + (int64_t)cc * wstep);
+        }
     }
     v16i acc[NB];
 #pragma unroll
@@ -1672,7 +1714,7 @@ __global__ __launch_bounds__(W * 64) void gemm_rows32_kernel(GemmArgs a) {
         const int64_t idx = (int64_t)m * a.n + n;
         if (EPI == EPI_RAW) {
             a.acc[idx] = sum[0];
-        } else if (EPI == EPI_ACC) {
+        } else if (EPI == EPI_ACC || EPI == EPI_ACC_F32) {
             __hip_atomic_fetch_add(a.acc + idx, sum[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         } else {
             const double sx = esx[ii];
@@ -1719,14 +1761,20 @@ hipError_t launch_gemm_rows32(hipStream_t s, int epi, const GemmArgs& args, int3
     GemmArgs a = args;
     if (a.m < 1 || a.m > 32 || a.n <= 0 || a.k <= 0 || a.k % 64 || a.k > kRowsWaves * kRowsChunks * 32)
         return hipErrorInvalidValue;
-    if (a.k_split <= 0 || a.k_split >= a.k || epi != EPI_ACC) a.k_split = a.k;
+    if (a.k_split <= 0 || a.k_split >= a.k || (epi != EPI_ACC && epi != EPI_ACC_F32)) a.k_split = a.k;
     if (a.k_split % 32) return hipErrorInvalidValue;
-    if (epi == EPI_ACC && !a.acc) return hipErrorInvalidValue;
+    if ((epi == EPI_ACC || epi == EPI_ACC_F32) && !a.acc) return hipErrorInvalidValue;
     if (epi == EPI_ARGMAX && !a.key) return hipErrorInvalidValue;
     const bool pk = a.wp != nullptr;
     if (pk && (a.n % 32 || (epi == EPI_GLU && !a.wp2))) return hipErrorInvalidValue;
+    // a float32 A (quantized in the kernel): the 16-wavefront kernel with one
+    // 32-byte K chunk per wavefront, 16-byte aligned rows
+    if (epi == EPI_ACC_F32 && (!pk || !a.af || !a.a || !a.amax || a.amax_n < 4 || a.amax_n > 32 || a.amax_n % 4 ||
+                                   (uintptr_t)a.amax % 16 || !a.as_out || a.k_split / 32 > kRowsWaves ||
+                 a.k % 4 || (uintptr_t)a.af % 16))
+        return hipErrorInvalidValue;
     const dim3 grid((unsigned)((a.n + 31) / 32), (unsigned)((a.k + a.k_split - 1) / a.k_split));
-    if (pk && (waves == 4 || waves == 8) && a.k_split <= 64 * 32)
+    if (pk && (waves == 4 || waves == 8) && a.k_split <= 64 * 32 && epi != EPI_ACC_F32)
         return waves == 4 ? launch_rows32_w<4>(s, epi, a, grid) : launch_rows32_w<8>(s, epi, a, grid);
     const dim3 block(1024);
     const size_t lds1 = rows32_lds_bytes(1), lds2 = rows32_lds_bytes(2);
@@ -1750,6 +1798,7 @@ hipError_t launch_gemm_rows32(hipStream_t s, int epi, const GemmArgs& args, int3
             break;
         case EPI_RAW: TL_R32(EPI_RAW, lds1); break;
         case EPI_ACC: TL_R32(EPI_ACC, lds1); break;
+        case EPI_ACC_F32: TL_KLAUNCH((gemm_rows32_kernel<EPI_ACC_F32, 4, true>), grid, block, lds1, s, a); break;
         case EPI_ARGMAX:
             if (!shortk) return hipErrorInvalidValue;
             TL_R32P(EPI_ARGMAX, 4, lds1);

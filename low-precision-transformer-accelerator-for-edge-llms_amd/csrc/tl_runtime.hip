@@ -104,6 +104,7 @@ struct tl_handle {
     float* rope_cos = nullptr;
     float* rope_sin = nullptr;
     int32_t rope_n = 0;
+    float* att_max = nullptr;   // [max rows][n_heads]: each head's max |attention output| (batched decode)
     float* kv_sk = nullptr;
     float* kv_sv = nullptr;
     KvGeom kv{};
@@ -172,6 +173,9 @@ struct tl_handle {
     bool qkv_kslice = true;               // batched decode: K-sliced Q|K|V GEMM whose sums the attention
                                           // kernel dequantizes (TL_BATCH_QKV_KSLICE=0 turns it off)
     bool qacc_clean = true;               // false from a Q|K|V EPI_ACC launch until qacc is cleared
+    bool o_fuse = true;                   // batched decode: the O GEMM K-sliced, quantizing the attention output itself
+                                          // at the row maxima the attention kernel leaves; its sums folded by the
+                                          // post-attention RMSNorm (TL_BATCH_O_FUSE=0 turns it off)
     bool qkv_fuse = true;                 // prefill on packed operands: qkv_post's work in the Q|K|V GEMM
                                           // epilogue and Q quantized by the attention kernel
                                           // (TL_PREFILL_QKV_FUSE=0 turns it off)
@@ -679,6 +683,10 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
     const int D = h->D, F = h->F, KVD = h->KVD, QKV = h->QKV;
     const bool ks = decode && kslice_ok(h, L, rows);
     const bool qks = ks && qkv_kslice_ok(h, L, rows, max_t);
+    // the O GEMM K-sliced with the attention output quantized in it (one
+    // 32-byte K chunk per wavefront of the 16-wavefront small-M GEMM)
+    const bool of = qks && h->o_fuse && L.wo_p && c.n_heads <= 32 && c.n_heads % 4 == 0 &&
+                    kslice_len(D, D) / 32 <= 16;
     const bool pk = !decode && prefill_packed(h, L, rows);   // h->a8 in the packed GEMM operand layout
     // prefill tiles on packed operands: qkv_post's work in the Q|K|V GEMM
     // epilogue, rotated Q in h->qkv ([rows][D]) quantized by the attention tiles
@@ -709,7 +717,8 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
         Prof p(h, TL_K_ATTN, (double)rows * c.n_kv_heads * (double)max_t * 128.0 + rows * QKV * 4.0);
         TL_LAUNCH(h, launch_attention_decode(h->stream, h->qkv, rows, c.n_heads, c.n_kv_heads, rowmap(h), h->rope_cos,
                                              h->rope_sin, h->kv, layer, h->kv_sk, h->kv_sv, h->att, max_t,
-                                             G == 8 && h->batch_hpw == 8 ? 8 : 1, nullptr, qks ? &sums : nullptr));
+                                             G == 8 && h->batch_hpw == 8 ? 8 : 1, nullptr, qks ? &sums : nullptr,
+                                             of ? h->att_max : nullptr));
     } else if (fq) {
         Prof p(h, TL_K_ATTN, (double)rows * c.n_kv_heads * (double)max_t * 128.0 + rows * D * 8.0);
         TL_LAUNCH(h, launch_attention_tiles(h->stream, nullptr, nullptr, rows, c.n_heads, c.n_kv_heads, h->rows_seq,
@@ -723,20 +732,43 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
         Prof p(h, TL_K_ATTN, (double)rows * c.n_kv_heads * (double)max_t * 128.0 + rows * D * 5.0);
         TL_LAUNCH(h, rows_attention(h, h->q8, h->qs, rows, layer, h->att, max_t));
     }
-    {
-        // with the Q|K|V sums (or the Q row maxima) consumed, this kernel also
-        // clears them
-        int32_t* zero = qks ? h->qacc : (fq ? (int32_t*)h->qmax : nullptr);
-        Prof p(h, TL_K_NORM, (double)rows * D * 5.0 + (qks ? (double)rows * QKV * 4.0 : 0.0));
-        TL_LAUNCH(h, launch_quantize_rows(h->stream, h->att, rows, D, h->a8, h->as, zero,
-                                          qks ? QKV : (fq ? kQmaxStride : 0), pk));
-        if (qks) h->qacc_clean = true;
-        if (fq) h->qmax_clean = true;
-    }
-    if ((r = linear(h, EPI_DEQUANT_RES, rows, h->a8, h->as, L.wo, L.so, nullptr, nullptr, D, D, h->x, h->x, TL_K_O,
-                    L.wo_p, nullptr, pk)))
-        return r;
-    {
+    if (of) {
+        // the O GEMM K-sliced over the chip, quantizing the float32 attention
+        // output itself at each row's maximum (from the heads' maxima); its
+        // integer sums wait in h->racc for the post-attention RMSNorm, which
+        // adds them to the residual and also clears the Q|K|V sums
+        GemmArgs a{};
+        a.a = h->a8; a.af = h->att; a.amax = h->att_max; a.amax_n = c.n_heads; a.as_out = h->as;
+        a.wp = L.wo_p; a.acc = h->racc; a.m = rows; a.n = D; a.k = D; a.k_split = kslice_len(D, D);
+        h->racc_clean = false;
+        {
+            Prof p(h, TL_K_O, (double)rows * D * 4.0 + (double)D * D + (double)rows * D * 4.0);
+            TL_LAUNCH(h, launch_gemm_rows32(h->stream, EPI_ACC_F32, a, 16));
+        }
+        FoldArgs f{};
+        f.x = h->x; f.acc = h->racc; f.as = h->as; f.ws = L.so; f.g = L.g_post;
+        f.rows = rows; f.n = D; f.eps = c.rms_eps; f.plan = h->plan; f.q = h->a8; f.scales = h->as;
+        f.zero = h->qacc; f.zero_n = QKV;
+        {
+            Prof p(h, TL_K_NORM, (double)rows * D * 13.0 + (double)rows * QKV * 4.0);
+            TL_LAUNCH(h, launch_rows_fold(h->stream, f));
+        }
+        h->racc_clean = true;
+        h->qacc_clean = true;
+    } else {
+        {
+            // with the Q|K|V sums (or the Q row maxima) consumed, this kernel also
+            // clears them
+            int32_t* zero = qks ? h->qacc : (fq ? (int32_t*)h->qmax : nullptr);
+            Prof p(h, TL_K_NORM, (double)rows * D * 5.0 + (qks ? (double)rows * QKV * 4.0 : 0.0));
+            TL_LAUNCH(h, launch_quantize_rows(h->stream, h->att, rows, D, h->a8, h->as, zero,
+                                              qks ? QKV : (fq ? kQmaxStride : 0), pk));
+            if (qks) h->qacc_clean = true;
+            if (fq) h->qmax_clean = true;
+        }
+        if ((r = linear(h, EPI_DEQUANT_RES, rows, h->a8, h->as, L.wo, L.so, nullptr, nullptr, D, D, h->x, h->x, TL_K_O,
+                        L.wo_p, nullptr, pk)))
+            return r;
         Prof p(h, TL_K_NORM, (double)rows * D * 9.0);
         TL_LAUNCH(h, launch_rmsnorm_quant(h->stream, h->x, L.g_post, rows, D, c.rms_eps, h->plan, nullptr, h->a8, h->as,
                                           pk));
@@ -1066,7 +1098,7 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
         (e = dalloc(h, &h->qmax, (size_t)kQmaxStride * R)) ||
         (e = dalloc(h, &h->tokens_out, (size_t)max_seqs * c.max_pos)) ||
         (e = dalloc(h, &h->logit_out, (size_t)max_seqs * c.max_pos)) ||
-        (e = dalloc(h, &h->rope_cos, (size_t)c.max_pos * kHeadDim)) ||
+        (e = dalloc(h, &h->rope_cos, (size_t)c.max_pos * kHeadDim)) || (e = dalloc(h, &h->att_max, (size_t)R * c.n_heads)) ||
         (e = dalloc(h, &h->rope_sin, (size_t)c.max_pos * kHeadDim)) ||
         (e = dalloc(h, &h->kv_sk, (size_t)c.n_layers * c.n_kv_heads)) ||
         (e = dalloc(h, &h->kv_sv, (size_t)c.n_layers * c.n_kv_heads)) ||
@@ -1132,6 +1164,7 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
     if (const char* env = std::getenv("TL_PREFILL_PACKED")) h->prefill_pk = env[0] != '0';
     if (const char* env = std::getenv("TL_PK_GLU_TN")) h->pk_glu_tn = std::atoi(env) == 2 ? 2 : 1;
     if (const char* env = std::getenv("TL_PREFILL_QKV_FUSE")) h->qkv_fuse = env[0] != '0';
+    if (const char* env = std::getenv("TL_BATCH_O_FUSE")) h->o_fuse = env[0] != '0';
     if (const char* env = std::getenv("TL_BATCH_KSLICE")) h->batch_kslice = env[0] != '0';
     if (const char* env = std::getenv("TL_BATCH_QKV_KSLICE")) h->qkv_kslice = env[0] != '0';
     if (const char* env = std::getenv("TL_ROWS32_WAVES")) h->rows32_waves = std::atoi(env);

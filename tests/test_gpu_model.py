@@ -339,18 +339,23 @@ def test_bad_arguments_raise_value_error(small_model):
     eng.close()
 
 
-@pytest.mark.parametrize("kslice,qkv_kslice", [("1", "1"), ("1", "0"), ("0", "1")],
-                         ids=["qkv_and_down_k_sliced", "down_k_sliced", "whole_k"])
+@pytest.mark.parametrize("kslice,qkv_kslice,o_fuse", [("1", "1", "1"), ("1", "1", "0"), ("1", "0", "1"),
+                                                    ("0", "1", "1")],
+                         ids=["o_quantizing_itself", "qkv_and_down_k_sliced", "down_k_sliced", "whole_k"])
 @pytest.mark.parametrize("hpw", ["1", "8"], ids=["head_per_workgroup", "kv_group_per_workgroup"])
-def test_decode_batch_tinyllama_heads(hpw, kslice, qkv_kslice, monkeypatch):
+def test_decode_batch_tinyllama_heads(hpw, kslice, qkv_kslice, o_fuse, monkeypatch):
     """Batched decode with TinyLlama's attention geometry (32 query heads over
     4 KV heads), with one workgroup per query head (default) and with one
     workgroup per KV head covering its 8 query heads (TL_BATCH_HPW=8); the
     down GEMM K-sliced with integer atomic adds folded by the next RMSNorm row
     prologue and the Q|K|V GEMM K-sliced with its sums dequantized by the
-    attention kernel (default), the down GEMM alone K-sliced
-    (TL_BATCH_QKV_KSLICE=0), and whole-K (TL_BATCH_KSLICE=0)."""
+    attention kernel, with the O GEMM K-sliced too, quantizing the attention
+    output itself at the row maxima the attention kernel writes per head
+    (default) or after a quantization kernel (TL_BATCH_O_FUSE=0), the down
+    GEMM alone K-sliced (TL_BATCH_QKV_KSLICE=0), and whole-K
+    (TL_BATCH_KSLICE=0)."""
     monkeypatch.setenv("TL_BATCH_HPW", hpw)
+    monkeypatch.setenv("TL_BATCH_O_FUSE", o_fuse)
     monkeypatch.setenv("TL_BATCH_KSLICE", kslice)
     monkeypatch.setenv("TL_BATCH_QKV_KSLICE", qkv_kslice)
     cfg = dict(oracle.TINYLLAMA_CFG, n_layers=2, vocab=512)
