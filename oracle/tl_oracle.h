@@ -4,7 +4,7 @@
  * TEST INFRASTRUCTURE ONLY.  This is a plain-C restatement of the reference
  * algorithm (model/tinyllama_gemm_int8.py, model/tinyllama.py and the integer
  * contracts of model/export_fpga_vectors.py and rtl/compute/ SystemVerilog leaves).  It is the
- * checker that the HIP path is compared against, and the timed CPU baseline.
+ * reference the HIP path is compared against in the tests, and the timed CPU baseline.
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load it;
  * the product library never links or calls it.
  *
