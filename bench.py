@@ -423,7 +423,7 @@ def main():
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU: this build measures the single-GPU hot path only "
+        print(f"bench.py runs on one GPU: it measures the single-GPU hot path only "
               f"(--gpus {args.gpus} requested; sharding is described, not run)", file=sys.stderr)
         sys.exit(2)
     if args.prompt + args.steps + args.warmup > CFG["max_pos"]:

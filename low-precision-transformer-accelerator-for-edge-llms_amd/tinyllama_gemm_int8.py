@@ -689,7 +689,7 @@ def dump_debug(dump_dir: str, token_ids: list[int], reference_debug: dict[str, A
 
 def maybe_load_tokenizer(model_id: str, local_files_only: bool):
     """A tokenizer from the local cache, or None with a warning (GI:330-337
-    behaviour; this build never downloads one)."""
+    behaviour; nothing is ever downloaded)."""
     try:
         from transformers import AutoTokenizer
         return AutoTokenizer.from_pretrained(model_id, local_files_only=local_files_only)
@@ -852,7 +852,7 @@ def run_analysis(prompt: str | None, token_ids_arg: str | None, weights_path, la
 
 def build_arg_parser():
     """The reference's command line (GI:688-717 flags and defaults; --weights
-    is required here: no archive ships with this build)."""
+    is required here: no weight archive ships with the package)."""
     import argparse
     ap = argparse.ArgumentParser(description="INT8 TinyLlama decoder path on MI355X: float32-vs-INT8 analysis "
                                              "or greedy generation")
