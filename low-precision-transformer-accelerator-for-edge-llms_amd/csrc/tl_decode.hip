@@ -677,8 +677,7 @@ __global__ __launch_bounds__(kGW * 64) void attention_group_kernel(AttnDecodeArg
     const int64_t pl = p.kv.plane(seq, p.layer, g);
     const int8_t* kp = p.kv.k + pl;
     const int8_t* vp = p.kv.v + pl;
-    float* s_buf = gdyn;                                  // [HPW][tpad]
-    int8_t* p8 = (int8_t*)(gdyn + HPW * tpad);            // [HPW][tpad]
+    int8_t* p8 = (int8_t*)gdyn;                           // [HPW][tpad]
     float* bsum = (float*)(p8 + HPW * tpad);              // [HPW][nblk]
     int* accs = (int*)(bsum + HPW * nblk);                // [kGW][HPW][64]
     const float* src = p.qkv + (int64_t)row * W;
@@ -751,7 +750,10 @@ __global__ __launch_bounds__(kGW * 64) void attention_group_kernel(AttnDecodeArg
     const float scl = (float)((s_q * (double)sk) * p.attn_scale);
     __syncthreads();
 
-    // 2) scores (lane <-> key) of this wavefront's blocks for the HPW heads
+    // 2) scores (lane <-> key) of this wavefront's blocks for the HPW heads;
+    //    each lane keeps its keys' scores, then exponentials, in registers
+    //    (key t = 64 (wave + kGW i) + lane in every phase)
+    float se[kGKB][HPW];
     float lmax[HPW];
 #pragma unroll
     for (int h = 0; h < HPW; h++) lmax[h] = -INFINITY;
@@ -776,7 +778,7 @@ __global__ __launch_bounds__(kGW * 64) void attention_group_kernel(AttnDecodeArg
                 S = sdot4v(k2, q4[2], S);
                 S = sdot4v(k3, q4[3], S);
                 const float sc = (float)S * scl;
-                s_buf[h * tpad + t] = sc;
+                se[i][h] = sc;
                 lmax[h] = fmaxf(lmax[h], sc);
             }
         }
@@ -805,8 +807,8 @@ __global__ __launch_bounds__(kGW * 64) void attention_group_kernel(AttnDecodeArg
             for (int h = 0; h < HPW; h++) {
                 float e = 0.0f;
                 if (t < T) {   // x - max <= 0: tl_expf_nonpos is tl_expf there
-                    e = tl_expf_nonpos(s_buf[h * tpad + t] - mh[h]);
-                    s_buf[h * tpad + t] = e;
+                    e = tl_expf_nonpos(se[i][h] - mh[h]);
+                    se[i][h] = e;
                 }
                 const float bs = wave_butterfly_sum(e);
                 if (lane == 0) bsum[h * nblk + b] = bs;
@@ -842,7 +844,7 @@ __global__ __launch_bounds__(kGW * 64) void attention_group_kernel(AttnDecodeArg
                 for (int h = 0; h < HPW; h++) {
                     int8_t pq = 0;
                     if (t < T) {
-                        const float e = s_buf[h * tpad + t];
+                        const float e = se[i][h];
                         const float q = decltype(fst)::value ? rn_div_fast(e, dt[h]) : __fdiv_rn(e, dt[h].b);
                         pq = (int8_t)(int)__builtin_rintf(q * 127.0f);
                     }
@@ -894,7 +896,7 @@ __global__ __launch_bounds__(kGW * 64) void attention_group_kernel(AttnDecodeArg
 }
 
 static size_t group_lds_bytes(int hpw, int tpad) {
-    return (size_t)hpw * tpad * 5 + (size_t)hpw * (tpad / 64) * 4 + (size_t)kGW * hpw * 64 * 4 + 16;
+    return (size_t)hpw * tpad + (size_t)hpw * (tpad / 64) * 4 + (size_t)kGW * hpw * 64 * 4 + 16;
 }
 
 // embedding of each row's current token and the row's position (= its
