@@ -520,7 +520,10 @@ __global__ __launch_bounds__(256) void attention_row_kernel(AttnDecodeArgs p) {
     const v4i* kn4 = (const v4i*)kn[wave];
     const v4i qa = q4[0], qb = q4[1], qc = q4[2], qd = q4[3];
     float lmax = -INFINITY;
-    auto score_block = [&](int b, v4i k0, v4i k1, v4i k2, v4i k3) {
+    // key t = 64 b + lane's score, then exponential, lives in out: a register
+    // for the KPF prefetched blocks of this wavefront, s_buf past them
+    float se[KPF];
+    auto score_block = [&](int b, v4i k0, v4i k1, v4i k2, v4i k3, float& out) {
         const int t = b * 64 + lane;
         if (t < T) {
             if (t == pos) {
@@ -534,13 +537,13 @@ __global__ __launch_bounds__(256) void attention_row_kernel(AttnDecodeArgs p) {
             S = sdot4v(k2, qc, S);
             S = sdot4v(k3, qd, S);
             const float s = (float)S * scl;
-            s_buf[t] = s;
+            out = s;
             lmax = fmaxf(lmax, s);
         }
     };
 #pragma unroll
     for (int i = 0; i < KPF; i++)
-        if (wave + NW * i < nblk) score_block(wave + NW * i, kreg[i][0], kreg[i][1], kreg[i][2], kreg[i][3]);
+        if (wave + NW * i < nblk) score_block(wave + NW * i, kreg[i][0], kreg[i][1], kreg[i][2], kreg[i][3], se[i]);
     for (int b0 = wave + NW * KPF; b0 < nblk; b0 += NW * KB) {
         v4i kk[KB][4];
 #pragma unroll
@@ -551,7 +554,8 @@ __global__ __launch_bounds__(256) void attention_row_kernel(AttnDecodeArgs p) {
         }
 #pragma unroll
         for (int i = 0; i < KB; i++)
-            if (b0 + NW * i < nblk) score_block(b0 + NW * i, kk[i][0], kk[i][1], kk[i][2], kk[i][3]);
+            if (b0 + NW * i < nblk)
+                score_block(b0 + NW * i, kk[i][0], kk[i][1], kk[i][2], kk[i][3], s_buf[(b0 + NW * i) * 64 + lane]);
     }
     lmax = wave_max_f32(lmax);
     if (lane == 0) wmax[wave] = lmax;
@@ -559,16 +563,20 @@ __global__ __launch_bounds__(256) void attention_row_kernel(AttnDecodeArgs p) {
     const float m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
 
     // 4) exponentials and block-64 butterfly sums of this wavefront's keys
-    for (int b = wave; b < nblk; b += NW) {
+    auto exp_block = [&](int b, float& x) {
         const int t = b * 64 + lane;
         float e = 0.0f;
         if (t < T) {   // x - max <= 0: tl_expf_nonpos is tl_expf there
-            e = tl_expf_nonpos(s_buf[t] - m);
-            s_buf[t] = e;
+            e = tl_expf_nonpos(x - m);
+            x = e;
         }
         const float bs = wave_butterfly_sum(e);
         if (lane == 0) bsum[b] = bs;
-    }
+    };
+#pragma unroll
+    for (int i = 0; i < KPF; i++)
+        if (wave + NW * i < nblk) exp_block(wave + NW * i, se[i]);
+    for (int b = wave + NW * KPF; b < nblk; b += NW) exp_block(b, s_buf[b * 64 + lane]);
     __syncthreads();
     const float tot = ordered_sum_aligned(bsum, nblk);   // bsum: 16-byte aligned, 16 bytes of slack
 
@@ -578,15 +586,19 @@ __global__ __launch_bounds__(256) void attention_row_kernel(AttnDecodeArgs p) {
     //    the same keys (lane <-> dimension; this row's V is v8 of lane d)
     const RnDiv dt = rn_div_prep(tot);
     auto probs = [&](auto fast) {
-        for (int b = wave; b < nblk; b += NW) {
+        auto prob_block = [&](int b, const float& x) {
             const int t = b * 64 + lane;
             int8_t pq = 0;
             if (t < T) {
-                const float q = decltype(fast)::value ? rn_div_fast(s_buf[t], dt) : __fdiv_rn(s_buf[t], tot);
+                const float q = decltype(fast)::value ? rn_div_fast(x, dt) : __fdiv_rn(x, tot);
                 pq = (int8_t)(int)__builtin_rintf(q * 127.0f);
             }
             p8[t] = pq;
-        }
+        };
+#pragma unroll
+        for (int i = 0; i < KPF; i++)
+            if (wave + NW * i < nblk) prob_block(wave + NW * i, se[i]);
+        for (int b = wave + NW * KPF; b < nblk; b += NW) prob_block(b, s_buf[b * 64 + lane]);
     };
     if (dt.fast) probs(std::true_type{});
     else probs(std::false_type{});
