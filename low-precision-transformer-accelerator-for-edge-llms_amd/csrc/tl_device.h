@@ -182,6 +182,18 @@ TL_DEV int32_t key_index(unsigned long long key) {
 // ---------------------------------------------------------------------------
 TL_DEV int lane_id() { return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
 
+// The wavefront's index in its workgroup as a wavefront-uniform (scalar)
+// value, for every kernel that issues MFMAs.  MFMA instructions ignore EXEC:
+// with no lane active, or some, an MFMA still multiplies and writes its whole
+// accumulator.  A condition the compiler takes for lane-divergent (anything
+// computed from threadIdx.x) becomes an EXEC mask, and the compiler drops the
+// branch that skips a masked block when the block is short and holds no memory
+// wait (it counts a masked-off instruction as a no-op), so an MFMA guarded by
+// such a condition can run anyway and add a product that was meant to be
+// skipped.  Conditions built from wave_id() and kernel arguments are uniform:
+// they compile to scalar branches, which skip the MFMA for real.
+TL_DEV int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
 // DPP controls
 constexpr int kDppXor1 = 0xB1;          // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;          // quad_perm [2,3,0,1]
@@ -331,7 +343,6 @@ TL_DEV unsigned long long row_value_u64(unsigned long long v, int row) {
     return ((unsigned long long)hi << 32) | lo;
 }
 
-// maximum of 64-bit keys over the wavefront, in every lane
 // Decode-timeline stamps: with ts set, lane 0 of the wavefront stores the
 // GPU clock (wall_clock64, constant rate) read when the kernel reached this
 // object and when the object leaves scope (on every return path) at
@@ -354,6 +365,7 @@ struct WaveStamp {
     }
 };
 
+// maximum of 64-bit keys over the wavefront, in every lane
 TL_DEV unsigned long long wave_max_u64(unsigned long long v) {
     v = row_max_u64(v);
     return max_u64(max_u64(row_value_u64(v, 0), row_value_u64(v, 1)),

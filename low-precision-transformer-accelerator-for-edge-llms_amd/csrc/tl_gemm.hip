@@ -64,7 +64,7 @@ __global__ __launch_bounds__(WM * WN * KS * 64) void gemm32_kernel(GemmArgs a) {
     auto sa = [&](int buf, int i) -> v4i& { return lds[buf * ACH + i]; };
     auto sb = [&](int buf, int b, int i) -> v4i& { return lds[NBUF * ACH + (buf * NB + b) * BCH + i]; };
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int ks = wave / (WM * WN), wt = wave % (WM * WN);
     const int wm = wt / WN, wn = wt % WN;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
@@ -325,7 +325,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_tile_kernel(GemmArgs a) {
     constexpr int STAGE = ACH + NB * BCH;            // chunks per LDS buffer
     __shared__ v4i lds[2 * STAGE];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int wm = wave / WN, wn = wave % WN;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const int nk = a.k / BK;
@@ -728,7 +728,7 @@ __global__ __launch_bounds__(256) void gemm_pk_split_kernel(GemmArgs a, QkvRopeA
     constexpr bool RES = EPI == EPI_DEQUANT_RES;
     extern __shared__ __align__(16) int pk_red[];   // [4 waves][NBLK][16][64]
     const int kc = a.k >> 5, per = kc >> 2;        // chunks of each wavefront (a multiple of PD)
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int mt0 = blockIdx.y * TM, nt0 = blockIdx.x * TN, c0 = wave * per;
     const int8_t* ab = a.ap + lane * 16;
     const int8_t* wb = a.wp + lane * 16;
@@ -893,7 +893,7 @@ __global__ __launch_bounds__(256) void gemm_pk_glu_kernel(GemmArgs a) {
     constexpr int NB = 2, BB = 8 * TN, PWB = BB / 4, NS = kPkGluStages;
     extern __shared__ __align__(16) int8_t pk_glu_lds[];   // [NS][BB][1024]
     const int kc = a.k >> 5, nk = a.k >> 7;                 // 128-byte stages, an even count >= 2
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int mt = blockIdx.y * 4 + wave, nt0 = blockIdx.x * TN;
     const int8_t* ab = a.ap + lane * 16;
     // The A fragment loads are issued from inline asm and waited for by

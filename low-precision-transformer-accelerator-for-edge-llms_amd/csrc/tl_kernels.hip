@@ -362,7 +362,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     __shared__ int4 sa[2][ACH];
     __shared__ int4 sb[2][NB][BCH];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int wm = wave >> 1, wn = wave & 1;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const int kb = blockIdx.z * a.k_split;
@@ -546,7 +546,7 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs a, int32_t sl
     constexpr int NB = EPI == EPI_GLU ? 2 : 1;
     extern __shared__ __align__(16) int8_t skinny_lds[];   // per wavefront: A + NB weight tiles of 32 x 256 bytes
     const int tid = threadIdx.x, lane = tid & 63, col = lane & 31, hi = lane >> 5;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: LDS load bases go to a scalar register
+    const int wave = wave_id();   // uniform: LDS load bases go to a scalar register
     const int tile = blockIdx.x / slices, sl = blockIdx.x % slices;
     const int n0 = tile * 32;
     const int kch = a.k >> 5;
@@ -962,7 +962,7 @@ __global__ __launch_bounds__(256) void attention_tile_kernel(AttnTileArgs p) {
     __shared__ __align__(16) int8_t qs8[32 * 64];   // Q quantized by the workgroup (float32 Q input)
     __shared__ float scl[32], mrow[32], tot[32];
     __shared__ float wmax[4][32];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int col = lane & 31, hi = lane >> 5;
     const int h = blockIdx.x, r0 = (gridDim.y - 1 - blockIdx.y) * 32;   // the longest (last) tiles dispatch first
     const int G = p.n_heads / p.n_kv, g = h / G;
@@ -1582,7 +1582,7 @@ template <int EPI, int CH, bool PK, int W = kRowsWaves>
 __global__ __launch_bounds__(W * 64) void gemm_rows32_kernel(GemmArgs a) {
     constexpr int NB = EPI == EPI_GLU ? 2 : 1;
     extern __shared__ __align__(16) int rows32_lds[];   // [W waves][NB][16][64]
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, col = lane & 31, hi = lane >> 5;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), col = lane & 31, hi = lane >> 5;
     const int n0 = blockIdx.x * 32;
     const int cps = a.k_split >> 5, c0 = blockIdx.y * cps;
     const int kch = min(cps, (a.k >> 5) - c0);   // chunks of this K slice (>= 1)
@@ -1926,7 +1926,7 @@ __global__ __launch_bounds__(256) void attention_tile_reg_kernel(AttnTileArgs p)
     __shared__ __align__(16) int8_t qs8[32 * 64];   // Q quantized by the workgroup (float32 Q input)
     __shared__ float scl[32], tot[32];
     __shared__ float wmax[4][32];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int col = lane & 31, hi = lane >> 5;
     const int h = blockIdx.x, r0 = (gridDim.y - 1 - blockIdx.y) * 32;   // the longest (last) tiles dispatch first
     const int G = p.n_heads / p.n_kv, g = h / G;
