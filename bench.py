@@ -21,8 +21,8 @@ Also reported, on the same model in the same run:
   prefill       512-token prefill (22 layers + LM head + argmax): wall time and
                 per-role GEMM dispatch durations at M = 512, i8 MFMA
                 utilisation against 5.0 POP/s dense
-  eos_watch     decode rate with an EOS id set (the stop flag is read once per
-                16 replayed steps)
+  eos_watch     decode rate with an EOS id set (the host keeps three steps in
+                flight and reads the device's stop flag after every step)
   cpu_baseline  the CPU oracle (tl_oracle.c) decoding the same steps from the
                 same KV cache on all host threads and on one; tokens must equal
                 the GPU's

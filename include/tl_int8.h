@@ -139,7 +139,10 @@ int32_t tl_gemm_i8(tl_handle *h, const int8_t *a, const int8_t *w, int32_t m, in
  * shape whose scratch would exceed it fails with TL_ERR_UNSUPPORTED (no shape
  * tl_gemm_i8 accepts needs more).  Every call on a GPU shares that array and
  * finds the last call's contents (the counters are cleared at the start of
- * each call): calls that overlap on one GPU race.  No profiling events are
+ * each call).  Calls from different handles on one GPU (other streams, other
+ * host threads) are put in order through one event per GPU, created at
+ * tl_create: each call's kernels start after the previous call's have
+ * finished, so overlapping calls do not race.  No profiling events are
  * taken. */
 int32_t tl_gemm_i8_noalloc(tl_handle *h, const int8_t *a, const int8_t *w, int32_t m, int32_t n, int32_t k,
                            int32_t *c);

@@ -17,7 +17,7 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 OUT_DIR = os.path.join(PKG, "_lib")
 LIB = os.path.join(OUT_DIR, "libtl_int8.so")
-SOURCES = ["tl_kernels.hip", "tl_decode.hip", "tl_gemm.hip", "tl_persist.hip", "tl_float.hip", "tl_runtime.hip"]
+SOURCES = ["tl_kernels.hip", "tl_decode.hip", "tl_gemm.hip", "tl_float.hip", "tl_runtime.hip"]
 HEADERS = ["tl_internal.h", "tl_device.h", os.path.join(ROOT, "include", "tl_int8.h")]
 
 # -ffp-contract=off: float32 math rounds exactly where the source (and the

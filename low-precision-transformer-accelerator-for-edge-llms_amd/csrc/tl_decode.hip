@@ -997,16 +997,15 @@ hipError_t launch_gemv_fused(hipStream_t s, int pro, int epi, const GemvArgs& a)
     return hipErrorInvalidValue;
 }
 
-bool attention_decode_grouped(int32_t rows, int32_t n_heads, int32_t n_kv, int32_t max_t, int32_t hpw) {
+bool attention_decode_grouped(int32_t rows, int32_t n_heads, int32_t n_kv, int32_t max_t) {
     if (rows <= 1 || n_kv <= 0 || n_heads % n_kv || n_heads > 32 * 4) return false;
     const int G = n_heads / n_kv, D = n_heads * kHeadDim;
-    return G <= kMaxGroupHeads && G % 4 == 0 && max_t <= kGroupMaxKeys && D <= 4 * kGW * 64 &&
-           (hpw == 1 || (hpw == 8 && G == 8));
+    return G <= kMaxGroupHeads && G % 4 == 0 && max_t <= kGroupMaxKeys && D <= 4 * kGW * 64;
 }
 
 hipError_t launch_attention_decode(hipStream_t s, const float* qkv, int32_t rows, int32_t n_heads, int32_t n_kv,
                                    RowMap rm, const float* cos, const float* sin, KvGeom kv, int32_t layer,
-                                   const float* kv_sk, const float* kv_sv, float* out, int32_t max_t, int32_t hpw,
+                                   const float* kv_sk, const float* kv_sv, float* out, int32_t max_t,
                                    unsigned long long* ts, const QkvSums* sums, float* out_max) {
     if (rows <= 0) return hipSuccess;
     const int G = n_heads / n_kv;
@@ -1014,7 +1013,7 @@ hipError_t launch_attention_decode(hipStream_t s, const float* qkv, int32_t rows
     const int D = n_heads * kHeadDim, W = D + 2 * n_kv * kHeadDim;
     const int tpad = (max_t + 63) & ~63;
     AttnDecodeArgs p{qkv, n_heads, n_kv, rm, cos, sin, kv, layer, kv_sk, kv_sv, 1.0 / sqrt((double)kHeadDim), out, ts};
-    const bool grouped = attention_decode_grouped(rows, n_heads, n_kv, max_t, hpw);
+    const bool grouped = attention_decode_grouped(rows, n_heads, n_kv, max_t);
     if (out_max && !grouped) return hipErrorInvalidValue;
     p.out_max = out_max;
     if (sums) {
@@ -1024,21 +1023,17 @@ hipError_t launch_attention_decode(hipStream_t s, const float* qkv, int32_t rows
         p.qws = sums->ws;
     }
     if (grouped) {
-        // many rows: the grouped kernel, 4 (or 8) query heads per workgroup
-        if (hpw == 8)
-            TL_KLAUNCH((attention_group_kernel<8>), dim3(n_heads / 8, rows), dim3(kGW * 64), group_lds_bytes(8, tpad),
-                       s, p);
-        else
-            TL_KLAUNCH((attention_group_kernel<4>), dim3(n_heads / 4, rows), dim3(kGW * 64), group_lds_bytes(4, tpad),
-                       s, p);
-    } else if (hpw == 1 && n_heads % 4 == 0 && D <= kRowQPerThread * kNT) {
+        // many rows: the grouped kernel, 4 query heads per workgroup (with 8
+        // per workgroup, one per KV head, it measured slower: half the
+        // workgroups, longer phases)
+        TL_KLAUNCH((attention_group_kernel<4>), dim3(n_heads / 4, rows), dim3(kGW * 64), group_lds_bytes(4, tpad), s,
+                   p);
+    } else if (n_heads % 4 == 0 && D <= kRowQPerThread * kNT) {
         const size_t lds = (size_t)tpad * 5 + (tpad / 64) * 4 + 16;
         TL_KLAUNCH((attention_row_kernel<2>), dim3(n_heads, rows), dim3(256), lds, s, p);
-    } else if (hpw == 1) {
+    } else {
         const size_t lds = sizeof(float) * W + (size_t)tpad * 4 + tpad + (tpad / 64) * 4 + 64;
         TL_KLAUNCH((attention_decode_kernel<1, 2, 8, 4>), dim3(n_heads, rows), dim3(256), lds, s, p);
-    } else {
-        return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
@@ -1053,12 +1048,8 @@ hipError_t launch_embed_step(hipStream_t s, const int32_t* tok_by_seq, const int
 }
 
 hipError_t init_decode_kernels() {
-    hipError_t e = hipFuncSetAttribute((const void*)attention_group_kernel<8>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)group_lds_bytes(8, kGroupMaxKeys));
-    if (e != hipSuccess) return e;
-    e = hipFuncSetAttribute((const void*)attention_row_kernel<2>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            120 * 1024);
+    hipError_t e = hipFuncSetAttribute((const void*)attention_row_kernel<2>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 120 * 1024);
     if (e != hipSuccess) return e;
     e = hipFuncSetAttribute((const void*)attention_group_kernel<4>, hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)group_lds_bytes(4, kGroupMaxKeys));

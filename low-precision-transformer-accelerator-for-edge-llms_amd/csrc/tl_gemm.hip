@@ -496,21 +496,15 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_tile_kernel(GemmArgs a) {
         }
 }
 
-// Tile configurations (index = cfg):
-//        waves (M x N x K)  wave tile  block tile  BK   register sets
-//   0:   2 x 2 x 2          32 x 32    64 x 64     128  3    (default)
-//   1:   2 x 2 x 2          64 x 32    128 x 64    128  3
-//   2:   2 x 2 x 2          32 x 64    64 x 128    128  3
-//   3:   2 x 2 x 2          32 x 32    64 x 64     256  3
-// and gemm_tile_kernel (one K slice group, two LDS buffers, one barrier per stage):
-//        waves (M x N)  blocks per wave  block tile  BK   register sets
-//   4:   2 x 2          2 x 2            128 x 128   128  2
-//   5:   2 x 2          2 x 1            128 x 64    128  3
-//   8:   2 x 2          1 x 1            64 x 64     128  4    (default; K a multiple of 128)
-// At M = 512 (one 22-layer TinyLlama prefill, GEMMs bit-identical across all
-// of them) cfg 8 measured fastest: GEMMs 1.41 ms against 1.61 ms for cfg 0;
-// the larger block tiles leave CUs idle at these N and were slower
-// (cfg 4: 2.22 ms).  Without K a multiple of 128, cfg 0 runs.
+// Row-major operands (the tl_gemm_i8 operator, and prefill shapes the packed
+// path does not take), M >= 64, 32x32x32 MFMA tiles:
+//   gemm_tile_kernel, K a multiple of 128: 2 x 2 wavefronts of one 32 x 32
+//     block each (64 x 64 block tile), 128-byte K stages through two LDS
+//     buffers, four register sets;
+//   gemm32_kernel otherwise: 2 x 2 x 2 wavefronts (the K slice split in two
+//     inside the workgroup), 64 x 64 block tile, three register sets.
+// At M = 512 the 64 x 64 tiles measured fastest; larger block tiles leave CUs
+// idle at these N.
 template <int WM, int WN, int TM, int TN, int BK, int PD, int KS, int EPI>
 static void go32(hipStream_t s, const GemmArgs& a, int32_t splits) {
     using G = GemmShape<WM, WN, TM, TN, BK, PD, KS>;
@@ -528,30 +522,25 @@ static bool go_tile(hipStream_t s, const GemmArgs& a) {
 }
 
 template <int EPI>
-static bool shape32(hipStream_t s, const GemmArgs& a, int32_t splits, int cfg) {
-    if (cfg >= 4 && splits != 1) return false;
-    switch (cfg) {
-        case 4: return go_tile<2, 2, 2, 2, 128, 2, EPI>(s, a);
-        case 5: return go_tile<2, 2, 2, 1, 128, 3, EPI>(s, a);
-        case 8: return go_tile<2, 2, 1, 1, 128, 4, EPI>(s, a);
-        case 0: go32<2, 2, 1, 1, 128, 3, 2, EPI>(s, a, splits); return true;
-        case 1: go32<2, 2, 2, 1, 128, 3, 2, EPI>(s, a, splits); return true;
-        case 2: go32<2, 2, 1, 2, 128, 3, 2, EPI>(s, a, splits); return true;
-        case 3: go32<2, 2, 1, 1, 256, 3, 2, EPI>(s, a, splits); return true;
-        default: return false;
-    }
+static bool shape32(hipStream_t s, const GemmArgs& a, bool tile) {
+    if (tile) return go_tile<2, 2, 1, 1, 128, 4, EPI>(s, a);
+    go32<2, 2, 1, 1, 128, 3, 2, EPI>(s, a, 1);
+    return true;
 }
 
-// M >= 64: 32x32x32 MFMA tiles; cfg selects the tile configuration above
-hipError_t launch_gemm32(hipStream_t s, int epi, const GemmArgs& a, int32_t splits, int32_t cfg) {
+// M >= 64, row-major operands, the whole K in one launch: gemm_tile_kernel
+// (tile; K a multiple of 128) or gemm32_kernel
+hipError_t launch_gemm32(hipStream_t s, int epi, const GemmArgs& args, bool tile) {
+    GemmArgs a = args;
     if (a.m <= 0 || a.n <= 0) return hipSuccess;
-    if (a.k <= 0 || a.k % 64 != 0 || a.k_split % 64 != 0 || splits < 1) return hipErrorInvalidValue;
+    if (a.k <= 0 || a.k % 64 != 0 || (tile && a.k % 128)) return hipErrorInvalidValue;
+    a.k_split = a.k;
     bool ok = false;
     switch (epi) {
-        case EPI_DEQUANT: ok = shape32<EPI_DEQUANT>(s, a, splits, cfg); break;
-        case EPI_DEQUANT_RES: ok = shape32<EPI_DEQUANT_RES>(s, a, splits, cfg); break;
-        case EPI_GLU: ok = shape32<EPI_GLU>(s, a, splits, cfg); break;
-        case EPI_RAW: ok = shape32<EPI_RAW>(s, a, splits, cfg); break;
+        case EPI_DEQUANT: ok = shape32<EPI_DEQUANT>(s, a, tile); break;
+        case EPI_DEQUANT_RES: ok = shape32<EPI_DEQUANT_RES>(s, a, tile); break;
+        case EPI_GLU: ok = shape32<EPI_GLU>(s, a, tile); break;
+        case EPI_RAW: ok = shape32<EPI_RAW>(s, a, tile); break;
         default: break;
     }
     if (!ok) return hipErrorInvalidValue;
@@ -1005,16 +994,14 @@ bool gemm_pk_supported(int epi, int32_t m, int32_t n, int32_t k) {
 
 int32_t gemm_pk_row_pad() { return 128; }
 
-hipError_t launch_gemm_pk(hipStream_t s, int epi, const GemmArgs& a, int32_t glu_tn) {
+hipError_t launch_gemm_pk(hipStream_t s, int epi, const GemmArgs& a) {
     if (a.m <= 0) return hipSuccess;
     if (!a.ap || !a.wp || !gemm_pk_supported(epi, a.m, a.n, a.k) || (epi == EPI_GLU && !a.wp2))
         return hipErrorInvalidValue;
     const dim3 block(256);
     const QkvRopeArgs f{};
     if (epi == EPI_GLU) {
-        if (glu_tn == 1)
-            TL_KLAUNCH(gemm_pk_glu_kernel<1>, dim3(a.n / 32, (a.m + 127) / 128), block, pk_glu_lds_bytes(1), s, a);
-        else TL_KLAUNCH(gemm_pk_glu_kernel<2>, dim3(a.n / 64, (a.m + 127) / 128), block, pk_glu_lds_bytes(2), s, a);
+        TL_KLAUNCH(gemm_pk_glu_kernel<1>, dim3(a.n / 32, (a.m + 127) / 128), block, pk_glu_lds_bytes(1), s, a);
         return hipGetLastError();
     }
     const bool res = epi == EPI_DEQUANT_RES;
@@ -1046,11 +1033,10 @@ hipError_t init_gemm_pk_kernels() {
                          (const void*)gemm_pk_split_kernel<1, 5, EPI_DEQUANT_RES>,
                          (const void*)gemm_pk_split_kernel<2, 2, EPI_DEQUANT>,
                          (const void*)gemm_pk_split_kernel<2, 2, EPI_DEQUANT_RES>, (const void*)gemm_pk_glu_kernel<1>,
-                         (const void*)gemm_pk_glu_kernel<2>, (const void*)gemm_pk_split_kernel<2, 2, EPI_QKV_ROPE>};
+                         (const void*)gemm_pk_split_kernel<2, 2, EPI_QKV_ROPE>};
     const size_t bytes[] = {pk_split_lds_bytes(1, 5), pk_split_lds_bytes(1, 5), pk_split_lds_bytes(2, 2),
-                            pk_split_lds_bytes(2, 2), pk_glu_lds_bytes(1), pk_glu_lds_bytes(2),
-                            pk_split_lds_bytes(2, 2)};
-    for (int i = 0; i < 7; i++) {
+                            pk_split_lds_bytes(2, 2), pk_glu_lds_bytes(1), pk_split_lds_bytes(2, 2)};
+    for (int i = 0; i < 6; i++) {
         const hipError_t e = hipFuncSetAttribute(fns[i], hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes[i]);
         if (e != hipSuccess) return e;
     }

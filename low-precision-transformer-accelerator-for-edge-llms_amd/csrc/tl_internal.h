@@ -223,7 +223,14 @@ struct EmbedNext {
     // while it is set a step records nothing and re-embeds the same token at
     // the same position, so further replays leave the state as it is
     const int32_t* eos;  // nullptr: no stop check
-    int32_t* stopped;
+    int32_t* stopped;    // 1 after EOS, 2 after a host abort
+    // host abort (stop_condition_unit.sv:26-28, abort outranks EOS): a word
+    // of pinned host memory the host sets; a step that reads it non-zero
+    // records nothing and sets *stopped = 2.  *stop_host (pinned host
+    // memory) mirrors *stopped for the host's per-step watch.  Null: no
+    // abort check, no mirror.
+    const int32_t* abort_word;
+    int32_t* stop_host;
     unsigned long long* ts;   // decode timeline: [1][2] clock stamps, or null
 };
 hipError_t launch_finalize_tokens(hipStream_t s, unsigned long long* keys, int32_t rows,
@@ -242,66 +249,11 @@ hipError_t init_kernels();
 hipError_t init_decode_kernels();
 hipError_t init_prefill_kernels();
 hipError_t init_skinny_kernels();
-// persistent batch-1 decode (tl_persist.hip)
-struct PLayer {
-    const int8_t* wqkv;
-    const float* sqkv;
-    const int8_t* wo;
-    const float* so;
-    const int8_t* wg;
-    const float* sg;
-    const int8_t* wu;
-    const float* su;
-    const int8_t* wd;
-    const float* sd;
-    const float* g_in;
-    const float* g_post;
-};
-
-struct PersistArgs {
-    const PLayer* layers;
-    int32_t n_layers;
-    const int8_t* lm_w;
-    const float* lm_s;
-    const float* g_final;
-    const int8_t* emb;
-    const float* emb_s;
-    const float* cosb;
-    const float* sinb;
-    KvGeom kv;
-    const float* kv_sk;
-    const float* kv_sv;
-    PwPlan plan;
-    float eps;
-    double attn_scale;
-    int32_t D, F, H, Hkv, V;
-    float* t_qkv;       // [D + 2 KVD]
-    float* t_att;       // [D]
-    float* t_xa;        // [D]  x after the attention block
-    float* t_h;         // [F]
-    float* t_x;         // [D]  layer output
-    unsigned* ctr;      // [8 phases][8 slices][32] producer counters (zero at launch)
-    unsigned long long* keys;  // [max steps] argmax key of each step (zero at launch)
-    unsigned* done;     // [max steps] workgroups that folded their rows into keys[step]
-    unsigned* err;
-    int32_t* status;    // [0] steps completed
-    int32_t seq, n_steps, eos_id, out_stride;
-    int32_t* token_cur;
-    int32_t* cursor;
-    int32_t* n_gen;
-    int32_t* tokens_out;
-    float* logit_out;
-};
-
-size_t persist_lds_bytes(int32_t qkv, int32_t f, int32_t max_pos);
-bool persist_supported(int32_t d, int32_t f, int32_t qkv);
-hipError_t launch_persist_decode(hipStream_t s, const PersistArgs& args, int32_t grid, size_t lds);
 hipError_t launch_fill_u32(hipStream_t s, unsigned* p, int32_t n, unsigned v);
 hipError_t launch_requant_q16(hipStream_t s, const int32_t* acc, const uint32_t* scale, int32_t n, int32_t active,
                               int32_t lanes_per_scale, int32_t nonnegative_only, int8_t* y);
-hipError_t persist_occupancy(int32_t d, int32_t f, size_t lds, int* blocks_per_cu);
 
-hipError_t launch_gemm32(hipStream_t s, int epi, const GemmArgs& a, int32_t splits, int32_t cfg);
+hipError_t launch_gemm32(hipStream_t s, int epi, const GemmArgs& a, bool tile);
 // prefill GEMM on packed A (a.ap) and packed weights (a.wp, a.wp2): DEQUANT,
 // DEQUANT_RES or GLU where gemm_pk_supported(); packed A holds row r's 16-byte
 // piece p (K bytes [16 p, 16 p + 16)) at byte ((r / 32) (K / 32) + p / 2) 1024 +
@@ -329,8 +281,7 @@ struct QkvRopeArgs {
 };
 hipError_t launch_gemm_pk_qkv(hipStream_t s, const GemmArgs& a, const QkvRopeArgs& f);
 int32_t gemm_pk_row_pad();
-// glu_tn: GLU output tiles of 128 x 32 (1) or 128 x 64 (2) columns of each matrix
-hipError_t launch_gemm_pk(hipStream_t s, int epi, const GemmArgs& a, int32_t glu_tn);
+hipError_t launch_gemm_pk(hipStream_t s, int epi, const GemmArgs& a);
 hipError_t init_gemm_pk_kernels();
 hipError_t launch_gemv_fused(hipStream_t s, int pro, int epi, const GemvArgs& a);
 // Q|K|V rows as the integer sums of a K-sliced GEMM with its dequantization
@@ -342,11 +293,11 @@ struct QkvSums {
 };
 // launch_attention_decode takes the grouped (many-row) kernel for these
 // arguments; the only path that accepts QkvSums
-bool attention_decode_grouped(int32_t rows, int32_t n_heads, int32_t n_kv, int32_t max_t, int32_t hpw);
+bool attention_decode_grouped(int32_t rows, int32_t n_heads, int32_t n_kv, int32_t max_t);
 // out_max (the grouped kernel only): [rows][n_heads] max |output| of each head
 hipError_t launch_attention_decode(hipStream_t s, const float* qkv, int32_t rows, int32_t n_heads, int32_t n_kv,
                                    RowMap rm, const float* cos, const float* sin, KvGeom kv, int32_t layer,
-                                   const float* kv_sk, const float* kv_sv, float* out, int32_t max_t, int32_t hpw,
+                                   const float* kv_sk, const float* kv_sv, float* out, int32_t max_t,
                                    unsigned long long* ts = nullptr, const QkvSums* sums = nullptr,
                                    float* out_max = nullptr);
 hipError_t launch_embed_step(hipStream_t s, const int32_t* tok_by_seq, const int32_t* seq_of_row, int32_t rows,

@@ -1239,6 +1239,9 @@ __global__ __launch_bounds__(64) void finalize_tokens_kernel(unsigned long long*
     // and the key before lane 0 may write them.
     constexpr int kFinUnroll = 16;
     const int32_t stop_v = (single && nx.stopped != nullptr) ? *nx.stopped : 0;
+    const int32_t abort_v = (single && nx.abort_word != nullptr)
+                                ? __hip_atomic_load(nx.abort_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)
+                                : 0;
     const unsigned long long key_r = keys[r];
     const int32_t tok_r = token_cur[r], cur_r = cursor[r], gen_r = n_gen[r];
     const int32_t eos = (single && nx.eos) ? *nx.eos : -1;
@@ -1248,7 +1251,9 @@ __global__ __launch_bounds__(64) void finalize_tokens_kernel(unsigned long long*
         const int i = threadIdx.x + 64 * j;
         wk[j] = i < n_wg ? wg_keys[i] : 0ull;
     }
-    const bool halted = stop_v != 0;
+    // a host abort outranks EOS (stop_condition_unit.sv:26-28): a step that
+    // sees it records nothing, even the token that would have been the EOS
+    const bool halted = stop_v != 0 || abort_v != 0;
     int32_t tok, cur;
     if (halted) {
         tok = tok_r;
@@ -1256,6 +1261,10 @@ __global__ __launch_bounds__(64) void finalize_tokens_kernel(unsigned long long*
         if (threadIdx.x == 0) {
             keys[r] = 0ull;
             if (nx.x) *nx.row_pos = cur;
+            if (stop_v == 0 && nx.stopped) {
+                *nx.stopped = 2;
+                if (nx.stop_host) __hip_atomic_store(nx.stop_host, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            }
         }
     } else {
         unsigned long long fold = 0;
@@ -1279,7 +1288,10 @@ __global__ __launch_bounds__(64) void finalize_tokens_kernel(unsigned long long*
             cursor[r] = cur;
             keys[r] = 0ull;
             if (nx.x) *nx.row_pos = cur;
-            if (single && nx.stopped && eos >= 0 && tok == eos) *nx.stopped = 1;
+            if (single && nx.stopped && eos >= 0 && tok == eos) {
+                *nx.stopped = 1;
+                if (nx.stop_host) __hip_atomic_store(nx.stop_host, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            }
         }
     }
     if (nx.x) {
@@ -1733,8 +1745,9 @@ __global__ __launch_bounds__(W * 64) void gemm_rows32_kernel(GemmArgs a) {
 
 static size_t rows32_lds_bytes(int nb, int w = kRowsWaves) { return (size_t)w * nb * 16 * 64 * sizeof(int); }
 
-// the 4- and 8-wavefront variants on packed weights: 64 / W chunks of 32
-// bytes per wavefront, so a K slice of at most 2048 bytes
+// the 8-wavefront variant on packed weights (gate/up: with 8 its GEMM took
+// 225 against 273 us per batched step at 32 x 2048): 8 chunks of 32 bytes per
+// wavefront, so a K slice of at most 2048 bytes
 template <int W>
 static hipError_t launch_rows32_w(hipStream_t s, int epi, const GemmArgs& a, dim3 grid) {
     constexpr int CH = 64 / W;
@@ -1754,9 +1767,9 @@ static hipError_t launch_rows32_w(hipStream_t s, int epi, const GemmArgs& a, dim
 
 // M <= 32, K a multiple of 64 and at most 6144; with packed weights (a.wp,
 // and a.wp2 for the GLU) N must be a multiple of 32.  a.k_split (a multiple
-// of 32, 0 = K) slices K over gridDim.y workgroups for EPI_ACC.  waves = 4 or
-// 8 runs workgroups of that many wavefronts (packed weights, K slice at most
-// 2048 bytes), else 16.
+// of 32, 0 = K) slices K over gridDim.y workgroups for EPI_ACC.  waves = 8
+// runs 8-wavefront workgroups (packed weights, K slice at most 2048 bytes),
+// else 16.
 hipError_t launch_gemm_rows32(hipStream_t s, int epi, const GemmArgs& args, int32_t waves) {
     GemmArgs a = args;
     if (a.m < 1 || a.m > 32 || a.n <= 0 || a.k <= 0 || a.k % 64 || a.k > kRowsWaves * kRowsChunks * 32)
@@ -1774,8 +1787,7 @@ hipError_t launch_gemm_rows32(hipStream_t s, int epi, const GemmArgs& args, int3
                  a.k % 4 || (uintptr_t)a.af % 16))
         return hipErrorInvalidValue;
     const dim3 grid((unsigned)((a.n + 31) / 32), (unsigned)((a.k + a.k_split - 1) / a.k_split));
-    if (pk && (waves == 4 || waves == 8) && a.k_split <= 64 * 32 && epi != EPI_ACC_F32)
-        return waves == 4 ? launch_rows32_w<4>(s, epi, a, grid) : launch_rows32_w<8>(s, epi, a, grid);
+    if (pk && waves == 8 && a.k_split <= 64 * 32 && epi != EPI_ACC_F32) return launch_rows32_w<8>(s, epi, a, grid);
     const dim3 block(1024);
     const size_t lds1 = rows32_lds_bytes(1), lds2 = rows32_lds_bytes(2);
     const bool shortk = a.k_split <= kRowsWaves * 4 * 32;

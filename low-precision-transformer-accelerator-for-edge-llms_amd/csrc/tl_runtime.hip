@@ -8,12 +8,14 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <mutex>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "tl_int8.h"
@@ -45,9 +47,8 @@ struct LayerDev {
     int8_t* wd_p = nullptr;
 };
 
-constexpr int kPersistChunk = 64;   // decode steps per persistent launch at most
-constexpr int kStopChunk = 16;      // decode steps replayed between reads of the stop flag
-constexpr int kPersistCounters = 8 * 8 * 32;   // phases x XCD slices x one 128-byte line
+constexpr int kWatchDepth = 3;      // decode steps (or prefill layers) in flight while the host watches
+                                    // for EOS and a host abort
 
 struct ProfEvent {
     int kclass;
@@ -67,19 +68,33 @@ constexpr size_t kNoAllocPartials = (size_t)512 * 1024;   // int32 elements
 constexpr int32_t kNoAllocCounters = 256;
 static __device__ __align__(256) int32_t scratch[kNoAllocPartials + kNoAllocCounters];
 
+// Every call on a GPU shares that GPU's copy, so calls from different handles
+// (different streams, different host threads) are put in order: under
+// g_scratch_mu a call makes its stream wait for the device's event, launches,
+// and records the event again, so its kernels start after the previous
+// call's have finished.  The event is created with the address lookup (at
+// tl_create), so the entry point itself creates nothing.
 std::mutex g_scratch_mu;
-std::vector<void*> g_scratch_dev;   // device address of `scratch`, by device ordinal
+std::vector<void*> g_scratch_dev;        // device address of `scratch`, by device ordinal
+std::vector<hipEvent_t> g_scratch_done;  // last use of that device's copy
 
-hipError_t scratch_address(int dev, void** out) {
+hipError_t scratch_address(int dev, void** out, hipEvent_t* done) {
     std::lock_guard<std::mutex> lock(g_scratch_mu);
-    if ((int)g_scratch_dev.size() <= dev) g_scratch_dev.resize(dev + 1, nullptr);
+    if ((int)g_scratch_dev.size() <= dev) {
+        g_scratch_dev.resize(dev + 1, nullptr);
+        g_scratch_done.resize(dev + 1, nullptr);
+    }
     if (!g_scratch_dev[dev]) {
         void* p = nullptr;
-        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess) return e;
+        hipEvent_t ev = nullptr;
+        if ((e = hipEventCreateWithFlags(&ev, hipEventDisableTiming)) != hipSuccess) return e;
         g_scratch_dev[dev] = p;
+        g_scratch_done[dev] = ev;
     }
     *out = g_scratch_dev[dev];
+    *done = g_scratch_done[dev];
     return hipSuccess;
 }
 
@@ -124,6 +139,7 @@ struct tl_handle {
     int32_t* tokens = nullptr;    // [max_rows]
     int8_t* kv_stage = nullptr;   // [2][max_pos][64] staging of tl_kv_write / tl_kv_read rows
     int32_t* noalloc_scratch = nullptr;   // this device's copy of `scratch` (tl_gemm_i8_noalloc)
+    hipEvent_t noalloc_done = nullptr;    // the device's event ordering the calls that use it
     float* fscratch = nullptr;    // small scratch
     unsigned long long* op_key = nullptr;  // argmax slot of the standalone LM-head operator
     unsigned long long* lm_wg_keys = nullptr;  // [vocab / 4] batch-1 LM head: argmax key per workgroup
@@ -152,19 +168,18 @@ struct tl_handle {
     float* logit_out = nullptr;      // [max_seqs][max_pos]
     std::vector<int32_t> host_cursor;
     int32_t stop_state[2] = {-1, 0};  // host words copied into eos_id / stopped
+    // pinned host words the device reads and writes: [0] the abort word the
+    // token bookkeeping kernel checks every step, [1 + seq] the mirror of
+    // stopped[seq] it writes (1 EOS, 2 host abort)
+    int32_t* ctl_host = nullptr;      // host view
+    int32_t* ctl_dev = nullptr;       // device view of the same words
+    hipEvent_t watch_ev[kWatchDepth] = {};
     std::vector<int32_t> host_ngen;
 
     std::vector<void*> allocs;
     std::string err;
 
-    bool use_graphs = true;
 
-    // persistent decode (tl_persist.hip)
-    bool use_persist = false;             // TL_PERSIST=1 turns on the single-kernel decode
-    int batch_hpw = 1;                    // query heads per workgroup of multi-row decode attention (TL_BATCH_HPW)
-    int gemm_small = 0;                   // M <= 32 GEMM: 0 one workgroup per tile, 1 split K, 2 16x16x64 tiles (TL_GEMM_SMALL)
-    int rows32_waves = -1;                // wavefronts per workgroup of the packed M <= 32 GEMMs (TL_ROWS32_WAVES;
-                                          // -1: 8 for gate/up, 16 for the others, as measured fastest)
     bool batch_kslice = true;             // batched decode: K-sliced down GEMM folded by the next RMSNorm
                                           // row prologue (TL_BATCH_KSLICE=0 turns it off)
     const float* racc_res_ws = nullptr;   // racc holds a down projection's sums (these weight scales) that
@@ -176,28 +191,9 @@ struct tl_handle {
     bool o_fuse = true;                   // batched decode: the O GEMM K-sliced, quantizing the attention output itself
                                           // at the row maxima the attention kernel leaves; its sums folded by the
                                           // post-attention RMSNorm (TL_BATCH_O_FUSE=0 turns it off)
-    bool qkv_fuse = true;                 // prefill on packed operands: qkv_post's work in the Q|K|V GEMM
-                                          // epilogue and Q quantized by the attention kernel
-                                          // (TL_PREFILL_QKV_FUSE=0 turns it off)
     bool qmax_clean = true;               // false from a fused Q|K|V GEMM until qmax is cleared
     bool rows_one_seq = false;            // the uploaded rows are one sequence at rows_pos0 + r
     int32_t rows_seq = 0, rows_pos0 = 0;
-    bool persist_ok = false;              // geometry and occupancy allow it
-    int32_t persist_grid = 0;             // one workgroup per CU
-    size_t persist_lds = 0;
-    PLayer* d_players = nullptr;          // device copy of the layer pointers
-    bool players_dirty = true;
-    float* t_buf = nullptr;               // exchanged vectors: qkv | att | xa | h | x
-    size_t t_count = 0;
-    unsigned* pctr = nullptr;             // [kPersistCounters] phase counters
-    unsigned long long* pkeys = nullptr;  // [kPersistChunk] argmax key per step
-    unsigned* pdone = nullptr;            // [kPersistChunk]
-    unsigned* perr = nullptr;
-    int32_t* pstatus = nullptr;
-    int gemm_cfg = -1;                    // < 0: choose the MFMA tile configuration per shape
-    bool prefill_pk = true;               // prefill GEMMs on packed A and weights (launch_gemm_pk) where the
-                                          // shapes allow (TL_PREFILL_PACKED=0 turns it off)
-    int pk_glu_tn = 1;                    // their GLU tile: 128 x 32 (1) or 128 x 64 (2) columns (TL_PK_GLU_TN)
     std::vector<hipGraphExec_t> graphs;   // captured batch-1 decode step per sequence
     std::vector<hipGraphExec_t> batch_graphs;   // captured batched decode step, by batch size
 
@@ -386,8 +382,7 @@ struct FixedScratch {
 // wavefronts per workgroup of the packed M <= 32 GEMM: with 8 (8 chunks of
 // 32 bytes each) the gate/up GEMM took 225 against 273 us per batched step at
 // 32 x 2048, while Q|K|V, O and down were 4-12 % slower than with 16
-static int rows32_waves(const tl_handle* h, int epi) {
-    if (h->rows32_waves > 0) return h->rows32_waves;
+static int rows32_waves(int epi) {
     return epi == EPI_GLU ? 8 : 16;
 }
 
@@ -398,31 +393,30 @@ int32_t run_gemm(tl_handle* h, int epi, GemmArgs a, int kclass, const FixedScrat
     if (a.ap) {
         // A was written in the packed operand layout for this GEMM
         Prof p(h, kclass, bytes, prof_ok);
-        TL_LAUNCH(h, launch_gemm_pk(h->stream, epi, a, h->pk_glu_tn));
+        TL_LAUNCH(h, launch_gemm_pk(h->stream, epi, a));
         return TL_OK;
     }
     if (a.m >= 64) {
         // 32x32x32 MFMA tiles: the 64 x 64 block-tiled kernel with 128-byte K
-        // stages (cfg 8) measured fastest at M = 512; K not a multiple of 128
-        // runs the two-K-slice kernel (cfg 0); TL_GEMM_CFG overrides
-        const int cfg = h->gemm_cfg >= 0 ? h->gemm_cfg : (a.k % 128 == 0 ? 8 : 0);
+        // stages when K is a multiple of 128, else the two-K-slice kernel
+        const bool tile = a.k % 128 == 0;
         a.k_split = a.k;
         Prof p(h, kclass, bytes, prof_ok);
-        TL_LAUNCH(h, launch_gemm32(h->stream, epi, a, 1, cfg));
+        TL_LAUNCH(h, launch_gemm32(h->stream, epi, a, tile));
         return TL_OK;
     }
     if (a.m <= 32 && a.wp && (epi != EPI_GLU || (a.wp2 && a.k <= 2048)) && a.k % 64 == 0 && a.k <= 6144 &&
-        a.n % 32 == 0 && h->gemm_small == 0) {
+        a.n % 32 == 0) {
         // batched decode on the packed weight copies: one 16-wavefront
         // workgroup per 32 output columns, every weight load a coalesced 1 KiB
         // (measured faster than splitting K over workgroups: the cross-XCD
         // reduction of the partial tiles costs more than the added bandwidth)
         Prof p(h, kclass, bytes, prof_ok);
-        TL_LAUNCH(h, launch_gemm_rows32(h->stream, epi, a, rows32_waves(h, epi)));
+        TL_LAUNCH(h, launch_gemm_rows32(h->stream, epi, a, rows32_waves(epi)));
         return TL_OK;
     }
     a.wp = a.wp2 = nullptr;
-    if (a.m <= 32 && a.k % 64 == 0 && a.k <= 6144 && h->gemm_small != 2) {
+    if (a.m <= 32 && a.k % 64 == 0 && a.k <= 6144) {
         // batched decode: one 32-row MFMA tile per 32 output columns, K split
         // over enough workgroups to cover the chip, reduced in the kernel
         const int tiles = (a.n + 31) / 32, kch = a.k / 32;
@@ -431,7 +425,7 @@ int32_t run_gemm(tl_handle* h, int epi, GemmArgs a, int kclass, const FixedScrat
         if (tiles > kSkinnyTiles) slices = 1;
         int32_t* part = h->partials;
         unsigned* ctr = h->tile_ctr;
-        const bool skinny = h->gemm_small == 1 || a.k > 2048;
+        const bool skinny = a.k > 2048;
         if (fx) {
             if (skinny && slices > 1) {
                 if ((size_t)tiles * slices * nb * 1024 > fx->part_cap || tiles > fx->ctr_cap)
@@ -548,7 +542,7 @@ int32_t layer_row1(tl_handle* h, int32_t layer, int32_t max_t) {
         Prof p(h, TL_K_ATTN, (double)c.n_heads * max_t * 128.0 + QKV * 4.0 + D * 4.0);
         unsigned long long* ts = ts_take(h, TL_K_ATTN, (int64_t)c.n_heads * 4);
         TL_LAUNCH(h, launch_attention_decode(h->stream, h->qkv, 1, c.n_heads, c.n_kv_heads, rowmap(h), h->rope_cos,
-                                             h->rope_sin, h->kv, layer, h->kv_sk, h->kv_sv, h->att, max_t, 1, ts));
+                                             h->rope_sin, h->kv, layer, h->kv_sk, h->kv_sv, h->att, max_t, ts));
     }
     {
         GemvArgs g = gemv_args(h);
@@ -592,7 +586,7 @@ static int32_t kslice_len(int32_t n, int32_t k) {
 // batched decode can run its down GEMM K-sliced
 static bool kslice_ok(tl_handle* h, const LayerDev& L, int32_t rows) {
     const int D = h->D, F = h->F;
-    return h->batch_kslice && h->gemm_small == 0 && rows > 1 && rows <= 32 && L.wd_p && D % 64 == 0 &&
+    return h->batch_kslice && rows > 1 && rows <= 32 && L.wd_p && D % 64 == 0 &&
            F % 64 == 0 && D <= 6144 && F <= 6144 && h->plan.n_leaves <= 64 && (size_t)rows * D <= h->racc_cap;
 }
 
@@ -600,9 +594,8 @@ static bool kslice_ok(tl_handle* h, const LayerDev& L, int32_t rows) {
 // grouped attention kernel
 static bool qkv_kslice_ok(tl_handle* h, const LayerDev& L, int32_t rows, int32_t max_t) {
     const tl_config& c = h->cfg;
-    const int hpw = c.n_heads / c.n_kv_heads == 8 && h->batch_hpw == 8 ? 8 : 1;
     return h->qkv_kslice && L.wqkv_p && h->QKV % 32 == 0 && (size_t)rows * h->QKV <= h->qacc_cap &&
-           attention_decode_grouped(rows, c.n_heads, c.n_kv_heads, max_t, hpw);
+           attention_decode_grouped(rows, c.n_heads, c.n_kv_heads, max_t);
 }
 
 // integer-sum GEMM into acc (h->racc or h->qacc, zero on entry; EPI_ACC),
@@ -615,7 +608,7 @@ static int32_t linear_acc(tl_handle* h, int32_t rows, const int8_t* wp, int32_t 
     const double bytes = (double)rows * k + (double)n * k + (double)rows * n * 4.0;
     *clean = false;
     Prof p(h, kclass, bytes);
-    TL_LAUNCH(h, launch_gemm_rows32(h->stream, EPI_ACC, a, rows32_waves(h, EPI_ACC)));
+    TL_LAUNCH(h, launch_gemm_rows32(h->stream, EPI_ACC, a, rows32_waves(EPI_ACC)));
     return TL_OK;
 }
 
@@ -643,7 +636,7 @@ static int32_t discard_pending_sums(tl_handle* h) {
 // row kernels then write h->a8 in the packed layout those GEMMs read
 static bool prefill_packed(const tl_handle* h, const LayerDev& L, int32_t rows) {
     const int D = h->D, F = h->F, QKV = h->QKV;
-    return h->prefill_pk && h->gemm_cfg < 0 && rows >= 64 && L.wqkv_p && L.wo_p && L.wg_p && L.wu_p && L.wd_p &&
+    return rows >= 64 && L.wqkv_p && L.wo_p && L.wg_p && L.wu_p && L.wd_p &&
            D % 64 == 0 && F % 64 == 0 && D <= 6144 && F <= 6144 && h->plan.n_leaves <= 64 &&
            gemm_pk_supported(EPI_DEQUANT, rows, QKV, D) && gemm_pk_supported(EPI_DEQUANT_RES, rows, D, D) &&
            gemm_pk_supported(EPI_GLU, rows, F, D) && gemm_pk_supported(EPI_DEQUANT_RES, rows, D, F);
@@ -690,7 +683,7 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
     const bool pk = !decode && prefill_packed(h, L, rows);   // h->a8 in the packed GEMM operand layout
     // prefill tiles on packed operands: qkv_post's work in the Q|K|V GEMM
     // epilogue, rotated Q in h->qkv ([rows][D]) quantized by the attention tiles
-    const bool fq = pk && h->qkv_fuse && h->rows_one_seq && h->rows_pos0 + rows <= kTileMaxKeys && D % 64 == 0 &&
+    const bool fq = pk && h->rows_one_seq && h->rows_pos0 + rows <= kTileMaxKeys && D % 64 == 0 &&
                     KVD % 64 == 0;
     int32_t r;
     if (!ks && (r = discard_pending_sums(h))) return r;
@@ -712,13 +705,11 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
         return r;
     }
     if (decode) {
-        const int G = c.n_heads / c.n_kv_heads;
         const QkvSums sums{h->qacc, h->as, L.sqkv};
         Prof p(h, TL_K_ATTN, (double)rows * c.n_kv_heads * (double)max_t * 128.0 + rows * QKV * 4.0);
         TL_LAUNCH(h, launch_attention_decode(h->stream, h->qkv, rows, c.n_heads, c.n_kv_heads, rowmap(h), h->rope_cos,
-                                             h->rope_sin, h->kv, layer, h->kv_sk, h->kv_sv, h->att, max_t,
-                                             G == 8 && h->batch_hpw == 8 ? 8 : 1, nullptr, qks ? &sums : nullptr,
-                                             of ? h->att_max : nullptr));
+                                             h->rope_sin, h->kv, layer, h->kv_sk, h->kv_sv, h->att, max_t, nullptr,
+                                             qks ? &sums : nullptr, of ? h->att_max : nullptr));
     } else if (fq) {
         Prof p(h, TL_K_ATTN, (double)rows * c.n_kv_heads * (double)max_t * 128.0 + rows * D * 8.0);
         TL_LAUNCH(h, launch_attention_tiles(h->stream, nullptr, nullptr, rows, c.n_heads, c.n_kv_heads, h->rows_seq,
@@ -801,7 +792,9 @@ int32_t lm_head_rows(tl_handle* h, const float* xrow, int32_t rows, int32_t seq,
     unsigned long long* keys = h->keys + (rows == 1 ? seq : 0);
     int32_t n_wg = 0;   // rows == 1: the finalize kernel folds one key per LM-head workgroup
     EmbedNext nx{};     // rows == 1: and embeds the new token into row 0 for the next step
-    if (rows == 1) nx = EmbedNext{h->emb, h->emb_s, h->D, c.vocab, h->x, h->row_pos, h->eos_id + seq, h->stopped + seq};
+    if (rows == 1)
+        nx = EmbedNext{h->emb, h->emb_s, h->D, c.vocab, h->x, h->row_pos, h->eos_id + seq, h->stopped + seq,
+                       h->ctl_dev, h->ctl_dev + 1 + seq, nullptr};
     if (rows == 1) {
         GemvArgs g = gemv_args(h);
         g.xf = xrow; g.gamma = h->g_final; g.w = h->lm_w; g.ws = h->lm_s; g.key = keys; g.n = V; g.k = D;
@@ -823,7 +816,7 @@ int32_t lm_head_rows(tl_handle* h, const float* xrow, int32_t rows, int32_t seq,
         }
         GemmArgs a{};
         a.a = h->a8; a.w = h->lm_w; a.as = h->as; a.ws = h->lm_s; a.y = h->logits; a.m = rows; a.n = V; a.k = D;
-        if (rows <= 32 && h->lm_wp && h->gemm_small == 0 && D % 64 == 0 && D <= 2048) {
+        if (rows <= 32 && h->lm_wp && D % 64 == 0 && D <= 2048) {
             // packed-weight MFMA GEMM with the argmax in its epilogue (one key
             // per 32-column tile and row), then the tiles' keys folded per row
             const int tiles = V / 32;
@@ -833,7 +826,7 @@ int32_t lm_head_rows(tl_handle* h, const float* xrow, int32_t rows, int32_t seq,
             a.key = (unsigned long long*)h->partials;
             a.y = nullptr;
             Prof p(h, TL_K_LMHEAD, (double)V * D + V * 4.0 + (double)rows * D);
-            TL_LAUNCH(h, launch_gemm_rows32(h->stream, EPI_ARGMAX, a, rows32_waves(h, EPI_ARGMAX)));
+            TL_LAUNCH(h, launch_gemm_rows32(h->stream, EPI_ARGMAX, a, rows32_waves(EPI_ARGMAX)));
             TL_LAUNCH(h, launch_argmax_tiles(h->stream, a.key, tiles, rows, keys));
         } else {
             // MFMA GEMM writes logits, a row argmax folds them into keys
@@ -878,6 +871,15 @@ int32_t set_stop_state(tl_handle* h, int32_t seq, int32_t eos_id) {
     return TL_OK;
 }
 
+// clears the abort word when a watched decode or prefill returns (also on an
+// error path), so no later step of another call reads a stale abort
+struct AbortWordReset {
+    tl_handle* h;
+    ~AbortWordReset() {
+        if (h->ctl_host) *(volatile int32_t*)h->ctl_host = 0;
+    }
+};
+
 int32_t check_model_loaded(tl_handle* h) {
     for (size_t l = 0; l < h->layers.size(); l++)
         if (!h->layers[l].wqkv) return fail(h, TL_ERR_BAD_DESCRIPTOR, "layer " + std::to_string(l) + " not loaded");
@@ -903,53 +905,6 @@ int32_t decode_step1(tl_handle* h, int32_t seq, int32_t max_t) {
     for (int l = 0; l < c.n_layers; l++)
         if ((r = layer_row1(h, l, max_t))) return r;
     return lm_head_rows(h, h->x, 1, seq, 1);
-}
-
-// n_steps (<= kPersistChunk) greedy decode steps of sequence seq in one
-// persistent launch; stops after eos_id when it comes.  Waits for the launch.
-int32_t persist_run(tl_handle* h, int32_t seq, int32_t n_steps, int32_t eos_id, int32_t* steps_done) {
-    const tl_config& c = h->cfg;
-    if (h->players_dirty) {
-        std::vector<PLayer> pl(c.n_layers);
-        for (int l = 0; l < c.n_layers; l++) {
-            const LayerDev& L = h->layers[l];
-            pl[l] = PLayer{L.wqkv, L.sqkv, L.wo, L.so, L.wg, L.sg, L.wu, L.su, L.wd, L.sd, L.g_in, L.g_post};
-        }
-        TL_HIP(h, hipMemcpy(h->d_players, pl.data(), sizeof(PLayer) * c.n_layers, hipMemcpyHostToDevice));
-        h->players_dirty = false;
-    }
-    TL_LAUNCH(h, launch_fill_u32(h->stream, h->pctr, kPersistCounters, 0u));
-    TL_LAUNCH(h, launch_reset_keys(h->stream, h->pkeys, n_steps));
-    TL_LAUNCH(h, launch_fill_u32(h->stream, h->pdone, n_steps, 0u));
-    TL_LAUNCH(h, launch_fill_u32(h->stream, h->perr, 1, 0u));
-    PersistArgs a{};
-    a.layers = h->d_players;
-    a.n_layers = c.n_layers;
-    a.lm_w = h->lm_w; a.lm_s = h->lm_s; a.g_final = h->g_final;
-    a.emb = h->emb; a.emb_s = h->emb_s;
-    a.cosb = h->rope_cos; a.sinb = h->rope_sin;
-    a.kv = h->kv; a.kv_sk = h->kv_sk; a.kv_sv = h->kv_sv;
-    a.plan = h->plan; a.eps = c.rms_eps; a.attn_scale = 1.0 / sqrt((double)kHeadDim);
-    a.D = h->D; a.F = h->F; a.H = c.n_heads; a.Hkv = c.n_kv_heads; a.V = c.vocab;
-    a.t_qkv = h->t_buf;
-    a.t_att = a.t_qkv + h->QKV;
-    a.t_xa = a.t_att + h->D;
-    a.t_h = a.t_xa + h->D;
-    a.t_x = a.t_h + h->F;
-    a.ctr = h->pctr;
-    a.keys = h->pkeys; a.done = h->pdone; a.err = h->perr; a.status = h->pstatus;
-    a.seq = seq; a.n_steps = n_steps; a.eos_id = eos_id; a.out_stride = c.max_pos;
-    a.token_cur = h->token_cur; a.cursor = h->cursor; a.n_gen = h->n_gen;
-    a.tokens_out = h->tokens_out; a.logit_out = h->logit_out;
-    TL_LAUNCH(h, launch_persist_decode(h->stream, a, h->persist_grid, h->persist_lds));
-    int32_t st[2] = {0, 0};
-    unsigned err = 0;
-    TL_HIP(h, hipMemcpyAsync(&err, h->perr, sizeof err, hipMemcpyDeviceToHost, h->stream));
-    TL_HIP(h, hipMemcpyAsync(st, h->pstatus, sizeof(int32_t), hipMemcpyDeviceToHost, h->stream));
-    TL_HIP(h, hipStreamSynchronize(h->stream));
-    if (err) return fail(h, TL_ERR_INTERNAL, "persistent decode: a dependency wait timed out");
-    *steps_done = st[0];
-    return TL_OK;
 }
 
 int32_t decode_graph_launch(tl_handle* h, int32_t seq) {
@@ -1113,22 +1068,6 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
     h->kv.n_layers = c.n_layers;
     h->kv.n_kv_heads = c.n_kv_heads;
     h->kv.max_pos = c.max_pos;
-    h->t_count = (size_t)h->QKV + 3 * (size_t)D + (size_t)F;
-    if ((e = dalloc(h, &h->d_players, (size_t)c.n_layers)) || (e = dalloc(h, &h->t_buf, h->t_count)) ||
-        (e = dalloc(h, &h->pkeys, (size_t)kPersistChunk)) || (e = dalloc(h, &h->pdone, (size_t)kPersistChunk)) ||
-        (e = dalloc(h, &h->perr, 1)) || (e = dalloc(h, &h->pstatus, 4)) ||
-        (e = dalloc(h, &h->pctr, (size_t)kPersistCounters)))
-        return bad(e);
-    {
-        // persistent decode: one workgroup per CU, all resident at once, and at
-        // least one workgroup per query head for the attention phase
-        int per_cu = 0;
-        h->persist_grid = prop.multiProcessorCount;
-        h->persist_lds = persist_lds_bytes(h->QKV, F, c.max_pos);
-        h->persist_ok = persist_supported(D, F, h->QKV) && h->persist_grid >= c.n_heads &&
-                        persist_occupancy(D, F, h->persist_lds, &per_cu) == hipSuccess && per_cu >= 1;
-        (void)hipGetLastError();
-    }
     if ((e = hipMemsetAsync(h->kv.k, 0, kv_bytes, h->stream)) || (e = hipMemsetAsync(h->kv.v, 0, kv_bytes, h->stream)) ||
         (e = hipMemsetAsync(h->keys, 0, sizeof(unsigned long long) * max_seqs, h->stream)) ||
         (e = hipMemsetAsync(h->cursor, 0, sizeof(int32_t) * max_seqs, h->stream)) ||
@@ -1148,26 +1087,31 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
     h->rope_n = c.max_pos;
     {
         void* sp = nullptr;
-        if ((e = scratch_address(dev, &sp))) return bad(e);
+        if ((e = scratch_address(dev, &sp, &h->noalloc_done))) return bad(e);
         h->noalloc_scratch = (int32_t*)sp;
+    }
+    {
+        // the abort word and the stop mirrors: pinned, coherent host memory
+        // that the token bookkeeping kernel reads and writes every step
+        void* hp = nullptr;
+        void* dp = nullptr;
+        const size_t words = 1 + (size_t)max_seqs;
+        if ((e = hipHostMalloc(&hp, sizeof(int32_t) * words, hipHostMallocMapped | hipHostMallocCoherent))) return bad(e);
+        h->ctl_host = (int32_t*)hp;
+        std::memset(hp, 0, sizeof(int32_t) * words);
+        if ((e = hipHostGetDevicePointer(&dp, hp, 0))) return bad(e);
+        h->ctl_dev = (int32_t*)dp;
+        for (auto& ev : h->watch_ev)
+            if ((e = hipEventCreateWithFlags(&ev, hipEventDisableTiming))) return bad(e);
     }
     if ((e = init_kernels())) return bad(e);
     if ((e = init_decode_kernels())) return bad(e);
     if ((e = init_prefill_kernels())) return bad(e);
     if ((e = init_gemm_pk_kernels())) return bad(e);
     if ((e = init_skinny_kernels())) return bad(e);
-    if (const char* env = std::getenv("TL_NO_GRAPHS")) h->use_graphs = env[0] == '0';
-    if (const char* env = std::getenv("TL_PERSIST")) h->use_persist = env[0] == '1';
-    if (const char* env = std::getenv("TL_BATCH_HPW")) h->batch_hpw = std::atoi(env) == 8 ? 8 : 1;
-    if (const char* env = std::getenv("TL_GEMM_SMALL")) h->gemm_small = std::atoi(env);
-    if (const char* env = std::getenv("TL_GEMM_CFG")) h->gemm_cfg = std::atoi(env);
-    if (const char* env = std::getenv("TL_PREFILL_PACKED")) h->prefill_pk = env[0] != '0';
-    if (const char* env = std::getenv("TL_PK_GLU_TN")) h->pk_glu_tn = std::atoi(env) == 2 ? 2 : 1;
-    if (const char* env = std::getenv("TL_PREFILL_QKV_FUSE")) h->qkv_fuse = env[0] != '0';
     if (const char* env = std::getenv("TL_BATCH_O_FUSE")) h->o_fuse = env[0] != '0';
     if (const char* env = std::getenv("TL_BATCH_KSLICE")) h->batch_kslice = env[0] != '0';
     if (const char* env = std::getenv("TL_BATCH_QKV_KSLICE")) h->qkv_kslice = env[0] != '0';
-    if (const char* env = std::getenv("TL_ROWS32_WAVES")) h->rows32_waves = std::atoi(env);
     if ((e = hipStreamSynchronize(h->stream))) return bad(e);
     *out = h;
     return TL_OK;
@@ -1186,6 +1130,9 @@ void tl_destroy(tl_handle* h) {
     for (auto g : h->batch_graphs)
         if (g) hipGraphExecDestroy(g);
     for (void* p : h->allocs) hipFree(p);
+    for (auto e : h->watch_ev)
+        if (e) hipEventDestroy(e);
+    if (h->ctl_host) hipHostFree(h->ctl_host);
     if (h->stream) hipStreamDestroy(h->stream);
     delete h;
 }
@@ -1253,7 +1200,6 @@ int32_t tl_load_layer(tl_handle* h, int32_t layer, const int8_t* const w[7], con
         TL_LAUNCH(h, launch_pack_weights(h->stream, L.wu, F, D, L.wu_p));
         TL_LAUNCH(h, launch_pack_weights(h->stream, L.wd, D, F, L.wd_p));
     }
-    h->players_dirty = true;
     return finish(h);
 }
 
@@ -1413,8 +1359,15 @@ int32_t tl_gemm_i8_noalloc(tl_handle* h, const int8_t* a, const int8_t* w, int32
     g.a = a; g.w = w; g.acc = c; g.m = m; g.n = n; g.k = k;
     const FixedScratch fx{h->noalloc_scratch, kNoAllocPartials, (unsigned*)(h->noalloc_scratch + kNoAllocPartials),
                           kNoAllocCounters};
-    int32_t r = run_gemm(h, EPI_RAW, g, TL_K_GEMM_PREFILL, &fx);
-    if (r) return r;
+    {
+        // after the previous user of this GPU's array, from any handle
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        TL_HIP(h, hipStreamWaitEvent(h->stream, h->noalloc_done, 0));
+        const int32_t r = run_gemm(h, EPI_RAW, g, TL_K_GEMM_PREFILL, &fx);
+        const hipError_t e = hipEventRecord(h->noalloc_done, h->stream);
+        if (r) return r;
+        TL_HIP(h, e);
+    }
     return finish(h);
 }
 
@@ -1559,7 +1512,11 @@ namespace {
 
 // embedding + all layers over n prompt tokens of sequence seq (positions
 // 0..n-1); leaves the final hidden rows in h->x
-int32_t prefill_layers(tl_handle* h, int32_t seq, const int32_t* tokens, int32_t n) {
+// With abort_flag, the layers are launched one at a time: layer l + 1 goes out
+// after layer l has finished and the flag has been read (prefill_decode_
+// controller.sv takes HOST_ABORT in every state); *aborted reports a stop.
+int32_t prefill_layers(tl_handle* h, int32_t seq, const int32_t* tokens, int32_t n,
+                       const volatile int32_t* abort_flag = nullptr, bool* aborted = nullptr) {
     const tl_config& c = h->cfg;
     TL_REQ(h, seq >= 0 && seq < h->max_seqs, "sequence out of range");
     TL_REQ(h, tokens && n >= 1, "Input token sequence is empty");
@@ -1567,6 +1524,8 @@ int32_t prefill_layers(tl_handle* h, int32_t seq, const int32_t* tokens, int32_t
     for (int i = 0; i < n; i++) TL_REQ(h, tokens[i] >= 0 && tokens[i] < c.vocab, "token id out of range");
     int32_t r = check_model_loaded(h);
     if (r) return r;
+    h->host_ngen[seq] = 0;   // the sequence is rewritten: no decode until prefill_finish
+    h->host_cursor[seq] = 0;
     if ((r = upload_rows(h, n, seq, false, 0))) return r;
     TL_HIP(h, hipMemcpyAsync(h->tokens, tokens, sizeof(int32_t) * n, hipMemcpyHostToDevice, h->stream));
     const int32_t zero = 0;
@@ -1575,8 +1534,25 @@ int32_t prefill_layers(tl_handle* h, int32_t seq, const int32_t* tokens, int32_t
     TL_LAUNCH(h, launch_reset_keys(h->stream, h->keys + seq, 1));
     if ((r = set_stop_state(h, seq, -1))) return r;
     TL_LAUNCH(h, launch_embed(h->stream, h->tokens, n, h->D, h->cfg.vocab, h->emb, h->emb_s, h->x));
-    for (int l = 0; l < c.n_layers; l++)
+    for (int l = 0; l < c.n_layers; l++) {
+        if (abort_flag) {
+            if (l > 0) {
+                hipEvent_t ev = h->watch_ev[0];
+                hipError_t q;
+                while ((q = hipEventQuery(ev)) == hipErrorNotReady) {
+                    if (*abort_flag) break;
+                    std::this_thread::sleep_for(std::chrono::microseconds(10));
+                }
+                if (q != hipErrorNotReady) TL_HIP(h, q);
+            }
+            if (*abort_flag) {
+                if (aborted) *aborted = true;
+                return finish(h);
+            }
+        }
         if ((r = layer_rows(h, l, n, n, false))) return r;
+        if (abort_flag) TL_HIP(h, hipEventRecord(h->watch_ev[0], h->stream));
+    }
     return TL_OK;
 }
 
@@ -1658,69 +1634,55 @@ int32_t tl_decode(tl_handle* h, int32_t seq, int32_t max_new, int32_t eos_id, co
     if (stop_reason) *stop_reason = TL_STOP_NONE;
     const int32_t first = h->host_ngen[seq];
     int32_t r;
-    if (h->use_persist && h->persist_ok && !h->profiling) {
-        // persistent kernel: up to kPersistChunk steps per launch (one at a
-        // time when the host may abort); EOS is checked on the device
-        int32_t done = 0;
-        while (done < max_new) {
-            if (abort_flag && *abort_flag) {
-                if (stop_reason) *stop_reason = TL_STOP_HOST_ABORT;
-                break;
-            }
-            const int32_t chunk = abort_flag ? 1 : std::min(max_new - done, kPersistChunk);
-            int32_t got = 0;
-            if ((r = persist_run(h, seq, chunk, eos_id, &got))) return r;
-            h->host_cursor[seq] += got;
-            h->host_ngen[seq] += got;
-            done += got;
-            if (got < chunk) break;   // stopped after EOS
-            if (eos_id >= 0) {
-                int32_t last = -1;
-                TL_HIP(h, hipMemcpy(&last, h->tokens_out + (size_t)seq * c.max_pos + first + done - 1, sizeof last,
-                                    hipMemcpyDeviceToHost));
-                if (last == eos_id) break;
-            }
-        }
-        *n_out = done;
-        if (done > 0)
-            TL_HIP(h, hipMemcpy(tokens_out, h->tokens_out + (size_t)seq * c.max_pos + first, sizeof(int32_t) * done,
-                                hipMemcpyDeviceToHost));
-        if (stop_reason && *stop_reason == TL_STOP_NONE)
-            *stop_reason = (eos_id >= 0 && done > 0 && tokens_out[done - 1] == eos_id) ? TL_STOP_EOS : TL_STOP_MAX_TOKENS;
-        return TL_OK;
-    }
-    // graph replays (or direct launches) in chunks: with an EOS id or an abort
-    // flag the stop flag the step sets on the device is read once per chunk
-    // (kStopChunk steps); steps replayed after the stop record nothing
     if ((r = set_stop_state(h, seq, eos_id))) return r;
     if ((r = upload_rows(h, 1, seq, false, h->host_cursor[seq]))) return r;
     if ((r = decode_embed1(h))) return r;
+    auto launch_step = [&](int32_t i) -> int32_t {
+        if (!h->profiling) return decode_graph_launch(h, seq);
+        return decode_step1(h, seq, h->host_cursor[seq] + i + 1);   // profiling: direct launches
+    };
+    volatile int32_t* abort_word = h->ctl_host;
+    volatile int32_t* stop_mirror = h->ctl_host + 1 + seq;
+    AbortWordReset reset_abort{h};
+    *abort_word = 0;
+    *stop_mirror = 0;
     const bool watch = eos_id >= 0 || abort_flag;
-    const int32_t chunk = watch ? kStopChunk : max_new;
     int32_t launched = 0;
-    bool eos_seen = false, aborted = false;
-    while (launched < max_new) {
-        if (abort_flag && *abort_flag) {
-            aborted = true;
-            break;
-        }
-        const int32_t cnt = std::min(chunk, max_new - launched);
-        for (int32_t i = 0; i < cnt; i++) {
-            if (h->use_graphs && !h->profiling) {
-                if ((r = decode_graph_launch(h, seq))) return r;
-            } else if ((r = decode_step1(h, seq, h->host_cursor[seq] + launched + i + 1))) {
-                return r;
+    bool abort_sent = false;
+    if (!watch) {
+        for (; launched < max_new; launched++)
+            if ((r = launch_step(launched))) return r;
+    } else {
+        // kWatchDepth steps in flight: the host waits for the oldest, polling
+        // the caller's abort flag, and after every step reads the mirror of the
+        // device's stop flag.  A raised abort flag goes to the abort word the
+        // token bookkeeping kernel reads, so the steps still in flight record
+        // nothing from then on (at most the step whose bookkeeping already ran
+        // records its token), and no further step is launched.
+        auto poll_abort = [&]() {
+            if (!abort_sent && abort_flag && *abort_flag) {
+                *abort_word = 1;
+                abort_sent = true;
             }
-        }
-        launched += cnt;
-        if (watch) {
-            TL_HIP(h, hipMemcpyAsync(&h->stop_state[1], h->stopped + seq, sizeof(int32_t), hipMemcpyDeviceToHost,
-                                     h->stream));
-            if ((r = finish(h))) return r;
-            if (h->stop_state[1]) {
-                eos_seen = true;
-                break;
+        };
+        poll_abort();
+        int32_t done = 0, dev_stop = 0;
+        for (;;) {
+            while (!abort_sent && dev_stop == 0 && launched < max_new && launched - done < kWatchDepth) {
+                if ((r = launch_step(launched))) return r;
+                TL_HIP(h, hipEventRecord(h->watch_ev[launched % kWatchDepth], h->stream));
+                launched++;
             }
+            if (done == launched) break;
+            hipError_t q;
+            while ((q = hipEventQuery(h->watch_ev[done % kWatchDepth])) == hipErrorNotReady) {
+                poll_abort();
+                std::this_thread::sleep_for(std::chrono::microseconds(20));
+            }
+            TL_HIP(h, q);
+            done++;
+            dev_stop = *stop_mirror;
+            poll_abort();
         }
     }
     int32_t ngen = 0;
@@ -1734,8 +1696,13 @@ int32_t tl_decode(tl_handle* h, int32_t seq, int32_t max_new, int32_t eos_id, co
     if (got > 0)
         TL_HIP(h, hipMemcpy(tokens_out, h->tokens_out + (size_t)seq * c.max_pos + first, sizeof(int32_t) * got,
                             hipMemcpyDeviceToHost));
+    // 1: the device recorded EOS (and then stopped checking); 2: it saw the
+    // abort word first; an abort raised before any step ran records nothing
+    const int32_t dstop = watch ? *stop_mirror : 0;
     if (stop_reason)
-        *stop_reason = eos_seen ? TL_STOP_EOS : (aborted ? TL_STOP_HOST_ABORT : TL_STOP_MAX_TOKENS);
+        *stop_reason = dstop == 1   ? TL_STOP_EOS
+                       : dstop == 2 ? TL_STOP_HOST_ABORT
+                                    : (abort_sent && got < max_new ? TL_STOP_HOST_ABORT : TL_STOP_MAX_TOKENS);
     return TL_OK;
 }
 
@@ -1753,8 +1720,14 @@ int32_t tl_generate(tl_handle* h, int32_t seq, const int32_t* prompt, int32_t n_
         return TL_OK;
     }
     int32_t first = 0;
-    int32_t r = tl_prefill(h, seq, prompt, n_prompt, &first, nullptr);
+    bool aborted = false;
+    int32_t r = prefill_layers(h, seq, prompt, n_prompt, abort_flag, &aborted);
     if (r) return r;
+    if (aborted) {
+        if (stop_reason) *stop_reason = TL_STOP_HOST_ABORT;
+        return TL_OK;
+    }
+    if ((r = prefill_finish(h, seq, n_prompt, &first, nullptr))) return r;
     tokens_out[0] = first;
     *n_out = 1;
     if (eos_id >= 0 && first == eos_id) {
@@ -1795,7 +1768,7 @@ int32_t tl_decode_batch(tl_handle* h, int32_t n_seqs, const int32_t* tokens, con
     // the first step runs eagerly (it sizes the scratch the LM head's tile
     // keys need), the rest replay the captured step
     for (int step = 0; step < n_steps; step++) {
-        if (step > 0 && h->use_graphs && !h->profiling) {
+        if (step > 0 && !h->profiling) {
             if ((r = batch_graph_launch(h, n_seqs))) return r;
         } else if ((r = batch_step(h, n_seqs, max_t))) {
             return r;

@@ -532,7 +532,8 @@ void or_decode_rows(const or_model *m, int32_t layer, int32_t rows, const int32_
     float *a = (float *)malloc(sizeof(float) * (size_t)rows * D);
     int8_t *a8 = (int8_t *)malloc((size_t)rows * KF);
     double *sa = (double *)malloc(sizeof(double) * (size_t)rows);
-    int32_t *acc = (int32_t *)malloc(sizeof(int32_t) * (size_t)rows * F);
+    /* the widest projection output: Q (D), gate / up (F) */
+    int32_t *acc = (int32_t *)malloc(sizeof(int32_t) * (size_t)rows * KF);
     float *qkv = (float *)malloc(sizeof(float) * (size_t)rows * QKV);
     int8_t *q8 = (int8_t *)malloc((size_t)rows * D);
     double *sq = (double *)malloc(sizeof(double) * (size_t)rows);

@@ -86,24 +86,81 @@ def generation_128_256(full):
     return prompt, want, cache
 
 
-@pytest.mark.parametrize("persist", ["0", "1"], ids=["graph", "persistent"])
-def test_generate_128_plus_256_22_layers(full, generation_128_256, persist, monkeypatch):
-    """Both batch-1 decode paths: the captured per-layer kernels replayed as a
-    HIP graph, and the single persistent kernel (TL_PERSIST=1)."""
-    eng, arrays, _ = full
+def test_generate_128_plus_256_22_layers(full, generation_128_256):
+    """Batch-1 decode: the captured per-layer kernels replayed as a HIP graph
+    give every token id and K/V row of the oracle's generation."""
+    eng, _, _ = full
     prompt, want, cache = generation_128_256
-    if persist == "1":
-        from lpta.engine import Engine
-        monkeypatch.setenv("TL_PERSIST", "1")
-        eng = Engine(FULL, max_seqs=1).load_model(arrays)
-    try:
-        got, stop = eng.generate(prompt, 256, seq=0)
-        assert stop == "max_tokens"
-        assert_bits_equal(got, want, "token ids")
-        check_kv(eng, 0, cache, 0, 128 + 255, "generation")
-    finally:
-        if persist == "1":
-            eng.close()
+    got, stop = eng.generate(prompt, 256, seq=0)
+    assert stop == "max_tokens"
+    assert_bits_equal(got, want, "token ids")
+    check_kv(eng, 0, cache, 0, 128 + 255, "generation")
+
+
+def _abort_after(flag, delay_s, stamp):
+    import threading
+
+    def run():
+        time.sleep(delay_s)
+        flag.value = 1
+        stamp.append(time.perf_counter())
+
+    t = threading.Thread(target=run)
+    t.start()
+    return t
+
+
+def test_host_abort_stops_decode_within_steps(full, generation_128_256):
+    """A host abort raised during batch-1 decode (stop_condition_unit.sv:18-37,
+    HOST_ABORT outranks EOS): the decode stops with reason host_abort, the
+    tokens it did record are the oracle's greedy ids, and it returns within a
+    few steps of the flag (each 22-layer step is about 0.5 ms; the abort word
+    is read by every step's token bookkeeping and the host keeps at most three
+    steps in flight).  The same sequence then decodes on from where it
+    stopped, so no abort is left behind."""
+    import ctypes
+    eng, _, orc = full
+    prompt, want, _ = generation_128_256
+    eng.prefill(prompt, seq=1)
+    flag = ctypes.c_int32(0)
+    stamp = []
+    th = _abort_after(flag, 0.04, stamp)
+    got, stop = eng.decode(1500, seq=1, abort_flag=flag)
+    t_ret = time.perf_counter()
+    th.join()
+    latency_ms = (t_ret - stamp[0]) * 1e3
+    log(f"abort after {got.size} decode steps; returned {latency_ms:.2f} ms after the flag")
+    assert stop == "host_abort"
+    assert 0 < got.size < 1500
+    assert_bits_equal(got[:min(got.size, 255)], want[1:1 + min(got.size, 255)], "ids before the abort")
+    assert latency_ms < 4.0
+    more, stop2 = eng.decode(3, seq=1)
+    assert stop2 == "max_tokens" and more.size == 3
+
+
+def test_host_abort_stops_prefill_between_layers(full):
+    """tl_generate with an abort flag launches the prefill one layer at a time
+    and reads the flag between layers: an abort raised during a 2000-token
+    prefill (about 0.4 ms per layer) returns host_abort with no token within
+    about a layer, and the handle then generates normally."""
+    import ctypes
+    eng, _, orc = full
+    prompt = np.random.default_rng(8).integers(0, FULL["vocab"], 2000).astype(np.int32)
+    flag = ctypes.c_int32(0)
+    stamp = []
+    th = _abort_after(flag, 0.003, stamp)
+    got, stop = eng.generate(prompt, 8, seq=2, abort_flag=flag)
+    t_ret = time.perf_counter()
+    th.join()
+    latency_ms = (t_ret - stamp[0]) * 1e3 if stamp else 0.0
+    log(f"prefill abort: {stop}, returned {latency_ms:.2f} ms after the flag")
+    assert stop == "host_abort" and got.size == 0
+    assert latency_ms < 2.0
+    short = prompt[:16]
+    got2, stop2 = eng.generate(short, 4, seq=2, abort_flag=ctypes.c_int32(0))
+    want2, _ = orc.generate(short, 4)
+    assert stop2 == "max_tokens"
+    assert_bits_equal(got2, want2, "ids after the aborted prefill")
 
 
 def test_decode_batch_32x2048_22_layers(full):

@@ -109,14 +109,7 @@ def small_model():
     return oracle.synthetic_model(dict(oracle.SMALL_CFG), seed=11)
 
 
-# the two batch-1 decode paths: per-layer kernels replayed as a HIP graph
-# (default) and the single persistent kernel (TL_PERSIST=1 at engine creation)
-DECODE_PATHS = pytest.mark.parametrize("persist", ["0", "1"], ids=["graph", "persistent"])
-
-
-@DECODE_PATHS
-def test_generate_matches_oracle(small_model, persist, monkeypatch):
-    monkeypatch.setenv("TL_PERSIST", persist)
+def test_generate_matches_oracle(small_model):
     eng = engine_for(small_model)
     prompt = np.array([5, 17, 1000, 3, 3, 2047, 64], np.int32)
     got, stop = eng.generate(prompt, 24)
@@ -126,12 +119,10 @@ def test_generate_matches_oracle(small_model, persist, monkeypatch):
     eng.close()
 
 
-@DECODE_PATHS
-def test_interleaved_sequences_match_oracle(small_model, persist, monkeypatch):
+def test_interleaved_sequences_match_oracle(small_model):
     """Batch-1 decode of two sequences in turns (3 steps of A, 5 of B, 4 of A,
     2 of B): every call starts from its own sequence's token and cursor, so
     each continuation equals the oracle's greedy generation of that prompt."""
-    monkeypatch.setenv("TL_PERSIST", persist)
     eng = engine_for(small_model, max_seqs=2)
     prompts = [np.array([5, 17, 1000, 3, 3, 2047, 64], np.int32), np.array([9, 8, 7, 300, 1], np.int32)]
     got = [[], []]
@@ -171,10 +162,8 @@ def test_prefill_cache_equals_sequential_decode(small_model):
     eng.close()
 
 
-@DECODE_PATHS
-def test_generate_eos_and_abort(small_model, persist, monkeypatch):
+def test_generate_eos_and_abort(small_model):
     import ctypes
-    monkeypatch.setenv("TL_PERSIST", persist)
     eng = engine_for(small_model)
     prompt = np.array([1, 2, 3], np.int32)
     free, _ = eng.generate(prompt, 12)
@@ -188,12 +177,10 @@ def test_generate_eos_and_abort(small_model, persist, monkeypatch):
     eng.close()
 
 
-@DECODE_PATHS
-def test_decode_continues_after_eos_stop(small_model, persist, monkeypatch):
+def test_decode_continues_after_eos_stop(small_model):
     """Steps replayed after the EOS stop record nothing and leave the cache
     and cursor as they were: decoding on from the stop gives the oracle's
     greedy continuation of the same sequence (EOS fed back like any token)."""
-    monkeypatch.setenv("TL_PERSIST", persist)
     eng = engine_for(small_model)
     prompt = np.array([3, 1, 4, 1, 5, 9, 2, 6], np.int32)
     free, _ = eng.generate(prompt, 30)
@@ -230,35 +217,6 @@ def test_decode_batch_matches_oracle(small_model):
                 x = orc.decode_row(layer, int(start[b]) + s, x, kc, vc)
             tok, _ = orc.lm_head(x)
             assert got[b, s] == tok, f"seq {b} step {s}"
-    eng.close()
-
-
-@pytest.mark.parametrize("waves", ["4", "16"])
-def test_decode_batch_rows32_waves(waves, monkeypatch):
-    """The packed M <= 32 GEMMs with 4 or 16 wavefronts per workgroup
-    (TL_ROWS32_WAVES; by default 8 for gate/up and 16 for the others) give the
-    oracle's batched greedy ids at TinyLlama's head geometry."""
-    monkeypatch.setenv("TL_ROWS32_WAVES", waves)
-    cfg = dict(oracle.TINYLLAMA_CFG, n_layers=2, vocab=512)
-    m = oracle.synthetic_model(cfg, seed=8)
-    B, steps = 5, 3
-    eng = engine_for(m, max_seqs=B)
-    start = np.array([3, 70, 129, 600, 1500], np.int32)
-    toks = np.array([4, 77, 300, 511, 0], np.int32)
-    caches = []
-    for b in range(B):
-        kc, vc = m.new_cache()
-        fill_cache_random(eng, m, b, int(start[b]), seed=500 + b, kc=kc, vc=vc)
-        caches.append((kc, vc))
-    got = eng.decode_batch(toks, start, steps)
-    orc = oracle.Oracle(m)
-    x = np.stack([orc.embed(int(t)) for t in toks]).astype(F32)
-    for s in range(steps):
-        for layer in range(cfg["n_layers"]):
-            orc.decode_rows(layer, start + s, x, caches)
-        want, _ = orc.lm_head_rows(x)
-        assert_bits_equal(got[:, s], want, f"ids of step {s}")
-        x = np.stack([orc.embed(int(t)) for t in want]).astype(F32)
     eng.close()
 
 
@@ -342,11 +300,9 @@ def test_bad_arguments_raise_value_error(small_model):
 @pytest.mark.parametrize("kslice,qkv_kslice,o_fuse", [("1", "1", "1"), ("1", "1", "0"), ("1", "0", "1"),
                                                     ("0", "1", "1")],
                          ids=["o_quantizing_itself", "qkv_and_down_k_sliced", "down_k_sliced", "whole_k"])
-@pytest.mark.parametrize("hpw", ["1", "8"], ids=["head_per_workgroup", "kv_group_per_workgroup"])
-def test_decode_batch_tinyllama_heads(hpw, kslice, qkv_kslice, o_fuse, monkeypatch):
+def test_decode_batch_tinyllama_heads(kslice, qkv_kslice, o_fuse, monkeypatch):
     """Batched decode with TinyLlama's attention geometry (32 query heads over
-    4 KV heads), with one workgroup per query head (default) and with one
-    workgroup per KV head covering its 8 query heads (TL_BATCH_HPW=8); the
+    4 KV heads, 4 query heads per attention workgroup): the
     down GEMM K-sliced with integer atomic adds folded by the next RMSNorm row
     prologue and the Q|K|V GEMM K-sliced with its sums dequantized by the
     attention kernel, with the O GEMM K-sliced too, quantizing the attention
@@ -354,7 +310,6 @@ def test_decode_batch_tinyllama_heads(hpw, kslice, qkv_kslice, o_fuse, monkeypat
     (default) or after a quantization kernel (TL_BATCH_O_FUSE=0), the down
     GEMM alone K-sliced (TL_BATCH_QKV_KSLICE=0), and whole-K
     (TL_BATCH_KSLICE=0)."""
-    monkeypatch.setenv("TL_BATCH_HPW", hpw)
     monkeypatch.setenv("TL_BATCH_O_FUSE", o_fuse)
     monkeypatch.setenv("TL_BATCH_KSLICE", kslice)
     monkeypatch.setenv("TL_BATCH_QKV_KSLICE", qkv_kslice)
@@ -454,19 +409,13 @@ def test_prefill_512_tinyllama_shape():
     eng.close()
 
 
-@pytest.mark.parametrize("packed,fuse", [("1", "1"), ("1", "0"), ("0", "1")],
-                         ids=["packed_fused_qkv", "packed", "row_major"])
 @pytest.mark.parametrize("n", [64, 100, 300])
-def test_prefill_lengths_tinyllama_shape(n, packed, fuse, monkeypatch):
+def test_prefill_lengths_tinyllama_shape(n):
     """Prefills whose length is not a multiple of the GEMM row tiles (the
-    packed-operand GEMMs pad A to 128 rows; TL_PREFILL_PACKED=0 runs the
-    row-major kernels; by default the packed Q|K|V GEMM also rotates,
-    quantizes and appends K/V and leaves Q for the attention tiles to
-    quantize, TL_PREFILL_QKV_FUSE=0 keeps qkv_post) on a 2-layer
-    TinyLlama-shape model: next token, its logit and every K/V row equal
-    token-by-token decode in the oracle."""
-    monkeypatch.setenv("TL_PREFILL_PACKED", packed)
-    monkeypatch.setenv("TL_PREFILL_QKV_FUSE", fuse)
+    packed-operand GEMMs pad A to 128 rows; the packed Q|K|V GEMM also
+    rotates, quantizes and appends K/V and leaves Q for the attention tiles to
+    quantize) on a 2-layer TinyLlama-shape model: next token, its logit and
+    every K/V row equal token-by-token decode in the oracle."""
     cfg = dict(oracle.TINYLLAMA_CFG, n_layers=2, vocab=4096)
     m = oracle.synthetic_model(cfg, seed=40 + n)
     prompt = np.random.default_rng(n).integers(0, cfg["vocab"], n).astype(np.int32)
@@ -488,17 +437,18 @@ def test_prefill_lengths_tinyllama_shape(n, packed, fuse, monkeypatch):
     eng.close()
 
 
-@pytest.mark.parametrize("geom", [(1024, 3072, 16, 4), (512, 1536, 8, 2)], ids=["hidden1024", "hidden512"])
-@pytest.mark.parametrize("fuse", ["1", "0"], ids=["fused_qkv", "qkv_post"])
-def test_prefill_packed_other_geometry(fuse, geom, monkeypatch):
-    """The packed-operand prefill GEMMs at two more geometries with 200 rows:
+@pytest.mark.parametrize("geom", [(1024, 3072, 16, 4), (512, 1536, 8, 2), (384, 1280, 6, 2)],
+                         ids=["hidden1024", "hidden512", "hidden384_row_major"])
+def test_prefill_other_geometry(geom):
+    """Prefill of 200 rows at three more geometries.  Packed-operand GEMMs:
     hidden 1024, FFN 3072, 16 query / 4 KV heads (Q|K|V N = 1536, one 64-row
     tile per head, the 32 x 160 split tile not taken) and hidden 512, FFN
     1536, 8 / 2 heads (K = 512: each wavefront's quarter of K is the four
-    register sets loaded before the main loop, which then never runs).  Next
-    token, its logit and every K/V row equal token-by-token decode in the
-    oracle."""
-    monkeypatch.setenv("TL_PREFILL_QKV_FUSE", fuse)
+    register sets loaded before the main loop, which then never runs).
+    Row-major GEMMs: hidden 384, FFN 1280 (K not a multiple of 512, so the
+    packed path is not taken; Q|K|V post-processing in qkv_post_kernel, Q
+    quantized there).  Next token, its logit and every K/V row equal
+    token-by-token decode in the oracle."""
     hidden, ffn, nh, nkv = geom
     cfg = dict(oracle.TINYLLAMA_CFG, hidden=hidden, intermediate=ffn, n_heads=nh, n_kv_heads=nkv, n_layers=2,
                vocab=2048, max_pos=512)
@@ -523,12 +473,10 @@ def test_prefill_packed_other_geometry(fuse, geom, monkeypatch):
     eng.close()
 
 
-@DECODE_PATHS
-def test_generate_tinyllama_shape_matches_oracle(persist, monkeypatch):
+def test_generate_tinyllama_shape_matches_oracle():
     """Greedy generation on a 2-layer TinyLlama-shape model (hidden 2048, FFN
     5632, 32/4 heads, vocab 32000), on either decode path: the oracle's token
     ids and KV rows."""
-    monkeypatch.setenv("TL_PERSIST", persist)
     cfg = dict(oracle.TINYLLAMA_CFG, n_layers=2)
     m = oracle.synthetic_model(cfg, seed=31)
     prompt = np.random.default_rng(9).integers(0, cfg["vocab"], 20).astype(np.int32)

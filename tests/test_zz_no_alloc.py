@@ -44,3 +44,46 @@ def test_noalloc_gemm_equals_gemm(shapes):
         if m * n * k <= 32 * 2048 * 5632:
             assert_bits_equal(host(got), oracle.gemm_i8(a, w), f"call {call} vs oracle")
     rt.close()
+
+
+def test_noalloc_two_handles_concurrently():
+    """Two handles on one GPU calling tl_gemm_i8_noalloc from two host threads
+    at once (ctypes releases the GIL during the call): the calls share the
+    GPU's one scratch array and are put in order, so every result equals
+    tl_gemm_i8's."""
+    import threading
+    import torch
+    rts = [runtime(), runtime()]
+    shapes = [(32, 2048, 5632), (24, 256, 6144)]   # both use the split-K scratch
+    rng = np.random.default_rng(71)
+    ops = []
+    for (m, n, k) in shapes:
+        a, w = _operands(rng, m, n, k)
+        want = empty((m, n), np.int32)
+        rts[0].call("tl_gemm_i8", dev(a), dev(w), m, n, k, want)
+        ops.append((dev(a), dev(w), m, n, k, want))
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(i):
+        da, dw, m, n, k, want = ops[i]
+        got = empty((m, n), np.int32)
+        try:
+            for it in range(40):
+                got.fill_(-1)
+                torch.cuda.synchronize()
+                rts[i].call("tl_gemm_i8_noalloc", da, dw, m, n, k, got)
+                if not torch.equal(got, want):
+                    errors.append(f"handle {i} call {it}")
+                    return
+        except Exception as e:   # noqa: BLE001 -- reported below
+            errors.append(f"handle {i}: {e}")
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    for rt in rts:
+        rt.close()
+    assert errors == []
