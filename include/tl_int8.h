@@ -124,6 +124,24 @@ int32_t tl_rmsnorm_quant(tl_handle *h, const float *x, const float *gamma, int32
  * tinyllama_pkg.sv BANK_SLICE_INT8).  Device pointers. */
 int32_t tl_requant_q16(tl_handle *h, const int32_t *acc, const uint32_t *scale_q16, int32_t n, int32_t active,
                        int32_t lanes_per_scale, int32_t nonnegative_only, int8_t *y);
+/* causal_mask_unit.sv:37-54 (model/export_fpga_vectors.py:1157-1184) on a tile
+ * of INT32 scores [rows][cols] (dev): element (r, c) keeps its score when
+ * r < query_row_count, c < key_col_count and key_pos_base + c <=
+ * query_pos_base + r; the other elements of those rows become MASK_NEG_INF
+ * (-1e9, tinyllama_pkg.sv), rows r >= query_row_count become 0. */
+int32_t tl_causal_mask_i32(tl_handle *h, const int32_t *scores, int32_t rows, int32_t cols, int32_t query_pos_base,
+                           int32_t key_pos_base, int32_t query_row_count, int32_t key_col_count, int32_t *out);
+/* rope_unit.sv:73-127 (model/export_fpga_vectors.py:684-732), the accelerator's
+ * INT8 RoPE: x [rows][n_heads x 64] int8 (dev) at positions pos [rows]
+ * (dev); cos / sin in Q16.16 from the RoPE table (rope_lut_rom.sv, EX:656-681);
+ * out[d] = sat+-127(rne16(x_d cos - x_{d+32} sin)) for d < 32 and
+ * sat+-127(rne16(x_d cos + x_{d-32} sin)) for d >= 32.  Positions outside
+ * the table fail with TL_ERR_BAD_DESCRIPTOR. */
+int32_t tl_rope_q16(tl_handle *h, const int8_t *x, int32_t rows, int32_t n_heads, const int32_t *pos, int8_t *out);
+/* argmax_reduction.sv:47-93 over INT32 logits v [n] (dev; Q16.16 in the
+ * accelerator): the greatest value and, among equal values, the lowest
+ * index (np.argmax, GI:671).  index and value (may be NULL) are host. */
+int32_t tl_argmax_i32(tl_handle *h, const int32_t *v, int32_t n, int32_t *index, int32_t *value);
 /* Decode GEMV + requantize (shared_gemm_engine.sv:126-135 + requantize_unit.sv:39-93):
  * acc[n] = sum_k x[k] W[n][k], y[n] = sat+-127(rne(f32(acc[n]) * m[n])).  acc may be NULL. */
 int32_t tl_gemv_i8_requant(tl_handle *h, const int8_t *x, const int8_t *w, const float *m,

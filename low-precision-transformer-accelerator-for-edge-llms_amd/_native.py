@@ -95,6 +95,9 @@ SIGNATURES = {
     "tl_rmsnorm_quant": (_i32, [_vp, _vp, _vp, _i32, _i32, _vp, _vp, _vp]),
     "tl_gemv_i8_requant": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp]),
     "tl_requant_q16": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp]),
+    "tl_causal_mask_i32": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
+    "tl_rope_q16": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp]),
+    "tl_argmax_i32": (_i32, [_vp, _vp, _i32, _i32p, _i32p]),
     "tl_gemm_i8": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _vp]),
     "tl_gemm_i8_noalloc": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _vp]),
     "tl_gemm_i8_dequant": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp]),

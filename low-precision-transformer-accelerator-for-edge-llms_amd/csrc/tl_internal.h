@@ -250,6 +250,11 @@ hipError_t init_decode_kernels();
 hipError_t init_prefill_kernels();
 hipError_t init_skinny_kernels();
 hipError_t launch_fill_u32(hipStream_t s, unsigned* p, int32_t n, unsigned v);
+hipError_t launch_causal_mask_i32(hipStream_t s, const int32_t* scores, int32_t rows, int32_t cols, int32_t qb,
+                                  int32_t kb, int32_t qrc, int32_t kcc, int32_t* out);
+hipError_t launch_rope_q16(hipStream_t s, const int8_t* x, int32_t rows, int32_t n_heads, const int32_t* pos,
+                           const float* cosb, const float* sinb, int32_t n_pos, int8_t* out);
+hipError_t launch_argmax_i32(hipStream_t s, const int32_t* v, int32_t n, unsigned long long* key);
 hipError_t launch_requant_q16(hipStream_t s, const int32_t* acc, const uint32_t* scale, int32_t n, int32_t active,
                               int32_t lanes_per_scale, int32_t nonnegative_only, int8_t* y);
 

@@ -1353,6 +1353,103 @@ hipError_t launch_requant_q16(hipStream_t s, const int32_t* acc, const uint32_t*
     return hipGetLastError();
 }
 
+// causal_mask_unit.sv:37-54 (EX:1157-1184) over a tile of INT32 scores
+// [rows][cols]: element (r, c) keeps its score when r < query_row_count,
+// c < key_col_count and key_pos_base + c <= query_pos_base + r; other
+// elements of active rows become MASK_NEG_INF, rows past query_row_count 0
+constexpr int32_t kMaskNegInf = -1000000000;   // tinyllama_pkg.sv MASK_NEG_INF
+
+__global__ __launch_bounds__(256) void causal_mask_i32_kernel(const int32_t* __restrict__ s, int64_t total,
+                                                              int32_t cols, int32_t qb, int32_t kb, int32_t qrc,
+                                                              int32_t kcc, int32_t* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    const int32_t r = (int32_t)(i / cols), c = (int32_t)(i % cols);
+    int32_t v = 0;
+    if (r < qrc) {
+        const bool allow = c < kcc && (int64_t)kb + c <= (int64_t)qb + r;
+        v = allow ? s[i] : kMaskNegInf;
+    }
+    out[i] = v;
+}
+
+hipError_t launch_causal_mask_i32(hipStream_t s, const int32_t* scores, int32_t rows, int32_t cols, int32_t qb,
+                                  int32_t kb, int32_t qrc, int32_t kcc, int32_t* out) {
+    const int64_t total = (int64_t)rows * cols;
+    if (total <= 0) return hipSuccess;
+    TL_KLAUNCH(causal_mask_i32_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, scores, total, cols, qb,
+               kb, qrc, kcc, out);
+    return hipGetLastError();
+}
+
+// rope_unit.sv:73-127 (EX:684-732) INT8 RoPE: the Q16.16 cos / sin of the
+// row's position are the float32 table (build_rope_cache) times 2^16 rounded
+// to nearest even, as EX:158-161 forms the ROM; dimension d < 32 gives
+// rne16(x_d c - x_{d+32} s), d >= 32 rne16(x_d c + x_{d-32} s), both
+// saturated to +-127.  Positions outside the table are clamped to it (the
+// operator checks host positions before the launch).
+__global__ __launch_bounds__(256) void rope_q16_kernel(const int8_t* __restrict__ x, int64_t total, int32_t width,
+                                                       const int32_t* __restrict__ pos, const float* __restrict__ cosb,
+                                                       const float* __restrict__ sinb, int32_t n_pos,
+                                                       int8_t* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    const int64_t r = i / width;
+    const int32_t e = (int32_t)(i % width), d = e & (kHeadDim - 1);
+    const int32_t p = min(max(pos[r], 0), n_pos - 1);
+    const int32_t cq = (int32_t)__builtin_rintf(cosb[(int64_t)p * kHeadDim + d] * 65536.0f);
+    const int32_t sq = (int32_t)__builtin_rintf(sinb[(int64_t)p * kHeadDim + d] * 65536.0f);
+    const bool lower = d < kHeadDim / 2;
+    const int32_t curr = x[i], pair = x[lower ? i + kHeadDim / 2 : i - kHeadDim / 2];
+    const long long sum = lower ? (long long)curr * cq - (long long)pair * sq : (long long)curr * cq + (long long)pair * sq;
+    const unsigned long long mag = sum < 0 ? (unsigned long long)(-sum) : (unsigned long long)sum;
+    unsigned long long q = mag >> 16;
+    const unsigned rem = (unsigned)(mag & 0xFFFFull);
+    if (rem > 0x8000u || (rem == 0x8000u && (q & 1ull))) q += 1;
+    long long v = sum < 0 ? -(long long)q : (long long)q;
+    v = v > 127 ? 127 : (v < -127 ? -127 : v);
+    out[i] = (int8_t)v;
+}
+
+hipError_t launch_rope_q16(hipStream_t s, const int8_t* x, int32_t rows, int32_t n_heads, const int32_t* pos,
+                           const float* cosb, const float* sinb, int32_t n_pos, int8_t* out) {
+    const int64_t total = (int64_t)rows * n_heads * kHeadDim;
+    if (total <= 0) return hipSuccess;
+    TL_KLAUNCH(rope_q16_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, x, total, n_heads * kHeadDim,
+               pos, cosb, sinb, n_pos, out);
+    return hipGetLastError();
+}
+
+// argmax_reduction.sv:47-93 over INT32 logits: the greatest value, the lowest
+// index among equal ones.  Each value becomes a 64-bit key (the value's
+// order-preserving bits above, the complemented index below); workgroups
+// fold theirs with one atomicMax into *key (zero before the launch)
+__global__ __launch_bounds__(256) void argmax_i32_kernel(const int32_t* __restrict__ v, int32_t n,
+                                                         unsigned long long* __restrict__ key) {
+    __shared__ unsigned long long wbest[4];
+    unsigned long long best = 0;
+    for (int32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const unsigned u = (unsigned)v[i] ^ 0x80000000u;
+        best = max_u64(best, ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - (unsigned)i));
+    }
+    best = wave_max_u64(best);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) wbest[wave] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned long long b = max_u64(max_u64(wbest[0], wbest[1]), max_u64(wbest[2], wbest[3]));
+        atomicMax(key, b);
+    }
+}
+
+hipError_t launch_argmax_i32(hipStream_t s, const int32_t* v, int32_t n, unsigned long long* key) {
+    if (n <= 0) return hipErrorInvalidValue;
+    TL_KLAUNCH(reset_keys_kernel, dim3(1), dim3(64), 0, s, key, 1);
+    const int grid = std::min(256, (n + 255) / 256);
+    TL_KLAUNCH(argmax_i32_kernel, dim3(grid), dim3(256), 0, s, v, n, key);
+    return hipGetLastError();
+}
+
 // argmax of each logits row (one workgroup per row) into its key slot
 __global__ __launch_bounds__(256) void argmax_rows_kernel(const float* __restrict__ logits, int32_t n,
                                                           unsigned long long* __restrict__ keys) {

@@ -1338,6 +1338,41 @@ int32_t tl_requant_q16(tl_handle* h, const int32_t* acc, const uint32_t* scale_q
     return finish(h);
 }
 
+int32_t tl_causal_mask_i32(tl_handle* h, const int32_t* scores, int32_t rows, int32_t cols, int32_t query_pos_base,
+                           int32_t key_pos_base, int32_t query_row_count, int32_t key_col_count, int32_t* out) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, scores && out && rows >= 0 && cols > 0, "bad causal mask arguments");
+    TL_REQ(h, query_pos_base >= 0 && key_pos_base >= 0 && query_row_count >= 0 && key_col_count >= 0,
+           "negative position or count");
+    TL_LAUNCH(h, launch_causal_mask_i32(h->stream, scores, rows, cols, query_pos_base, key_pos_base, query_row_count,
+                                        key_col_count, out));
+    return finish(h);
+}
+
+int32_t tl_rope_q16(tl_handle* h, const int8_t* x, int32_t rows, int32_t n_heads, const int32_t* pos, int8_t* out) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, x && pos && out && rows >= 0 && n_heads > 0, "bad rope arguments");
+    std::vector<int32_t> hp(rows);
+    if (rows > 0) TL_HIP(h, hipMemcpy(hp.data(), pos, sizeof(int32_t) * rows, hipMemcpyDefault));
+    for (int32_t r = 0; r < rows; r++)
+        TL_REQ(h, hp[r] >= 0 && hp[r] < h->rope_n, "position outside the RoPE table");
+    TL_LAUNCH(h, launch_rope_q16(h->stream, x, rows, n_heads, pos, h->rope_cos, h->rope_sin, h->rope_n, out));
+    return finish(h);
+}
+
+int32_t tl_argmax_i32(tl_handle* h, const int32_t* v, int32_t n, int32_t* index, int32_t* value) {
+    if (!h) return TL_ERR_BAD_DESCRIPTOR;
+    TL_REQ(h, v && index && n > 0, "bad argmax arguments");
+    TL_LAUNCH(h, launch_argmax_i32(h->stream, v, n, h->op_key));
+    unsigned long long key = 0;
+    TL_HIP(h, hipMemcpyAsync(&key, h->op_key, sizeof key, hipMemcpyDeviceToHost, h->stream));
+    int32_t r = finish(h);
+    if (r) return r;
+    *index = (int32_t)(0xFFFFFFFFu - (unsigned)(key & 0xFFFFFFFFull));
+    if (value) *value = (int32_t)((unsigned)(key >> 32) ^ 0x80000000u);
+    return TL_OK;
+}
+
 int32_t tl_gemm_i8(tl_handle* h, const int8_t* a, const int8_t* w, int32_t m, int32_t n, int32_t k, int32_t* c) {
     if (!h) return TL_ERR_BAD_DESCRIPTOR;
     TL_REQ(h, a && w && c && m > 0 && n > 0, "bad gemm arguments");

@@ -18,6 +18,10 @@
 - replay_requant_case / replay_requant_fixture: run an exported
   requantize_unit case (EX:528-653: 512 accumulator lanes, 16 Q16.16
   multipliers) through tl_requant_q16 and compare the INT8 lanes.
+- replay of the element-wise case types: rope_unit (tl_rope_q16),
+  causal_mask_unit (tl_causal_mask_i32), rmsnorm (tl_rmsnorm_quant), softmax
+  (tl_softmax_rows), silu (tl_silu_mul) and argmax (tl_argmax_i32), with the
+  exporter's Q16.16 conversions on the host (EX:152-161, 191-192, 875-927).
 """
 from __future__ import annotations
 
@@ -449,6 +453,165 @@ def replay_requant_fixture(rt: Runtime, fixture_base) -> dict:
     return {"out": out, "match": bool(out.shape == exp.shape and np.array_equal(out, exp))}
 
 
+# ---------------------------------------------------------------------------
+# Q16.16 conversions of the exporter's fixed-point cases, vectorised
+# restatements of EX:152-161, 191-192, 875-927
+# ---------------------------------------------------------------------------
+Q16 = 1 << 16
+MASK_NEG_INF = -1000000000   # tinyllama_pkg.sv (EX:73)
+
+
+def q16_from_float(v) -> np.ndarray:
+    """EX:152-155: round(max(0, v) 2^16) clamped to uint32 (round half to
+    even, as Python's round on a float)."""
+    x = np.rint(np.maximum(np.asarray(v, np.float64), 0.0) * Q16)
+    return np.clip(x, 0, 0xFFFFFFFF).astype(np.uint32)
+
+
+def q16_signed_from_float(v) -> np.ndarray:
+    """EX:158-161: round(v 2^16) clamped to int32."""
+    x = np.rint(np.asarray(v, np.float64) * Q16)
+    return np.clip(x, -(1 << 31), (1 << 31) - 1).astype(np.int32)
+
+
+def float_from_q16(raw) -> np.ndarray:
+    """EX:191-192: float32(raw / 2^16)."""
+    return (np.asarray(raw, np.int64).astype(np.float64) / Q16).astype(np.float32)
+
+
+def quantize_fixed_by_scale_q16(values_q16, scale_q16: int, nonnegative_only: bool = False) -> np.ndarray:
+    """EX:900-927: |v| / scale rounded half to even on the exact integer
+    quotient and remainder, sign restored, clamped to +-127 or [0, 127]."""
+    den = int(scale_q16) if int(scale_q16) != 0 else 1
+    v = np.asarray(values_q16, np.int64)
+    mag = np.abs(v)
+    q, rem = mag // den, mag % den
+    q = q + ((2 * rem > den) | ((2 * rem == den) & (q & 1 == 1))).astype(np.int64)
+    r = np.where(v < 0, -q, q)
+    return np.clip(r, 0 if nonnegative_only else -127, 127).astype(np.int8)
+
+
+def quantize_probability_q16(prob_q16) -> np.ndarray:
+    """EX:875-888: round_half_even(p 127 / 2^16) of Q16.16 probabilities,
+    clamped to [0, 127]."""
+    prod = np.asarray(prob_q16, np.int64) * 127
+    q, rem = prod >> 16, prod & (Q16 - 1)
+    q = q + ((rem > Q16 // 2) | ((rem == Q16 // 2) & (q & 1 == 1))).astype(np.int64)
+    return np.clip(q, 0, 127).astype(np.int8)
+
+
+def _scalar(arrays: dict, key: str) -> float:
+    return np.asarray(arrays[key]).ravel()[0].item()
+
+
+def _fp_close(got, want, rtol: float = 1e-6, atol: float = 1e-9) -> bool:
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    return bool(got.shape == want.shape and np.all(np.abs(got - want) <= atol + rtol * np.abs(want)))
+
+
+# ---------------------------------------------------------------------------
+# replay of the exporter's phase-4/5/6 element-wise case types
+# ---------------------------------------------------------------------------
+def replay_rope_case(rt: Runtime, arrays: dict) -> dict:
+    """rope_unit case (EX:930-1006: q_in / k_in [tokens][64] int8 of one head
+    at positions token_base + t, q_out_expected / k_out_expected) through
+    tl_rope_q16, the accelerator's INT8 RoPE."""
+    from .tinyllama import dev, empty, host
+    base = int(_scalar(arrays, "token_base"))
+    out = {}
+    for name in ("q", "k"):
+        x = np.ascontiguousarray(arrays[f"{name}_in"], np.int8)
+        rows = x.shape[0]
+        pos = np.arange(base, base + rows, dtype=np.int32)
+        y = empty(x.shape, np.int8)
+        rt.call("tl_rope_q16", dev(x), rows, x.shape[1] // 64, dev(pos), y)
+        out[name] = host(y)
+    match = all(np.array_equal(out[n], np.asarray(arrays[f"{n}_out_expected"], np.int8)) for n in ("q", "k"))
+    return {"q_out": out["q"], "k_out": out["k"], "match": bool(match)}
+
+
+def replay_causal_mask_case(rt: Runtime, arrays: dict) -> dict:
+    """causal_mask_unit case (EX:1009-1086: score_in [8][64] int32 with the
+    query / key position bases and active row / column counts) through
+    tl_causal_mask_i32."""
+    from .tinyllama import dev, empty, host
+    s = np.ascontiguousarray(arrays["score_in"], np.int32)
+    out = empty(s.shape, np.int32)
+    rt.call("tl_causal_mask_i32", dev(s), s.shape[0], s.shape[1], int(_scalar(arrays, "query_pos_base")),
+            int(_scalar(arrays, "key_pos_base")), int(_scalar(arrays, "query_row_count")),
+            int(_scalar(arrays, "key_col_count")), out)
+    got = host(out)
+    return {"score_out": got, "match": bool(np.array_equal(got, np.asarray(arrays["score_out_expected"], np.int32)))}
+
+
+def replay_rmsnorm_case(rt: Runtime, arrays: dict) -> dict:
+    """rmsnorm case (EX:1705-1805): the golden RMSNorm of the Q16.16-exact
+    input rows x_deq with the gains rounded through Q16.16 (EX:1722-1724) runs
+    on the device (tl_rmsnorm_quant, TL:45-50 arithmetic); its output goes to
+    Q16.16 and is quantized at the case's output scale as EX:1725-1727 does.
+    Match: y_fp bit for bit and y_q equal."""
+    from .tinyllama import dev, empty, host
+    x = np.ascontiguousarray(arrays["x_deq"], np.float32)
+    rows, n = x.shape
+    gamma = float_from_q16(q16_signed_from_float(np.asarray(arrays["gamma_fp"], np.float32)))
+    y = empty((rows, n), np.float32)
+    q = empty((rows, n), np.int8)
+    sc = empty((rows,), np.float64)
+    rt.call("tl_rmsnorm_quant", dev(x), dev(gamma), rows, n, y, q, sc)
+    y_fp = host(y)
+    y_q = quantize_fixed_by_scale_q16(q16_signed_from_float(y_fp), int(q16_from_float(_scalar(arrays, "output_scale"))))
+    fp_ok = bool(np.array_equal(y_fp.view(np.uint32), np.asarray(arrays["y_fp"], np.float32).view(np.uint32)))
+    q_ok = bool(np.array_equal(y_q, np.asarray(arrays["y_q"], np.int8)))
+    return {"y_fp": y_fp, "y_q": y_q, "match_fp": fp_ok, "match": fp_ok and q_ok}
+
+
+def replay_softmax_case(rt: Runtime, arrays: dict) -> dict:
+    """softmax case (EX:1808-1893): the active rows of score_fp (the masked
+    scores times the Q16.16 score scale) through tl_softmax_rows (TL:100-103
+    arithmetic), then Q16.16 probabilities and their INT8 form (EX:1820-1824).
+    The golden's softmax agrees with the library's within 1e-6 relative, so
+    the float match is to that tolerance; prob_q must be equal."""
+    from .tinyllama import dev, empty, host
+    s = np.ascontiguousarray(arrays["score_fp"], np.float32)
+    rows = int(np.count_nonzero(np.asarray(arrays["prob_fp"], np.float32).any(axis=1)))
+    prob = np.zeros_like(s)
+    if rows:
+        p = empty((rows, s.shape[1]), np.float32)
+        rt.call("tl_softmax_rows", dev(np.ascontiguousarray(s[:rows])), rows, s.shape[1], p)
+        prob[:rows] = host(p)
+    prob_q = quantize_probability_q16(q16_signed_from_float(prob))
+    fp_ok = _fp_close(prob, arrays["prob_fp"])
+    q_ok = bool(np.array_equal(prob_q, np.asarray(arrays["prob_q"], np.int8)))
+    return {"prob_fp": prob, "prob_q": prob_q, "match_fp": fp_ok, "match": fp_ok and q_ok}
+
+
+def replay_silu_case(rt: Runtime, arrays: dict) -> dict:
+    """silu case (EX:1896-1990): SiLU of x_deq through tl_silu_mul (TL:159-161
+    arithmetic), then Q16.16 and the fixed-point quantization at the case's
+    output scale (EX:1905-1907).  Float match within 1e-6 relative (the
+    golden's np.exp), y_q equal."""
+    from .tinyllama import dev, empty, host
+    x = np.ascontiguousarray(arrays["x_deq"], np.float32)
+    y = empty(x.shape, np.float32)
+    rt.call("tl_silu_mul", dev(x), None, int(x.size), y)
+    y_fp = host(y)
+    y_q = quantize_fixed_by_scale_q16(q16_signed_from_float(y_fp), int(q16_from_float(_scalar(arrays, "output_scale"))))
+    fp_ok = _fp_close(y_fp, arrays["y_fp"])
+    q_ok = bool(np.array_equal(y_q, np.asarray(arrays["y_q"], np.int8)))
+    return {"y_fp": y_fp, "y_q": y_q, "match_fp": fp_ok, "match": fp_ok and q_ok}
+
+
+def replay_argmax_case(rt: Runtime, arrays: dict) -> dict:
+    """argmax case (EX:1651-1702: Q16.16 logits of the whole vocabulary)
+    through tl_argmax_i32 (argmax_reduction.sv, lowest id wins a tie)."""
+    from .tinyllama import dev
+    v = np.ascontiguousarray(arrays["logits_q16"], np.int32)
+    idx, val = C.c_int32(), C.c_int32()
+    rt.call("tl_argmax_i32", dev(v), int(v.size), C.byref(idx), C.byref(val))
+    match = idx.value == int(_scalar(arrays, "argmax_expected")) and val.value == int(_scalar(arrays, "logit_expected"))
+    return {"token": idx.value, "logit": val.value, "match": bool(match)}
+
+
 def replay_fixture(rt: Runtime, fixture_base) -> dict:
     """Replay one RTL fixture: a requantize_unit fixture has .acc.memh, a
     shared_gemm_engine fixture .act_steps.memh."""
@@ -458,12 +621,15 @@ def replay_fixture(rt: Runtime, fixture_base) -> dict:
     return replay_gemm_fixture(rt, base)
 
 
-REPLAYERS = {"shared_gemm_engine": replay_gemm_case, "requantize_unit": replay_requant_case}
+REPLAYERS = {"shared_gemm_engine": replay_gemm_case, "requantize_unit": replay_requant_case,
+             "rope_unit": replay_rope_case, "causal_mask_unit": replay_causal_mask_case,
+             "rmsnorm": replay_rmsnorm_case, "softmax": replay_softmax_case, "silu": replay_silu_case,
+             "argmax": replay_argmax_case}
 
 
 def replay_manifest(rt: Runtime, root) -> list[dict]:
-    """Replay every shared_gemm_engine and requantize_unit case a manifest
-    lists; other blocks are reported as not replayed."""
+    """Replay every case a manifest lists whose block has a replayer
+    (REPLAYERS); other blocks are reported as not replayed."""
     root = Path(root)
     results = []
     for entry in read_manifest(root).get("cases", []):

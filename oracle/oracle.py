@@ -89,6 +89,8 @@ def lib() -> C.CDLL:
             "or_apply_rope": (None, [_f32p, C.c_int32, C.c_int32, _f32p, _f32p]),
             "or_argmax_first": (C.c_int32, [_f32p, C.c_int32]),
             "or_argmax_i32_tiles": (C.c_int32, [_i32p, C.c_int32, C.c_int32, _i32p]),
+            "or_causal_mask_tile": (None, [_i32p, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                           C.c_int32, _i32p]),
             "or_attention_row": (None, [C.POINTER(OrConfig), C.c_int32, C.c_int32, _i8p, C.c_double,
                                         _i8p, _i8p, _f32p, _f32p, _f32p, _i32p, _i8p, _i32p]),
             "or_embed": (None, [C.POINTER(OrModel), C.c_int32, _f32p]),

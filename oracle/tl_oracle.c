@@ -42,6 +42,11 @@
  *   or_decode_row                  vs golden mixed_precision_decoder_layer at one
  *                                  token within tolerance
  *   or_lm_head_argmax              argmax_reduction KATs (lower id wins a tie)
+ *   or_argmax_i32_tiles            argmax_reduction KATs; np.argmax on random
+ *                                  INT32 vectors with forced ties
+ *   or_causal_mask_tile            tb_causal_mask_unit KAT (col 0 kept, cols
+ *                                  1-4 masked, inactive row 0); brute-force
+ *                                  restatement of the allow rule
  *   or_decode_rows, or_lm_head_rows  bit-exact vs or_decode_row / or_lm_head_argmax
  *                                  row by row (prompt rows of one sequence and
  *                                  rows of different sequences)
@@ -340,6 +345,20 @@ int32_t or_argmax_i32_tiles(const int32_t *v, int32_t n, int32_t tile, int32_t *
     }
     if (best_val) *best_val = best;
     return best_id;
+}
+
+/* causal_mask_unit.sv:37-54 / EX:1157-1184  one tile of INT32 scores
+ * [rows][cols]: (r, c) keeps its score when r < qrc, c < kcc and
+ * kb + c <= qb + r; the rest of an active row is MASK_NEG_INF (-1e9,
+ * tinyllama_pkg.sv), rows r >= qrc are 0. */
+void or_causal_mask_tile(const int32_t *s, int32_t rows, int32_t cols, int32_t qb, int32_t kb, int32_t qrc,
+                         int32_t kcc, int32_t *out) {
+    for (int32_t r = 0; r < rows; r++)
+        for (int32_t c = 0; c < cols; c++) {
+            const int64_t i = (int64_t)r * cols + c;
+            if (r >= qrc) out[i] = 0;
+            else out[i] = (c < kcc && (int64_t)kb + c <= (int64_t)qb + r) ? s[i] : -1000000000;
+        }
 }
 
 static inline int64_t cache_row(const or_config *c, int32_t layer, int32_t g, int32_t t) {

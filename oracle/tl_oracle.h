@@ -99,6 +99,8 @@ void    or_quantize_probs(const float *p, int32_t n, int8_t *p8);
 void    or_apply_rope(float *v, int32_t n_heads, int32_t hd, const float *cos_p, const float *sin_p);
 int32_t or_argmax_first(const float *v, int32_t n);
 int32_t or_argmax_i32_tiles(const int32_t *v, int32_t n, int32_t tile, int32_t *best_val);
+void    or_causal_mask_tile(const int32_t *s, int32_t rows, int32_t cols, int32_t qb, int32_t kb, int32_t qrc,
+                            int32_t kcc, int32_t *out);
 
 /* ---- attention over the INT8 KV cache ------------------------------------ */
 /* K/V cache of one sequence, logical layout [L][Hkv][max_pos][hd] int8. */

@@ -139,3 +139,52 @@ def test_case_manifest_round_trip(tmp_path):
     man["cases"][1]["path"] = f"sim/{tmp_path.name}/phase3/phase3_x.npz"
     (tmp_path / "manifest.json").write_text(json.dumps(man))
     np.testing.assert_array_equal(gt.load_case(tmp_path, "phase3_x")[1]["act"], a + 1)
+
+
+# ---- Q16.16 conversions of the exporter's fixed-point cases --------------------------
+
+def _rne_div(num: int, den: int) -> int:
+    """num / den rounded half to even, exactly (Fraction arithmetic)."""
+    from fractions import Fraction
+    return round(Fraction(num, den))
+
+
+def test_q16_conversions_match_scalar_definitions():
+    """The vectorised conversions against the scalar arithmetic they restate
+    (EX:152-161, 191-192), element by element, on random values, exact
+    half-LSB ties and the clamping ends."""
+    rng = np.random.default_rng(5)
+    v = np.concatenate([rng.standard_normal(2000) * 10, rng.uniform(-40000, 40000, 500),
+                        (np.arange(-40, 40) + 0.5) / 65536.0, [0.0, -0.0, 1e12, -1e12, 32767.99999]])
+    v32 = v.astype(np.float32)
+    want_s = [max(-(1 << 31), min(int(round(float(x) * 65536.0)), (1 << 31) - 1)) for x in v32]
+    want_u = [max(0, min(int(round(max(0.0, float(x)) * 65536.0)), 0xFFFFFFFF)) for x in v32]
+    assert gt.q16_signed_from_float(v32).tolist() == want_s
+    assert gt.q16_from_float(v32).tolist() == want_u
+    raw = np.concatenate([rng.integers(-(1 << 31), (1 << 31) - 1, 1000), [0, 1, -1, 65536, -(1 << 31)]])
+    got = gt.float_from_q16(raw)
+    assert got.dtype == np.float32
+    assert all(g == np.float32(int(r) / 65536.0) for g, r in zip(got, raw))
+
+
+def test_fixed_point_quantizers_match_exact_rounding():
+    """quantize_fixed_by_scale_q16 (EX:900-927) and quantize_probability_q16
+    (EX:875-888) against exact rational rounding half to even, with ties
+    planted, both clamps and a zero scale (treated as 1)."""
+    rng = np.random.default_rng(6)
+    for den in (1, 2, 3, 65536, 77777, 1234567):
+        vals = rng.integers(-(1 << 28), 1 << 28, 3000).astype(np.int64)
+        ties = (np.arange(-20, 20) * 2 + 1) * den // 2 if den % 2 == 0 else np.arange(-20, 20) * den
+        vals = np.concatenate([vals, ties, [0]])
+        for nonneg in (False, True):
+            got = gt.quantize_fixed_by_scale_q16(vals, den, nonnegative_only=nonneg)
+            lo = 0 if nonneg else -127
+            want = [max(lo, min(127, (-1 if x < 0 else 1) * _rne_div(abs(int(x)), den))) for x in vals]
+            assert got.tolist() == want
+    z = gt.quantize_fixed_by_scale_q16(np.array([5, -5, 130]), 0)
+    assert z.tolist() == [5, -5, 127]
+    p = np.concatenate([rng.integers(-1000, 70000, 5000), [0, 65536, 32768 // 127 * 127]]).astype(np.int64)
+    p = np.concatenate([p, [x for x in range(0, 70000) if (x * 127) % 65536 == 32768][:50]])
+    got = gt.quantize_probability_q16(p)
+    want = [max(0, min(127, _rne_div(int(x) * 127, 65536))) for x in p]
+    assert got.tolist() == want

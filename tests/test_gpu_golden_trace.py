@@ -283,3 +283,149 @@ def test_requant_q16_edges():
             rt.call("tl_requant_q16", dev(acc), dev(scale.view(np.int32)), acc.size, active, 32, nonneg, y)
             assert_bits_equal(host(y), want, f"nonnegative_only={nonneg} active={active}")
     rt.close()
+
+
+# ---- replay of exporter-format element-wise cases (phases 4-6) ----------------------
+
+EX_CFG = dict(oracle.TINYLLAMA_CFG, n_layers=1, vocab=64)
+
+
+def ex_rope_case(rng, base, tokens):
+    """rope_unit (EX:930-1006): one head's INT8 Q and K rows at positions
+    base .. base + tokens - 1, rotated by the oracle's or_rotate_q16 with
+    cos / sin in Q16.16 as EX:656-668 forms the ROM."""
+    cos, sin = oracle.rope_table(2048, 64, 1e4)
+    cq, sq = gt.q16_signed_from_float(cos), gt.q16_signed_from_float(sin)
+    L = oracle.lib()
+    arrays = {}
+    for name in ("q", "k"):
+        x = rng.integers(-127, 128, (tokens, 64)).astype(np.int8)
+        y = np.zeros_like(x)
+        for t in range(tokens):
+            for d in range(64):
+                lower = d < 32
+                pair = x[t, d + 32] if lower else x[t, d - 32]
+                y[t, d] = L.or_rotate_q16(int(x[t, d]), int(pair), int(cq[base + t, d]), int(sq[base + t, d]),
+                                          int(lower))
+        arrays[f"{name}_in"], arrays[f"{name}_out_expected"] = x, y
+    return dict(arrays, token_base=np.asarray([base], np.int32), token_count=np.asarray([tokens], np.int32),
+                q_head_id=np.asarray([3], np.int32), kv_head_id=np.asarray([0], np.int32))
+
+
+def ex_mask_case(rng, qb, kb, qrc, kcc):
+    """causal_mask_unit (EX:1009-1086) on an 8 x 64 INT32 score tile."""
+    s = rng.integers(-(1 << 20), 1 << 20, (8, 64)).astype(np.int32)
+    out = np.empty_like(s)
+    oracle.lib().or_causal_mask_tile(oracle.ptr(s, oracle.C.c_int32), 8, 64, qb, kb, qrc, kcc,
+                                     oracle.ptr(out, oracle.C.c_int32))
+    return dict(score_in=s, score_out_expected=out, query_pos_base=np.asarray([qb], np.int32),
+                key_pos_base=np.asarray([kb], np.int32), query_row_count=np.asarray([qrc], np.int32),
+                key_col_count=np.asarray([kcc], np.int32))
+
+
+def ex_rmsnorm_case(rng, rows):
+    """rmsnorm (EX:1705-1805): per-tensor INT8 input rows, Q16.16-exact input
+    and gains, the oracle's RMSNorm (TL:45-50, NumPy's pairwise mean), output
+    quantized at the Q16.16 output scale."""
+    x_fp = rng.standard_normal((rows, 2048)).astype(np.float32)
+    gamma = rng.uniform(0.8, 1.2, 2048).astype(np.float32)
+    x_q, s_in = oracle.quantize_int8(x_fp)
+    x_deq = gt.float_from_q16(x_q.astype(np.int64) * int(gt.q16_from_float(s_in)))
+    gamma_core = gt.float_from_q16(gt.q16_signed_from_float(gamma))
+    y_fp = oracle.rms_norm(x_deq, gamma_core, EX_CFG["rms_eps"])
+    _, s_out = oracle.quantize_int8(oracle.rms_norm(x_q.astype(np.float32) * np.float32(s_in), gamma,
+                                                    EX_CFG["rms_eps"]))
+    s_out_q16 = int(gt.q16_from_float(s_out))
+    y_q = gt.quantize_fixed_by_scale_q16(gt.q16_signed_from_float(y_fp), s_out_q16)
+    return dict(x_q=x_q, x_deq=x_deq, gamma_fp=gamma, y_fp=y_fp, y_q=y_q,
+                input_scale=np.asarray([s_in], np.float32),
+                output_scale=np.asarray([gt.float_from_q16(s_out_q16)], np.float32))
+
+
+def ex_softmax_case(rng, qrc, kcc, qb):
+    """softmax (EX:1808-1893): masked INT32 scores times the Q16.16 score
+    scale, the oracle's row softmax over the active rows, Q16.16 probabilities
+    and their INT8 form."""
+    raw = rng.integers(-3000, 3000, (8, 64)).astype(np.int32)
+    masked = np.empty_like(raw)
+    oracle.lib().or_causal_mask_tile(oracle.ptr(raw, oracle.C.c_int32), 8, 64, qb, 0, qrc, kcc,
+                                     oracle.ptr(masked, oracle.C.c_int32))
+    scale = 0.004
+    core = np.clip(masked.astype(np.int64) * int(gt.q16_from_float(scale)), -(1 << 31), (1 << 31) - 1)
+    score_fp = gt.float_from_q16(core)
+    prob_fp = np.zeros((8, 64), np.float32)
+    for r in range(qrc):
+        prob_fp[r] = oracle.softmax_row(score_fp[r])
+    prob_q = gt.quantize_probability_q16(gt.q16_signed_from_float(prob_fp))
+    return dict(score_in=masked, score_fp=score_fp, prob_fp=prob_fp, prob_q=prob_q,
+                score_scale=np.asarray([scale], np.float32))
+
+
+def ex_silu_case(rng, rows):
+    """silu (EX:1896-1990): per-tensor INT8 gate values through Q16.16, the
+    oracle's SiLU (TL:159-161), output quantized at its Q16.16 scale."""
+    x_fp = (rng.standard_normal((rows, 32)) * 4).astype(np.float32)
+    x_q, s_in = oracle.quantize_int8(x_fp)
+    x_deq = gt.float_from_q16(x_q.astype(np.int64) * int(gt.q16_from_float(s_in)))
+    y_fp = oracle.silu(x_deq)
+    s_out_q16 = int(gt.q16_from_float(oracle.quantize_int8(y_fp)[1]))
+    y_q = gt.quantize_fixed_by_scale_q16(gt.q16_signed_from_float(y_fp), s_out_q16)
+    return dict(x_q=x_q, x_deq=x_deq, y_fp=y_fp, y_q=y_q, input_scale=np.asarray([s_in], np.float32),
+                output_scale=np.asarray([gt.float_from_q16(s_out_q16)], np.float32))
+
+
+def ex_argmax_case(rng, tie):
+    """argmax (EX:1651-1702): Q16.16 logits of the 32000-entry vocabulary;
+    with `tie`, the maximum is planted at three ids across 128-wide tiles."""
+    logits_fp = (rng.standard_normal(32000) * 3).astype(np.float32)
+    q16 = gt.q16_signed_from_float(logits_fp)
+    if tie:
+        top = int(q16.max()) + 7
+        q16[[31999, 20001, 20000]] = top
+    best = np.asarray([0], np.int32)
+    idx = oracle.lib().or_argmax_i32_tiles(oracle.ptr(q16, oracle.C.c_int32), 32000, 128,
+                                           oracle.ptr(best, oracle.C.c_int32))
+    assert idx == int(np.argmax(q16))
+    return dict(logits_fp=logits_fp, logits_q16=q16, argmax_expected=np.asarray([idx], np.uint32),
+                logit_expected=best)
+
+
+def test_replay_elementwise_cases(tmp_path):
+    """Cases of six more exporter block types, written in the exporter's
+    .npz layout with a manifest (expected values from the oracle), replayed
+    through the library's operators: rope_unit (INT8 RoPE), causal_mask_unit,
+    rmsnorm, softmax, silu and argmax.  Each case matches; a planted error in
+    each type is reported as a mismatch."""
+    rng = np.random.default_rng(2024)
+    cases = [
+        ("phase4_prefill_layer0_rope_q3_kv0_t0", "phase4", "rope_unit", ex_rope_case(rng, 0, 8)),
+        ("phase4_decode_layer0_rope_q3_kv0_t1500", "phase4", "rope_unit", ex_rope_case(rng, 1500, 8)),
+        ("phase4_prefill_layer0_causal_mask_q0_kv0_qb8_kb0", "phase4", "causal_mask_unit",
+         ex_mask_case(rng, 8, 0, 8, 64)),
+        ("phase4_decode_layer0_causal_mask_q0_kv0_qb70_kb64", "phase4", "causal_mask_unit",
+         ex_mask_case(rng, 70, 64, 1, 30)),
+        ("phase5_prefill_layer0_rmsnorm1", "phase5", "rmsnorm", ex_rmsnorm_case(rng, 4)),
+        ("phase5_prefill_layer0_softmax_q0_kv0_qb8_kb0", "phase5", "softmax", ex_softmax_case(rng, 8, 64, 8)),
+        ("phase5_decode_layer0_softmax_q0_kv0_qb5_kb0", "phase5", "softmax", ex_softmax_case(rng, 1, 6, 5)),
+        ("phase5_prefill_layer0_silu_gate_m0", "phase5", "silu", ex_silu_case(rng, 16)),
+        ("phase6_prefill_argmax", "phase6", "argmax", ex_argmax_case(rng, False)),
+        ("phase6_decode_argmax", "phase6", "argmax", ex_argmax_case(rng, True)),
+    ]
+    for cid, phase, block, arrays in cases:
+        gt.write_case(tmp_path, cid, phase, block, arrays)
+    rt = gt.Runtime(EX_CFG)
+    res = gt.replay_manifest(rt, tmp_path)
+    print("replay:", [(r["case_id"], r.get("match")) for r in res], flush=True)
+    assert res == [{"case_id": cid, "replayed": True, "match": True} for cid, _, _, _ in cases]
+    # planted errors: one element of an expected output per block type
+    plants = {"rope_unit": "k_out_expected", "causal_mask_unit": "score_out_expected", "rmsnorm": "y_q",
+              "softmax": "prob_q", "silu": "y_q", "argmax": "argmax_expected"}
+    for cid, phase, block, arrays in cases:
+        bad = dict(arrays)
+        key = plants[block]
+        v = np.array(bad[key], copy=True)
+        flat = v.reshape(-1)
+        flat[-1] = flat[-1] + 1 if block != "rmsnorm" else np.int8(flat[-1] ^ 1)
+        bad[key] = v
+        assert not gt.REPLAYERS[block](rt, bad)["match"], f"planted error in {cid} not reported"
+    rt.close()
