@@ -645,27 +645,37 @@ __global__ __launch_bounds__(256) void attention_row_kernel(AttnDecodeArgs p) {
 }
 
 // Batched decode attention (many rows, long contexts): one workgroup of 16
-// wavefronts per (row, group of HPW query heads sharing a KV head).  Every
-// wavefront issues all of its key and value loads first (T <= 2048: two
-// 64-key blocks and eight 16-key value groups per wavefront), so each phase
-// costs about one memory latency, and the HPW heads share every loaded key
-// and value.  Same arithmetic as attention_row_kernel.
+// wavefronts per (row, group of HPW = 4 query heads sharing a KV head).  The
+// Q.K scores and the P.V sums run on v_mfma_i32_16x16x64_i8 with the four
+// heads as rows 0, 4, 8 and 12 of the 16-row A operand (the other rows zero),
+// so accumulator register 0 of lane l holds head l / 16 at column l % 16: a
+// wavefront keeps every (head, key) value it computes in all 64 lanes, one
+// 16-lane row per head.  Wavefront w owns key blocks b = w + 16 i (64 keys,
+// i < 2): per block four MFMAs of 16 keys for the scores (lane l: keys
+// 16 j + l % 16, j < 4, of head l / 16) and, per 16 output dimensions, one
+// MFMA over the block's 64 keys for P.V.  Every wavefront issues all of its
+// key and value loads first (T <= 2048), so each phase costs about one
+// memory latency.  Same arithmetic as attention_row_kernel: the integer dot
+// products are exact in any order, and the block sums keep the block-64
+// butterfly order (levels 32 and 16 inside a lane's registers, 8, 4, 2, 1
+// across its row).
 constexpr int kGW = 16;                         // wavefronts
-constexpr int kGKB = 2;                         // key blocks per wavefront
-constexpr int kGVG = 8;                         // value groups per wavefront
+constexpr int kGKB = 2;                         // key blocks of 64 per wavefront
 constexpr int kGroupMaxKeys = kGW * kGKB * 64;  // 2048
 
 template <int HPW>
 __global__ __launch_bounds__(kGW * 64) void attention_group_kernel(AttnDecodeArgs p) {
+    static_assert(HPW == 4, "one head per 16-lane row of the MFMA accumulators");
     extern __shared__ __align__(16) float gdyn[];
     __shared__ __align__(16) int8_t qs[HPW][64];
     __shared__ __align__(16) int8_t kn[64];
-    __shared__ int8_t vn[64];
+    __shared__ __align__(16) int8_t vn[64];
     __shared__ float red[kGW];
     __shared__ float wmax[kGW][HPW];
     __shared__ float mh[HPW], toth[HPW];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    const int hl = lane >> 4, cl = lane & 15;   // the lane's head (row of 16 lanes) and column
     const int G = p.n_heads / p.n_kv;
     // workgroups are dispatched to the 8 XCDs round-robin by linear id: the
     // G / HPW workgroups of one (row, KV head), which read the same K and V
@@ -685,47 +695,79 @@ __global__ __launch_bounds__(kGW * 64) void attention_group_kernel(AttnDecodeArg
     const int D = p.n_heads * kHeadDim, KVD = p.n_kv * kHeadDim, W = D + 2 * KVD;
     const int pos = p.rm.pos[row], seq = p.rm.seq[row];
     if (pos < 0 || pos >= p.kv.max_pos) return;   // a row outside the cache (uniform per workgroup)
-    const int T = pos + 1, tpad = (T + 63) & ~63, nblk = tpad >> 6, ngrp = tpad >> 4;
+    const int T = pos + 1, tpad = (T + 63) & ~63, nblk = tpad >> 6;
     const int64_t pl = p.kv.plane(seq, p.layer, g);
     const int8_t* kp = p.kv.k + pl;
     const int8_t* vp = p.kv.v + pl;
     int8_t* p8 = (int8_t*)gdyn;                           // [HPW][tpad]
     float* bsum = (float*)(p8 + HPW * tpad);              // [HPW][nblk]
     int* accs = (int*)(bsum + HPW * nblk);                // [kGW][HPW][64]
-    const float* src = p.qkv + (int64_t)row * W;
-    const int32_t* srci = p.qacc + (int64_t)row * W;
     const bool sums = p.qacc != nullptr;   // uniform
     const double qsx = sums ? p.qas[row] : 0.0;
-    auto qkv_at = [&](int i) -> float { return sums ? (float)srci[i] * deq_mult(qsx, p.qws[i]) : src[i]; };
+    // one load path for both forms, so that no load waits on another: the
+    // row's 32-bit words (integer sums, or the float values' bits) and, for
+    // sums, the column multipliers (for floats a second copy of the row,
+    // unused)
+    const int32_t* srcw = sums ? p.qacc + (int64_t)row * W : (const int32_t*)(p.qkv + (int64_t)row * W);
+    const float* srcm = sums ? p.qws : p.qkv + (int64_t)row * W;
+    auto qkv_val = [&](int32_t wv, float m) -> float {
+        return sums ? (float)wv * deq_mult(qsx, m) : __int_as_float(wv);
+    };
     const int d = lane;
 
-    // 0) loads in the order they are needed (loads complete in issue order):
-    //    the Q row, this group's Q heads and the row's own K and V, the RoPE
-    //    factors, then this wavefront's cached key blocks and value groups
-    //    (indices clamped inside the plane; rows 0..pos-1 are final, surplus
-    //    copies unused)
+    // 0) loads in the order they are needed (loads complete in issue order),
+    //    all issued before any is used: the Q row, this group's Q heads and the
+    //    row's own K and V (every wavefront loads them, unconditionally), the
+    //    RoPE factors, then this wavefront's key operands (blocks clamped
+    //    inside the plane; rows 0..pos-1 are final, surplus copies unused):
+    //    key operand j of block b: keys 64 b + 16 j + l % 16, dimensions
+    //    16 (l / 16) .. +16 (K plane: dimension group l / 16 of the block).
+    //    A wavefront's 16 KB of key and value loads stall its instruction
+    //    issue while the CU drains them, so the value operands (dimension
+    //    16 j + l % 16 of keys 64 b + 16 (l / 16) .. +16, V plane group
+    //    4 b + l / 16) are requested later, one block before the scores and
+    //    one before the probabilities, where their issue delays less:
+    //    measured per workgroup at 2048 keys, 13.4 us with every load at the
+    //    start, 11.9 with all value loads before the scores, 11.4 split
     constexpr int kQPer = 4;   // Q elements per thread: D <= 4 x 1024
-    float qv[kQPer];
+    int32_t qw[kQPer + 3];
+    float qm[kQPer + 3];
 #pragma unroll
-    for (int j = 0; j < kQPer; j++) qv[j] = qkv_at(min(tid + kGW * 64 * j, D - 1));
-    float qh = 0.0f, kx = 0.0f, vx = 0.0f;
-    if (wave < HPW) qh = qkv_at((h0 + wave) * kHeadDim + d);
-    if (wave == HPW) {
-        kx = qkv_at(D + g * kHeadDim + d);
-        vx = qkv_at(D + KVD + g * kHeadDim + d);
+    for (int j = 0; j < kQPer; j++) {
+        const int i = min(tid + kGW * 64 * j, D - 1);
+        qw[j] = srcw[i];
+        qm[j] = srcm[i];
+    }
+    {
+        const int iq = (h0 + min(wave, HPW - 1)) * kHeadDim + d, ik = D + g * kHeadDim + d, iv = ik + KVD;
+        qw[kQPer] = srcw[iq];
+        qm[kQPer] = srcm[iq];
+        qw[kQPer + 1] = srcw[ik];
+        qm[kQPer + 1] = srcm[ik];
+        qw[kQPer + 2] = srcw[iv];
+        qm[kQPer + 2] = srcm[iv];
     }
     const float cs = p.cosb[(int64_t)pos * kHeadDim + d];
     const float sn = p.sinb[(int64_t)pos * kHeadDim + d];
-    v4i kreg[kGKB][4], vreg[kGVG];
+    v4i kreg[kGKB][4], vreg[kGKB][4];
 #pragma unroll
     for (int i = 0; i < kGKB; i++) {
         const int b = min(wave + kGW * i, nblk - 1);
 #pragma unroll
-        for (int q = 0; q < 4; q++) kreg[i][q] = ld16(kp + (int64_t)b * 4096 + q * 1024 + lane * 16);
+        for (int j = 0; j < 4; j++) kreg[i][j] = ld16(kp + (int64_t)b * 4096 + hl * 1024 + (16 * j + cl) * 16);
     }
+    auto v_load = [&](int i) {
+        const int b = min(wave + kGW * i, nblk - 1);
 #pragma unroll
-    for (int i = 0; i < kGVG; i++) vreg[i] = ld16(vp + (int64_t)min(wave + kGW * i, ngrp - 1) * 1024 + lane * 16);
+        for (int j = 0; j < 4; j++) vreg[i][j] = ld16(vp + (int64_t)(4 * b + hl) * 1024 + (16 * j + cl) * 16);
+    };
     __builtin_amdgcn_sched_barrier(0);
+    float qv[kQPer];
+#pragma unroll
+    for (int j = 0; j < kQPer; j++) qv[j] = qkv_val(qw[j], qm[j]);
+    const float qh = qkv_val(qw[kQPer], qm[kQPer]);
+    const float kx = qkv_val(qw[kQPer + 1], qm[kQPer + 1]);
+    const float vx = qkv_val(qw[kQPer + 2], qm[kQPer + 2]);
 
     // 1) RoPE of every Q element of the row -> the row's scale; this group's
     //    rotated Q and the row's K (RoPE, static scale) and V
@@ -762,44 +804,37 @@ __global__ __launch_bounds__(kGW * 64) void attention_group_kernel(AttnDecodeArg
     const float scl = (float)((s_q * (double)sk) * p.attn_scale);
     __syncthreads();
 
-    // 2) scores (lane <-> key) of this wavefront's blocks for the HPW heads;
-    //    each lane keeps its keys' scores, then exponentials, in registers
-    //    (key t = 64 (wave + kGW i) + lane in every phase)
-    float se[kGKB][HPW];
-    float lmax[HPW];
-#pragma unroll
-    for (int h = 0; h < HPW; h++) lmax[h] = -INFINITY;
+    // 2) scores: A = rotated Q (row 4 h = head h, dimensions 16 (l / 16) ..
+    //    +16 from lane l), B = the key operands, the row's own key in place of
+    //    the cache's at key pos
+    v_load(0);
+    const v4i vzero = {0, 0, 0, 0};
+    const v4i qrow = *(const v4i*)&qs[cl >> 2][16 * hl];
+    const v4i qa = (cl & 3) == 0 ? qrow : vzero;
+    const v4i kown = *(const v4i*)&kn[16 * hl];
+    float se[kGKB][4];
+    float lmax = -INFINITY;
 #pragma unroll
     for (int i = 0; i < kGKB; i++) {
         const int b = wave + kGW * i;
-        const int t = b * 64 + lane;
-        if (b < nblk && t < T) {
-            v4i k0 = kreg[i][0], k1 = kreg[i][1], k2 = kreg[i][2], k3 = kreg[i][3];
-            if (t == pos) {
-                const v4i* kn4 = (const v4i*)kn;
-                k0 = kn4[0];
-                k1 = kn4[1];
-                k2 = kn4[2];
-                k3 = kn4[3];
-            }
+        if (b < nblk) {
 #pragma unroll
-            for (int h = 0; h < HPW; h++) {
-                const v4i* q4 = (const v4i*)qs[h];
-                int S = sdot4v(k0, q4[0], 0);
-                S = sdot4v(k1, q4[1], S);
-                S = sdot4v(k2, q4[2], S);
-                S = sdot4v(k3, q4[3], S);
-                const float sc = (float)S * scl;
-                se[i][h] = sc;
-                lmax[h] = fmaxf(lmax[h], sc);
+            for (int j = 0; j < 4; j++) {
+                const int t = b * 64 + 16 * j + cl;
+                const v4i kb = t == pos ? kown : kreg[i][j];
+                const v4i c = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa, kb, vzero, 0, 0, 0);
+                const float sc = (float)c[0] * scl;
+                se[i][j] = sc;
+                if (t < T) lmax = fmaxf(lmax, sc);
             }
         }
     }
-#pragma unroll
-    for (int h = 0; h < HPW; h++) {
-        const float m = wave_max_f32(lmax[h]);
-        if (lane == 0) wmax[wave][h] = m;
-    }
+    // the head's maximum over the row's 16 lanes
+    lmax = fmaxf(lmax, __int_as_float(dpp<kDppXor1>(__float_as_int(lmax))));
+    lmax = fmaxf(lmax, __int_as_float(dpp<kDppXor2>(__float_as_int(lmax))));
+    lmax = fmaxf(lmax, __int_as_float(dpp<kDppHalfMirror>(__float_as_int(lmax))));
+    lmax = fmaxf(lmax, __int_as_float(dpp<kDppRowMirror>(__float_as_int(lmax))));
+    if (cl == 0) wmax[wave][hl] = lmax;
     __syncthreads();
     if (tid < HPW) {
         float m = wmax[0][tid];
@@ -808,23 +843,26 @@ __global__ __launch_bounds__(kGW * 64) void attention_group_kernel(AttnDecodeArg
     }
     __syncthreads();
 
-    // 3) exponentials and block-64 butterfly sums, then each head's total
-    //    (block sums added in key order)
+    // 3) exponentials and block-64 butterfly sums: key 16 j + c of a block
+    //    meets 16 (j ^ 2) + c (level 32), then 16 (j ^ 1) + c (level 16) in
+    //    this lane's registers, then lanes c ^ 8, 4, 2, 1 of its row
+    const float mhh = mh[hl];
 #pragma unroll
     for (int i = 0; i < kGKB; i++) {
         const int b = wave + kGW * i;
         if (b < nblk) {
-            const int t = b * 64 + lane;
 #pragma unroll
-            for (int h = 0; h < HPW; h++) {
-                float e = 0.0f;
-                if (t < T) {   // x - max <= 0: tl_expf_nonpos is tl_expf there
-                    e = tl_expf_nonpos(se[i][h] - mh[h]);
-                    se[i][h] = e;
-                }
-                const float bs = wave_butterfly_sum(e);
-                if (lane == 0) bsum[h * nblk + b] = bs;
+            for (int j = 0; j < 4; j++) {
+                const int t = b * 64 + 16 * j + cl;
+                // x - max <= 0: tl_expf_nonpos is tl_expf there
+                se[i][j] = t < T ? tl_expf_nonpos(se[i][j] - mhh) : 0.0f;
             }
+            float s = (se[i][0] + se[i][2]) + (se[i][1] + se[i][3]);
+            s = s + lane_xor<8>(s);
+            s = s + lane_xor<4>(s);
+            s = s + lane_xor<2>(s);
+            s = s + lane_xor<1>(s);
+            if (cl == 0) bsum[hl * nblk + b] = s;
         }
     }
     __syncthreads();
@@ -834,33 +872,30 @@ __global__ __launch_bounds__(kGW * 64) void attention_group_kernel(AttnDecodeArg
     __syncthreads();
 
     // 4) INT8 probabilities (zero past the last key): exponential / total
-    //    correctly rounded from each head's reciprocal and two residual
+    //    correctly rounded from the head's reciprocal and two residual
     //    corrections (e <= 1 <= total keeps e y finite).  A float sum of
     //    nonnegative terms is never below any of them, so e <= total and
     //    rne(127 e / total) lies in [0, 127]: the probability clip needs no
     //    clamp.
-    RnDiv dt[HPW];
+    v_load(1);
     bool fast = true;
 #pragma unroll
-    for (int h = 0; h < HPW; h++) {
-        dt[h] = rn_div_prep(toth[h]);
-        fast = fast && dt[h].fast;
-    }
+    for (int h = 0; h < HPW; h++) fast = fast && rn_div_prep(toth[h]).fast;
+    RnDiv dt;
+    dt.b = toth[hl];
+    dt.y = __fdiv_rn(1.0f, dt.b);
+    dt.fast = fast;
     auto probs = [&](auto fst) {
 #pragma unroll
         for (int i = 0; i < kGKB; i++) {
             const int b = wave + kGW * i;
             if (b < nblk) {
-                const int t = b * 64 + lane;
 #pragma unroll
-                for (int h = 0; h < HPW; h++) {
-                    int8_t pq = 0;
-                    if (t < T) {
-                        const float e = se[i][h];
-                        const float q = decltype(fst)::value ? rn_div_fast(e, dt[h]) : __fdiv_rn(e, dt[h].b);
-                        pq = (int8_t)(int)__builtin_rintf(q * 127.0f);
-                    }
-                    p8[h * tpad + t] = pq;
+                for (int j = 0; j < 4; j++) {
+                    const int t = b * 64 + 16 * j + cl;
+                    const float e = se[i][j];
+                    const float q = decltype(fst)::value ? rn_div_fast(e, dt) : __fdiv_rn(e, dt.b);
+                    p8[hl * tpad + t] = t < T ? (int8_t)(int)__builtin_rintf(q * 127.0f) : (int8_t)0;
                 }
             }
         }
@@ -869,30 +904,36 @@ __global__ __launch_bounds__(kGW * 64) void attention_group_kernel(AttnDecodeArg
     else probs(std::false_type{});
     __syncthreads();
 
-    // 5) P . V (lane <-> dimension) over this wavefront's value groups; the
-    //    row's own V comes from vn
-    int o[HPW];
+    // 5) P . V: A = the probabilities (row 4 h = head h, keys 64 b + 16 (l / 16)
+    //    .. +16 from lane l), B = the value operands, the row's own V byte in
+    //    place of the cache's at key pos; accumulator j, register 0 of lane l:
+    //    head l / 16, dimension 16 j + l % 16
+    v4i oacc[4];
 #pragma unroll
-    for (int h = 0; h < HPW; h++) o[h] = 0;
-    const int cpos = pos >> 4, bpos = pos & 15;
+    for (int j = 0; j < 4; j++) oacc[j] = vzero;
+    const int gpos = pos >> 4, bq = (pos & 15) >> 2, bsh = (pos & 3) * 8;
 #pragma unroll
-    for (int i = 0; i < kGVG; i++) {
-        const int c = wave + kGW * i;
-        if (c < ngrp) {
-            v4i vv = vreg[i];
-            if (c == cpos) {
-                const unsigned nb = (uint8_t)vn[d];
-                const int sh = (bpos & 3) * 8;
-                const unsigned keep = ~(0xFFu << sh);
-                const int q = bpos >> 2;
-                vv[q] = (int)(((unsigned)vv[q] & keep) | (nb << sh));
+    for (int i = 0; i < kGKB; i++) {
+        const int b = wave + kGW * i;
+        if (b < nblk) {
+            const v4i prow = *(const v4i*)(p8 + (cl >> 2) * tpad + b * 64 + 16 * hl);
+            const v4i pa = (cl & 3) == 0 ? prow : vzero;
+            const bool own = 4 * b + hl == gpos;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                v4i vv = vreg[i][j];
+                const unsigned nb = (uint8_t)vn[16 * j + cl];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const unsigned rep = ((unsigned)vv[q] & ~(0xFFu << bsh)) | (nb << bsh);
+                    vv[q] = own && q == bq ? (int)rep : vv[q];
+                }
+                oacc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, vv, oacc[j], 0, 0, 0);
             }
-#pragma unroll
-            for (int h = 0; h < HPW; h++) o[h] = sdot4v(vv, *(const v4i*)(p8 + h * tpad + c * 16), o[h]);
         }
     }
 #pragma unroll
-    for (int h = 0; h < HPW; h++) accs[(wave * HPW + h) * 64 + lane] = o[h];
+    for (int j = 0; j < 4; j++) accs[(wave * HPW + hl) * 64 + 16 * j + cl] = oacc[j][0];
     __syncthreads();
     if (tid < HPW * 64) {   // wavefront h: head h0 + h
         const int h = tid >> 6, dd = tid & 63;
