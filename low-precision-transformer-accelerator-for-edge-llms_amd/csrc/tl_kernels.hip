@@ -101,7 +101,13 @@ __global__ __launch_bounds__(kNT) void rows_prologue_kernel(const float* __restr
     __shared__ __align__(16) float part[PRO == PRO_RMSNORM ? 8 * 64 : 4];
     __shared__ float red[16];
     __shared__ double xscale;
-    const int tid = threadIdx.x, row = blockIdx.x;
+    const int tid = threadIdx.x;
+    // packed rows: workgroups go to the 8 XCDs round-robin by id, so workgroup
+    // w takes row (w % 8) (rows / 8) + w / 8 and each XCD writes whole 32-row
+    // blocks, whose 16-byte pieces (adjacent for consecutive rows) then meet
+    // in that XCD's L2
+    const int nr = (int)gridDim.x;
+    const int row = pk && nr % 8 == 0 ? (int)(blockIdx.x % 8) * (nr / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
     const float4* xr = (const float4*)(x + (int64_t)row * n);
     const int kq = n / 4 - 1;
     float4 xv[KCH], gv[KCH];
