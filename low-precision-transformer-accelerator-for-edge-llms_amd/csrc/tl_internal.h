@@ -122,17 +122,31 @@ struct GemmArgs {
     double* as_out;
 };
 
+// Weight tiles to bring into L2 ahead of the GEMM that reads them, by extra
+// workgroups of a row kernel launched before it.  Workgroups go to the 8 XCDs
+// round-robin by linear id, and the GEMMs that take a prefetch place the
+// workgroups of column tile t on XCD t % 8 (their grids have a multiple of 8
+// column tiles in x), so the workgroups added on XCD x load tiles x, x + 8,
+// ... of every matrix: the GEMM then reads them from its own XCD's L2.
+struct L2Prefetch {
+    const int8_t* w[2];    // the packed weight copies (nmat), or w[0] null: none
+    int32_t nmat;
+    int32_t ntiles;        // column tiles, a multiple of 8
+    int64_t tile_bytes;    // contiguous bytes of one tile (all of its K blocks), a multiple of 16
+    int32_t* sink;         // a word the loads' combined value is written to, never in practice
+};
+
 // ---- launchers (tl_kernels.hip) ------------------------------------------
 // packed: q is written in the packed GEMM operand layout (launch_gemm_pk)
 // instead of row-major; needs n % 64 == 0 and n <= 6144 (else invalid value)
 hipError_t launch_rmsnorm_quant(hipStream_t s, const float* x, const float* g, int32_t rows,
                                 int32_t n, float eps, PwPlan plan, float* y, int8_t* q,
-                                double* scales, bool packed = false);
+                                double* scales, bool packed = false, const L2Prefetch* pf = nullptr);
 // zero: optional [rows][zero_n] int32 buffer (zero_n % 4 == 0, 16-byte
 // aligned) each row's workgroup clears after quantizing
 hipError_t launch_quantize_rows(hipStream_t s, const float* x, int32_t rows, int32_t n,
                                 int8_t* q, double* scales, int32_t* zero = nullptr, int32_t zero_n = 0,
-                                bool packed = false);
+                                bool packed = false, const L2Prefetch* pf = nullptr);
 
 // RMSNorm row prologue that first finishes a K-sliced small-M GEMM with a
 // residual epilogue: its integer sums acc (EPI_ACC, rows x n) are dequantized
@@ -153,6 +167,7 @@ struct FoldArgs {
     double* scales;       // [rows]
     int32_t* zero;        // or null: [rows][zero_n] int32 the kernel also clears (consumed integer sums)
     int32_t zero_n;
+    L2Prefetch pf;        // the next GEMM's weight tiles (pf.w[0] null: none)
 };
 hipError_t launch_rows_fold(hipStream_t s, const FoldArgs& f);
 hipError_t launch_quantize_tensor(hipStream_t s, const float* x, int64_t n, int8_t* q,

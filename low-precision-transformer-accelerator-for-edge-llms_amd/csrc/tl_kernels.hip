@@ -91,23 +91,65 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const float* __restr
 // ((p % 2) 32 + r % 32) 16).  With `zero`, the workgroup also clears zero_n
 // int32 of its row of that buffer (integer sums that the kernels before it
 // have consumed, zero again for the next K-sliced GEMM).
+// the weight tiles of XCD xcd, split in 64 KB units over the nslots
+// prefetching workgroups of that XCD (slot = this one's index): plain loads,
+// a whole unit (sixteen 16-byte loads per thread) in flight at once, so the
+// lines are kept in L2
+TL_DEV void l2_prefetch(const L2Prefetch& pf, int xcd, int slot, int nslots) {
+    constexpr int kU = 16;
+    constexpr int64_t kUnit = 65536;
+    const int nch = (int)((pf.tile_bytes + kUnit - 1) / kUnit);
+    const int units = (pf.ntiles >> 3) * pf.nmat * nch;
+    v4i acc = {0, 0, 0, 0};
+    for (int u = slot; u < units; u += nslots) {
+        const int c = u % nch, mt = u / nch, m = mt % pf.nmat, i = mt / pf.nmat;
+        const int64_t off = (int64_t)c * kUnit;
+        const int nv = (int)(min(kUnit, pf.tile_bytes - off) >> 4);
+        const v4i* src = (const v4i*)(pf.w[m] + (int64_t)(xcd + 8 * i) * pf.tile_bytes + off);
+        for (int o = threadIdx.x; o < nv; o += kU * kNT) {
+            v4i r[kU];
+#pragma unroll
+            for (int j = 0; j < kU; j++) r[j] = src[min(o + j * kNT, nv - 1)];
+#pragma unroll
+            for (int j = 0; j < kU; j++) acc ^= r[j];
+        }
+    }
+    if ((acc[0] ^ acc[1] ^ acc[2] ^ acc[3]) == 0x5EED1E55) *pf.sink = 1;
+}
+
+// prefetching workgroups per XCD for a plan (0: none): one per 64 KB unit of
+// the XCD's tiles, at most 28 (with a row kernel's 32 workgroups, 256 in all)
+static int l2_prefetch_slots(const L2Prefetch* pf) {
+    if (!pf || !pf->w[0] || pf->ntiles <= 0 || pf->ntiles % 8 || pf->nmat < 1 || pf->nmat > 2 ||
+        (pf->nmat == 2 && !pf->w[1]) || !pf->sink || pf->tile_bytes <= 0 || pf->tile_bytes % 16)
+        return 0;
+    const int64_t units = (int64_t)(pf->ntiles / 8) * pf->nmat * ((pf->tile_bytes + 65535) / 65536);
+    return (int)std::min<int64_t>(28, units);
+}
+
 template <int PRO, int KCH>
 __global__ __launch_bounds__(kNT) void rows_prologue_kernel(const float* __restrict__ x, const float* __restrict__ g,
                                                            int32_t n, float eps, PwPlan plan, int8_t* __restrict__ q,
                                                            double* __restrict__ scales, int32_t* __restrict__ zero,
-                                                           int32_t zero_n, int32_t pk) {
+                                                           int32_t zero_n, int32_t pk, int32_t rows, L2Prefetch pf) {
     __shared__ __align__(16) int8_t xs8[KCH * 1024];
     __shared__ __align__(16) float sq[PRO == PRO_RMSNORM ? KCH * 1024 : 4];
     __shared__ __align__(16) float part[PRO == PRO_RMSNORM ? 8 * 64 : 4];
     __shared__ float red[16];
     __shared__ double xscale;
     const int tid = threadIdx.x;
+    // workgroups past the rows (from the next multiple of 8) prefetch
+    const int rows8 = (rows + 7) & ~7;
+    if ((int)blockIdx.x >= rows) {
+        if ((int)blockIdx.x >= rows8)
+            l2_prefetch(pf, (int)(blockIdx.x - rows8) % 8, (int)(blockIdx.x - rows8) / 8, ((int)gridDim.x - rows8) / 8);
+        return;
+    }
     // packed rows: workgroups go to the 8 XCDs round-robin by id, so workgroup
     // w takes row (w % 8) (rows / 8) + w / 8 and each XCD writes whole 32-row
     // blocks, whose 16-byte pieces (adjacent for consecutive rows) then meet
     // in that XCD's L2
-    const int nr = (int)gridDim.x;
-    const int row = pk && nr % 8 == 0 ? (int)(blockIdx.x % 8) * (nr / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+    const int row = pk && rows % 8 == 0 ? (int)(blockIdx.x % 8) * (rows / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
     const float4* xr = (const float4*)(x + (int64_t)row * n);
     const int kq = n / 4 - 1;
     float4 xv[KCH], gv[KCH];
@@ -135,10 +177,12 @@ __global__ __launch_bounds__(kNT) void rows_prologue_kernel(const float* __restr
 template <int PRO>
 static hipError_t launch_rows_prologue(hipStream_t s, const float* x, const float* g, int32_t rows, int32_t n,
                                        float eps, PwPlan plan, int8_t* q, double* scales, int32_t* zero = nullptr,
-                                       int32_t zero_n = 0, bool packed = false) {
-    const dim3 grid(rows), block(kNT);
+                                       int32_t zero_n = 0, bool packed = false, const L2Prefetch* pfp = nullptr) {
+    const int slots = l2_prefetch_slots(pfp);
+    const L2Prefetch pf = slots ? *pfp : L2Prefetch{};
+    const dim3 grid(slots ? ((rows + 7) & ~7) + 8 * slots : rows), block(kNT);
     const int32_t pk = packed ? 1 : 0;
-#define TL_RPL(C) TL_KLAUNCH((rows_prologue_kernel<PRO, C>), grid, block, 0, s, x, g, n, eps, plan, q, scales, zero, zero_n, pk)
+#define TL_RPL(C) TL_KLAUNCH((rows_prologue_kernel<PRO, C>), grid, block, 0, s, x, g, n, eps, plan, q, scales, zero, zero_n, pk, rows, pf)
     switch ((n + 1023) / 1024) {
         case 1: TL_RPL(1); break;
         case 2: TL_RPL(2); break;
@@ -164,6 +208,12 @@ __global__ __launch_bounds__(kNT) void rows_fold_kernel(FoldArgs f) {
     __shared__ float red[16];
     __shared__ double xscale;
     const int tid = threadIdx.x, row = blockIdx.x, n = f.n;
+    // workgroups past the rows (from the next multiple of 8) prefetch
+    const int rows8 = (f.rows + 7) & ~7;
+    if (row >= f.rows) {
+        if (row >= rows8) l2_prefetch(f.pf, (row - rows8) % 8, (row - rows8) / 8, ((int)gridDim.x - rows8) / 8);
+        return;
+    }
     const int kq = n / 4 - 1;
     const int64_t ro = (int64_t)row * n;
     // f.as[row] may be the buffer this workgroup's scale is written to: every
@@ -208,14 +258,17 @@ hipError_t launch_rows_fold(hipStream_t s, const FoldArgs& f) {
         !f.scales || f.plan.n_leaves > 64)
         return hipErrorInvalidValue;
     if (f.zero && (f.zero_n <= 0 || f.zero_n % 4 || (uintptr_t)f.zero % 16)) return hipErrorInvalidValue;
-    const dim3 grid(f.rows), block(kNT);
+    const int slots = l2_prefetch_slots(&f.pf);
+    FoldArgs fa = f;
+    if (!slots) fa.pf = L2Prefetch{};
+    const dim3 grid(slots ? ((f.rows + 7) & ~7) + 8 * slots : f.rows), block(kNT);
     switch ((f.n + 1023) / 1024) {
-        case 1: TL_KLAUNCH(rows_fold_kernel<1>, grid, block, 0, s, f); break;
-        case 2: TL_KLAUNCH(rows_fold_kernel<2>, grid, block, 0, s, f); break;
-        case 3: TL_KLAUNCH(rows_fold_kernel<3>, grid, block, 0, s, f); break;
-        case 4: TL_KLAUNCH(rows_fold_kernel<4>, grid, block, 0, s, f); break;
-        case 5: TL_KLAUNCH(rows_fold_kernel<5>, grid, block, 0, s, f); break;
-        case 6: TL_KLAUNCH(rows_fold_kernel<6>, grid, block, 0, s, f); break;
+        case 1: TL_KLAUNCH(rows_fold_kernel<1>, grid, block, 0, s, fa); break;
+        case 2: TL_KLAUNCH(rows_fold_kernel<2>, grid, block, 0, s, fa); break;
+        case 3: TL_KLAUNCH(rows_fold_kernel<3>, grid, block, 0, s, fa); break;
+        case 4: TL_KLAUNCH(rows_fold_kernel<4>, grid, block, 0, s, fa); break;
+        case 5: TL_KLAUNCH(rows_fold_kernel<5>, grid, block, 0, s, fa); break;
+        case 6: TL_KLAUNCH(rows_fold_kernel<6>, grid, block, 0, s, fa); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -1569,10 +1622,10 @@ static inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b)
 
 hipError_t launch_rmsnorm_quant(hipStream_t s, const float* x, const float* g, int32_t rows,
                                 int32_t n, float eps, PwPlan plan, float* y, int8_t* q,
-                                double* scales, bool packed) {
+                                double* scales, bool packed, const L2Prefetch* pf) {
     if (rows <= 0) return hipSuccess;
     if (!y && plan.n_leaves <= 64 && rows_fast_ok(x, g, q, n))
-        return launch_rows_prologue<PRO_RMSNORM>(s, x, g, rows, n, eps, plan, q, scales, nullptr, 0, packed);
+        return launch_rows_prologue<PRO_RMSNORM>(s, x, g, rows, n, eps, plan, q, scales, nullptr, 0, packed, pf);
     if (packed) return hipErrorInvalidValue;
     const size_t lds = sizeof(float) * ((size_t)2 * n + 10 * (size_t)plan.n_leaves + 16);
     TL_KLAUNCH(rmsnorm_quant_kernel, dim3(rows), dim3(256), lds, s, x, g, n, eps, plan, y, q, scales);
@@ -1580,13 +1633,13 @@ hipError_t launch_rmsnorm_quant(hipStream_t s, const float* x, const float* g, i
 }
 
 hipError_t launch_quantize_rows(hipStream_t s, const float* x, int32_t rows, int32_t n, int8_t* q,
-                                double* scales, int32_t* zero, int32_t zero_n, bool packed) {
+                                double* scales, int32_t* zero, int32_t zero_n, bool packed, const L2Prefetch* pf) {
     if (rows <= 0) return hipSuccess;
     if ((zero || packed) && !rows_fast_ok(x, nullptr, q, n)) return hipErrorInvalidValue;
     if (zero && (zero_n <= 0 || zero_n % 4 || (uintptr_t)zero % 16)) return hipErrorInvalidValue;
     if (rows_fast_ok(x, nullptr, q, n))
         return launch_rows_prologue<PRO_QUANT>(s, x, nullptr, rows, n, 0.0f, PwPlan{8, 1}, q, scales, zero, zero_n,
-                                               packed);
+                                               packed, pf);
     TL_KLAUNCH(quantize_rows_kernel<false>, dim3(rows), dim3(256), 0, s, x, n, q, (void*)scales);
     return hipGetLastError();
 }

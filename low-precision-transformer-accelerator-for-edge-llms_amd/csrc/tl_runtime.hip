@@ -120,6 +120,7 @@ struct tl_handle {
     float* rope_sin = nullptr;
     int32_t rope_n = 0;
     float* att_max = nullptr;   // [max rows][n_heads]: each head's max |attention output| (batched decode)
+    int32_t* pf_sink = nullptr; // written by the L2 prefetch workgroups only if their loads XOR to a magic value
     float* kv_sk = nullptr;
     float* kv_sv = nullptr;
     KvGeom kv{};
@@ -645,11 +646,13 @@ static bool prefill_packed(const tl_handle* h, const LayerDev& L, int32_t rows) 
 // RMSNorm + quantization of the rows of h->x into h->a8 / h->as (in the packed
 // GEMM operand layout with pk), first adding a pending down projection's sums
 // from h->racc (launch_rows_fold)
-static int32_t rows_rmsnorm(tl_handle* h, int32_t rows, const float* g, bool pk = false) {
+static int32_t rows_rmsnorm(tl_handle* h, int32_t rows, const float* g, bool pk = false,
+                            const L2Prefetch* pf = nullptr) {
     if (h->racc_res_ws) {
         FoldArgs f{};
         f.x = h->x; f.acc = h->racc; f.as = h->as; f.ws = h->racc_res_ws; f.g = g;
         f.rows = rows; f.n = h->D; f.eps = h->cfg.rms_eps; f.plan = h->plan; f.q = h->a8; f.scales = h->as;
+        if (pf) f.pf = *pf;
         h->racc_res_ws = nullptr;
         {
             Prof p(h, TL_K_NORM, (double)rows * h->D * 13.0);
@@ -660,7 +663,7 @@ static int32_t rows_rmsnorm(tl_handle* h, int32_t rows, const float* g, bool pk 
     }
     Prof p(h, TL_K_NORM, (double)rows * h->D * 9.0);
     TL_LAUNCH(h, launch_rmsnorm_quant(h->stream, h->x, g, rows, h->D, h->cfg.rms_eps, h->plan, nullptr, h->a8, h->as,
-                                      pk));
+                                      pk, pf));
     return TL_OK;
 }
 
@@ -685,9 +688,30 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
     // epilogue, rotated Q in h->qkv ([rows][D]) quantized by the attention tiles
     const bool fq = pk && h->rows_one_seq && h->rows_pos0 + rows <= kTileMaxKeys && D % 64 == 0 &&
                     KVD % 64 == 0;
+    // The row kernel before a GEMM also brings that GEMM's packed weight tiles
+    // into the L2 of the XCD whose workgroups read them: the packed GEMMs'
+    // grids have a multiple of 8 column tiles in x, so column tile t runs on
+    // XCD t % 8 (batched decode: 32-column tiles; prefill: 64-column tiles,
+    // gate/up's 32).  Batched decode prefetches for Q|K|V, gate/up and down
+    // (O follows attention, not a row kernel); prefill for all four.
+    auto pf_plan = [&](const int8_t* w0, const int8_t* w1, int nmat, int cols, int n, int k) {
+        L2Prefetch p{};
+        p.w[0] = w0;
+        p.w[1] = w1;
+        p.nmat = nmat;
+        p.ntiles = n / cols;
+        p.tile_bytes = (int64_t)cols * k;
+        p.sink = h->pf_sink;
+        return p;
+    };
+    const bool l2pf = ks || pk;
+    const int tc = pk ? 64 : 32;
+    const L2Prefetch pf_qkv = pf_plan(L.wqkv_p, nullptr, 1, tc, QKV, D), pf_o = pf_plan(L.wo_p, nullptr, 1, tc, D, D),
+                     pf_glu = pf_plan(L.wg_p, L.wu_p, 2, 32, F, D), pf_down = pf_plan(L.wd_p, nullptr, 1, tc, D, F);
+    const L2Prefetch* pfq = l2pf && (ks || fq) ? &pf_qkv : nullptr;   // prefill: the RoPE-epilogue tiles
     int32_t r;
     if (!ks && (r = discard_pending_sums(h))) return r;
-    if ((r = rows_rmsnorm(h, rows, L.g_in, pk))) return r;
+    if ((r = rows_rmsnorm(h, rows, L.g_in, pk, pfq))) return r;
     if (qks) {
         // Q|K|V (K = D) K-sliced over the chip: the attention kernel
         // dequantizes the integer sums it reads from h->qacc
@@ -740,6 +764,7 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
         f.x = h->x; f.acc = h->racc; f.as = h->as; f.ws = L.so; f.g = L.g_post;
         f.rows = rows; f.n = D; f.eps = c.rms_eps; f.plan = h->plan; f.q = h->a8; f.scales = h->as;
         f.zero = h->qacc; f.zero_n = QKV;
+        if (l2pf) f.pf = pf_glu;
         {
             Prof p(h, TL_K_NORM, (double)rows * D * 13.0 + (double)rows * QKV * 4.0);
             TL_LAUNCH(h, launch_rows_fold(h->stream, f));
@@ -753,7 +778,8 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
             int32_t* zero = qks ? h->qacc : (fq ? (int32_t*)h->qmax : nullptr);
             Prof p(h, TL_K_NORM, (double)rows * D * 5.0 + (qks ? (double)rows * QKV * 4.0 : 0.0));
             TL_LAUNCH(h, launch_quantize_rows(h->stream, h->att, rows, D, h->a8, h->as, zero,
-                                              qks ? QKV : (fq ? kQmaxStride : 0), pk));
+                                              qks ? QKV : (fq ? kQmaxStride : 0), pk,
+                                              l2pf && pk ? &pf_o : nullptr));
             if (qks) h->qacc_clean = true;
             if (fq) h->qmax_clean = true;
         }
@@ -762,14 +788,15 @@ int32_t layer_rows(tl_handle* h, int32_t layer, int32_t rows, int32_t max_t, boo
             return r;
         Prof p(h, TL_K_NORM, (double)rows * D * 9.0);
         TL_LAUNCH(h, launch_rmsnorm_quant(h->stream, h->x, L.g_post, rows, D, c.rms_eps, h->plan, nullptr, h->a8, h->as,
-                                          pk));
+                                          pk, l2pf ? &pf_glu : nullptr));
     }
     if ((r = linear(h, EPI_GLU, rows, h->a8, h->as, L.wg, L.sg, L.wu, L.su, F, D, nullptr, h->hid, TL_K_GLU, L.wg_p,
                     L.wu_p, pk)))
         return r;
     {
         Prof p(h, TL_K_NORM, (double)rows * F * 5.0);
-        TL_LAUNCH(h, launch_quantize_rows(h->stream, h->hid, rows, F, h->a8, h->as, nullptr, 0, pk));
+        TL_LAUNCH(h, launch_quantize_rows(h->stream, h->hid, rows, F, h->a8, h->as, nullptr, 0, pk,
+                                          l2pf ? &pf_down : nullptr));
     }
     if (ks) {
         // the down GEMM (K = F) K-sliced over the chip: its integer sums wait
@@ -1050,6 +1077,7 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
         (e = dalloc(h, &h->stopped, (size_t)max_seqs)) ||
         (e = dalloc(h, &h->racc, h->racc_cap = (size_t)std::min(32, max_seqs) * D)) ||
         (e = dalloc(h, &h->qacc, h->qacc_cap = (size_t)std::min(32, max_seqs) * h->QKV)) ||
+        (e = dalloc(h, &h->pf_sink, 1)) ||
         (e = dalloc(h, &h->qmax, (size_t)kQmaxStride * R)) ||
         (e = dalloc(h, &h->tokens_out, (size_t)max_seqs * c.max_pos)) ||
         (e = dalloc(h, &h->logit_out, (size_t)max_seqs * c.max_pos)) ||
