@@ -304,7 +304,7 @@ struct Prof {
 
 void harvest_profile(tl_handle* h) {
     if (h->prof_pending.empty()) return;
-    hipStreamSynchronize(h->stream);
+    (void)hipStreamSynchronize(h->stream);   // a failed step shows as failed elapsed-time reads below
     for (auto& p : h->prof_pending) {
         float ms = 0.0f;
         if (hipEventElapsedTime(&ms, p.start, p.stop) == hipSuccess) {
@@ -362,7 +362,7 @@ int32_t finish(tl_handle* h) {
 int32_t ensure_partials(tl_handle* h, size_t need) {
     if (need <= h->partial_cap) return TL_OK;
     if (h->partials) {
-        hipFree(h->partials);
+        (void)hipFree(h->partials);
         h->allocs.erase(std::remove(h->allocs.begin(), h->allocs.end(), (void*)h->partials), h->allocs.end());
         h->partials = nullptr;
     }
@@ -943,14 +943,14 @@ int32_t decode_graph_launch(tl_handle* h, int32_t seq) {
         hipGraph_t cap = nullptr;
         hipError_t e = hipStreamEndCapture(h->stream, &cap);
         if (r) {
-            if (cap) hipGraphDestroy(cap);
+            if (cap) (void)hipGraphDestroy(cap);
             return r;
         }
         TL_HIP(h, e);
         g = cap;
         hipGraphExec_t ex = nullptr;
         e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
-        hipGraphDestroy(g);
+        (void)hipGraphDestroy(g);
         TL_HIP(h, e);
         h->graphs[seq] = ex;
     }
@@ -984,13 +984,13 @@ int32_t batch_graph_launch(tl_handle* h, int32_t n_seqs) {
         hipGraph_t cap = nullptr;
         hipError_t e = hipStreamEndCapture(h->stream, &cap);
         if (r) {
-            if (cap) hipGraphDestroy(cap);
+            if (cap) (void)hipGraphDestroy(cap);
             return r;
         }
         TL_HIP(h, e);
         hipGraphExec_t ex = nullptr;
         e = hipGraphInstantiate(&ex, cap, nullptr, nullptr, 0);
-        hipGraphDestroy(cap);
+        (void)hipGraphDestroy(cap);
         TL_HIP(h, e);
         h->batch_graphs[n_seqs] = ex;
     }
@@ -1036,7 +1036,7 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
     int ndev = 0;
     if (hipGetDeviceCount(&ndev) != hipSuccess || ndev < 1) return fail(nullptr, TL_ERR_INTERNAL, "no HIP device");
     int dev = 0;
-    hipGetDevice(&dev);
+    if (hipGetDevice(&dev) != hipSuccess) return fail(nullptr, TL_ERR_INTERNAL, "hipGetDevice failed");
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return fail(nullptr, TL_ERR_INTERNAL, "hipGetDeviceProperties failed");
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
@@ -1147,21 +1147,21 @@ int32_t tl_create(const tl_config* cfg, int32_t max_seqs, tl_handle** out) {
 
 void tl_destroy(tl_handle* h) {
     if (!h) return;
-    if (h->stream) hipStreamSynchronize(h->stream);
+    if (h->stream) (void)hipStreamSynchronize(h->stream);
     for (auto& p : h->prof_pending) {
-        hipEventDestroy(p.start);
-        hipEventDestroy(p.stop);
+        (void)hipEventDestroy(p.start);
+        (void)hipEventDestroy(p.stop);
     }
-    for (auto e : h->event_pool) hipEventDestroy(e);
+    for (auto e : h->event_pool) (void)hipEventDestroy(e);
     for (auto g : h->graphs)
-        if (g) hipGraphExecDestroy(g);
+        if (g) (void)hipGraphExecDestroy(g);
     for (auto g : h->batch_graphs)
-        if (g) hipGraphExecDestroy(g);
-    for (void* p : h->allocs) hipFree(p);
+        if (g) (void)hipGraphExecDestroy(g);
+    for (void* p : h->allocs) (void)hipFree(p);
     for (auto e : h->watch_ev)
-        if (e) hipEventDestroy(e);
-    if (h->ctl_host) hipHostFree(h->ctl_host);
-    if (h->stream) hipStreamDestroy(h->stream);
+        if (e) (void)hipEventDestroy(e);
+    if (h->ctl_host) (void)hipHostFree(h->ctl_host);
+    if (h->stream) (void)hipStreamDestroy(h->stream);
     delete h;
 }
 
@@ -1859,8 +1859,8 @@ struct CaptureScratch {
     std::vector<void*> ptrs;
     explicit CaptureScratch(hipStream_t s) : stream(s) {}
     ~CaptureScratch() {
-        hipStreamSynchronize(stream);
-        for (void* p : ptrs) hipFree(p);
+        (void)hipStreamSynchronize(stream);
+        for (void* p : ptrs) (void)hipFree(p);
     }
     template <class T>
     T* get(size_t n) {
@@ -2054,16 +2054,16 @@ int32_t tl_decode_timeline(tl_handle* h, int32_t seq, int32_t n_steps, tl_timeli
     }
     h->ts_on = false;
     if (r || e != hipSuccess) {
-        if (graph) hipGraphDestroy(graph);
+        if (graph) (void)hipGraphDestroy(graph);
         return r ? r : fail(h, TL_ERR_INTERNAL, std::string("timeline capture: ") + hipGetErrorString(e));
     }
     if (h->ts_overflow) {
-        hipGraphDestroy(graph);
+        (void)hipGraphDestroy(graph);
         return fail(h, TL_ERR_INTERNAL, "timeline stamp buffer too small");
     }
     hipGraphExec_t exec = nullptr;
     e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-    hipGraphDestroy(graph);
+    (void)hipGraphDestroy(graph);
     TL_HIP(h, e);
     std::vector<unsigned long long> st(h->ts_used);
     *out = tl_timeline{};
@@ -2102,7 +2102,7 @@ int32_t tl_decode_timeline(tl_handle* h, int32_t seq, int32_t n_steps, tl_timeli
         out->kernels = kernels;
         out->step_us += (double)(last - first) * us_per_tick;
     }
-    hipGraphExecDestroy(exec);
+    (void)hipGraphExecDestroy(exec);
     // the steps that ran are ordinary decode steps
     h->host_cursor[seq] += done;
     h->host_ngen[seq] += done;
