@@ -316,6 +316,22 @@ def forward(token_ids: list[int], weights: "TinyLlamaWeights", cos: np.ndarray, 
 # ---------------------------------------------------------------------------
 # TL:198-267: the weight archive
 # ---------------------------------------------------------------------------
+# the archive's geometry keys (``meta_<name>``, TL:205-217) and how each
+# becomes a cfg value
+_META_SCHEMA = (
+    ("model_id", lambda v: str(np.asarray(v).item())),
+    ("hidden_size", int),
+    ("intermediate_size", int),
+    ("num_hidden_layers", int),
+    ("num_attention_heads", int),
+    ("num_key_value_heads", int),
+    ("head_dim", int),
+    ("vocab_size", int),
+    ("max_position_embeddings", int),
+    ("rms_norm_eps", float),
+    ("rope_theta", float),
+)
+
 class TinyLlamaWeights:
     """The reference's weight archive: ``meta_*`` geometry keys,
     ``embed_w`` [V][D], ``final_norm_w``, ``lm_head_w`` [D][V] and per layer
@@ -336,20 +352,7 @@ class TinyLlamaWeights:
         self.compute_dtype = compute_dtype
         self.cache_arrays = cache_arrays
         self._cache: dict = {}
-        d = self.data
-        self.cfg = {
-            "model_id": str(np.asarray(d["meta_model_id"]).item()),
-            "hidden_size": int(d["meta_hidden_size"]),
-            "intermediate_size": int(d["meta_intermediate_size"]),
-            "num_hidden_layers": int(d["meta_num_hidden_layers"]),
-            "num_attention_heads": int(d["meta_num_attention_heads"]),
-            "num_key_value_heads": int(d["meta_num_key_value_heads"]),
-            "head_dim": int(d["meta_head_dim"]),
-            "vocab_size": int(d["meta_vocab_size"]),
-            "max_position_embeddings": int(d["meta_max_position_embeddings"]),
-            "rms_norm_eps": float(d["meta_rms_norm_eps"]),
-            "rope_theta": float(d["meta_rope_theta"]),
-        }
+        self.cfg = {name: conv(self.data["meta_" + name]) for name, conv in _META_SCHEMA}
         self.cfg["num_key_value_groups"] = self.cfg["num_attention_heads"] // self.cfg["num_key_value_heads"]
         self.cfg["attn_scale"] = 1.0 / np.sqrt(self.cfg["head_dim"])
 
@@ -361,13 +364,13 @@ class TinyLlamaWeights:
         return self.data.files
 
     def _array(self, key: str) -> np.ndarray:
-        if self.cache_arrays and key in self._cache:
-            return self._cache[key]
-        arr = self.data[key]
-        if arr.dtype != self.compute_dtype:
-            arr = arr.astype(self.compute_dtype, copy=False)
-        if self.cache_arrays:
-            self._cache[key] = arr
+        """Archive entry ``key`` in compute_dtype (no copy when it already is),
+        memoised per key when cache_arrays is set."""
+        arr = self._cache.get(key)
+        if arr is None:
+            arr = self.data[key].astype(self.compute_dtype, copy=False)
+            if self.cache_arrays:
+                self._cache[key] = arr
         return arr
 
     def _optional_array(self, key: str):
