@@ -125,3 +125,15 @@ def test_capture_layout_matches_header(tmp_path):
     want = [getattr(_native.TlCapture, f).offset for f in fields] + [ctypes.sizeof(_native.TlCapture),
                                                                      _native.CAPTURE_TOPK]
     assert got == want
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures the single-GPU hot path: --gpus N > 1 exits non-zero
+    with a message saying so, before touching any device."""
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], cwd=root,
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode != 0
+    assert "one GPU" in (r.stdout + r.stderr)
