@@ -58,6 +58,31 @@ def test_decode_layer_tinyllama_shape(layer_model):
     eng.close()
 
 
+@pytest.mark.parametrize("pos", [0, 63, 64, 127, 128, 511, 512, 2047])
+def test_decode_layer_positions(layer_model, pos):
+    """One TinyLlama-shape decode layer with `pos` cached rows (the new row at
+    position pos): an empty cache, both sides of a 64-key block edge, both
+    sides of the 512 keys the batch-1 attention keeps in registers, and the
+    last position of a 2048-row cache.  The layer output and every K/V row
+    equal the oracle bit for bit."""
+    m = layer_model
+    assert pos < m.cfg["max_pos"]
+    eng = engine_for(m)
+    orc = oracle.Oracle(m)
+    kc, vc = m.new_cache()
+    if pos:
+        fill_cache_random(eng, m, 0, pos, seed=100 + pos, kc=kc, vc=vc)
+    x = np.random.default_rng(pos).standard_normal(2048).astype(F32)
+    xd = dev(x)
+    eng.decode_layer(xd, layer=0, pos=pos)
+    assert_bits_equal(host(xd), orc.decode_row(0, pos, x, kc, vc), f"layer output at position {pos}")
+    for g in range(4):
+        k, v = eng.kv_read(0, 0, g, 0, pos + 1)
+        assert_bits_equal(k, kc[0, g, :pos + 1], f"K cache head {g}")
+        assert_bits_equal(v, vc[0, g, :pos + 1], f"V cache head {g}")
+    eng.close()
+
+
 def test_decode_sharp_softmax_matches_oracle():
     """Decode attention with K/V scales of 1-3 (scores spread over hundreds,
     so most exponentials fall past the cut-off at -80): the batch-1 decode
