@@ -462,6 +462,33 @@ def test_prefill_lengths_tinyllama_shape(n):
     eng.close()
 
 
+@pytest.mark.parametrize("n", [1000, 2048])
+def test_prefill_long_tinyllama_shape(n):
+    """Prefills past the 512 keys of the register-resident attention tiles
+    (the general attention_tile_kernel, quantizing the float Q that the fused
+    Q|K|V epilogue leaves), up to the 2048-position limit, on a 2-layer
+    TinyLlama-shape model: next token, its logit and every K/V row equal the
+    oracle's layer-major prefill (on up to 16 host threads) bit for bit."""
+    import os
+    cfg = dict(oracle.TINYLLAMA_CFG, n_layers=2, vocab=4096)
+    m = oracle.synthetic_model(cfg, seed=70 + n)
+    prompt = np.random.default_rng(n).integers(0, cfg["vocab"], n).astype(np.int32)
+    eng = engine_for(m)
+    tok, lg = eng.prefill(prompt)
+    oracle.lib().or_set_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
+    orc = oracle.Oracle(m)
+    kc, vc = m.new_cache()
+    want_tok, want_lg = orc.prefill(prompt, (kc, vc))
+    assert tok == want_tok
+    assert F32(lg).view(np.uint32) == F32(want_lg).view(np.uint32)
+    for layer in range(cfg["n_layers"]):
+        for g in range(cfg["n_kv_heads"]):
+            k, v = eng.kv_read(0, layer, g, 0, n)
+            assert_bits_equal(k, kc[layer, g, :n], f"K layer {layer} head {g}")
+            assert_bits_equal(v, vc[layer, g, :n], f"V layer {layer} head {g}")
+    eng.close()
+
+
 @pytest.mark.parametrize("geom", [(1024, 3072, 16, 4), (512, 1536, 8, 2), (384, 1280, 6, 2)],
                          ids=["hidden1024", "hidden512", "hidden384_row_major"])
 def test_prefill_other_geometry(geom):
