@@ -1053,7 +1053,8 @@ hipError_t launch_attention_decode(hipStream_t s, const float* qkv, int32_t rows
     if (n_heads % n_kv || G > kMaxGroupHeads || n_heads > 32 * 4) return hipErrorInvalidValue;
     const int D = n_heads * kHeadDim, W = D + 2 * n_kv * kHeadDim;
     const int tpad = (max_t + 63) & ~63;
-    AttnDecodeArgs p{qkv, n_heads, n_kv, rm, cos, sin, kv, layer, kv_sk, kv_sv, 1.0 / sqrt((double)kHeadDim), out, ts};
+    AttnDecodeArgs p{qkv, n_heads, n_kv, rm, cos, sin, kv, layer, kv_sk, kv_sv, 1.0 / sqrt((double)kHeadDim), out, ts,
+                     nullptr, nullptr, nullptr, nullptr};
     const bool grouped = attention_decode_grouped(rows, n_heads, n_kv, max_t);
     if (out_max && !grouped) return hipErrorInvalidValue;
     p.out_max = out_max;
