@@ -489,6 +489,32 @@ def test_prefill_long_tinyllama_shape(n):
     eng.close()
 
 
+@pytest.mark.parametrize("pos0,rows", [(300, 100), (1000, 64), (1900, 148)])
+def test_layer_rows_after_cached_rows(pos0, rows):
+    """tl_layer_rows over `rows` tokens of a sequence that already holds pos0
+    cached rows (the prefill path of a continuation: packed GEMMs, the fused
+    Q|K|V epilogue, attention tiles that start mid-context): the layer output
+    rows and every K/V row equal the oracle's layer-major rows at positions
+    pos0 .. pos0 + rows - 1, bit for bit."""
+    cfg = dict(oracle.TINYLLAMA_CFG, n_layers=1, vocab=64)
+    m = oracle.synthetic_model(cfg, seed=500 + pos0)
+    eng = engine_for(m)
+    orc = oracle.Oracle(m)
+    kc, vc = m.new_cache()
+    fill_cache_random(eng, m, 0, pos0, seed=pos0, kc=kc, vc=vc)
+    x = np.random.default_rng(rows).standard_normal((rows, cfg["hidden"])).astype(F32)
+    xd = dev(x)
+    eng.rt.call("tl_layer_rows", 0, 0, pos0, rows, xd)
+    want = orc.decode_rows(0, np.arange(pos0, pos0 + rows, dtype=np.int32), x.copy(), [(kc, vc)] * rows)
+    assert_bits_equal(host(xd), want, "layer output rows")
+    n = pos0 + rows
+    for g in range(cfg["n_kv_heads"]):
+        k, v = eng.kv_read(0, 0, g, 0, n)
+        assert_bits_equal(k, kc[0, g, :n], f"K head {g}")
+        assert_bits_equal(v, vc[0, g, :n], f"V head {g}")
+    eng.close()
+
+
 @pytest.mark.parametrize("geom", [(1024, 3072, 16, 4), (512, 1536, 8, 2), (384, 1280, 6, 2)],
                          ids=["hidden1024", "hidden512", "hidden384_row_major"])
 def test_prefill_other_geometry(geom):
