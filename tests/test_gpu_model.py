@@ -368,6 +368,48 @@ def test_decode_batch_tinyllama_heads(kslice, qkv_kslice, o_fuse, monkeypatch):
     eng.close()
 
 
+@pytest.mark.parametrize("B", [2, 17, 31])
+def test_decode_batch_sizes_tinyllama_heads(B):
+    """Batched decode at batch sizes 2, 17 and 31 (the M <= 32 GEMMs at row
+    counts other than 32, the grouped attention's workgroup order at other
+    grid sizes) with TinyLlama's geometry and ragged cache lengths: every id
+    and every K/V row equals the oracle's (layer-major over the batch's rows,
+    on up to 16 host threads)."""
+    import os
+    cfg = dict(oracle.TINYLLAMA_CFG, n_layers=2, vocab=512)
+    m = oracle.synthetic_model(cfg, seed=900 + B)
+    steps = 2
+    eng = engine_for(m, max_seqs=B)
+    rng = np.random.default_rng(B)
+    start = rng.integers(1, 1500, B).astype(np.int32)
+    toks = rng.integers(0, cfg["vocab"], B).astype(np.int32)
+    caches = []
+    for b in range(B):
+        kc, vc = m.new_cache()
+        fill_cache_random(eng, m, b, int(start[b]), seed=1000 + b, kc=kc, vc=vc)
+        caches.append((kc, vc))
+    got = eng.decode_batch(toks, start, steps)
+    oracle.lib().or_set_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
+    orc = oracle.Oracle(m)
+    tok = toks
+    for s in range(steps):
+        x = np.stack([orc.embed(int(t)) for t in tok]).astype(F32)
+        for layer in range(cfg["n_layers"]):
+            orc.decode_rows(layer, start + s, x, caches)
+        want, _ = orc.lm_head_rows(x)
+        assert_bits_equal(np.asarray(got[:, s], np.int32), want, f"ids of step {s}")
+        tok = want
+    for b in range(B):
+        kc, vc = caches[b]
+        n = int(start[b]) + steps
+        for layer in range(cfg["n_layers"]):
+            for g in range(cfg["n_kv_heads"]):
+                k, v = eng.kv_read(b, layer, g, 0, n)
+                assert_bits_equal(k, kc[layer, g, :n], f"K seq {b} layer {layer} head {g}")
+                assert_bits_equal(v, vc[layer, g, :n], f"V seq {b} layer {layer} head {g}")
+    eng.close()
+
+
 def test_decode_timeline_steps_are_decode_steps(small_model):
     """tl_decode_timeline runs ordinary greedy steps from a graph captured
     with clock stamps: decoding on afterwards gives the tokens plain decode
