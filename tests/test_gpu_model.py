@@ -410,6 +410,36 @@ def test_decode_batch_sizes_tinyllama_heads(B):
     eng.close()
 
 
+def test_prefill_then_batched_decode():
+    """Three prompts of 37, 128 and 300 tokens prefilled one sequence at a
+    time (tl_prefill), then continued together by tl_decode_batch from each
+    prompt's predicted token: the ids are the oracle's greedy generation over
+    each prompt and the K/V rows of prompt and generated tokens the oracle's."""
+    import os
+    cfg = dict(oracle.TINYLLAMA_CFG, n_layers=2, vocab=1024)
+    m = oracle.synthetic_model(cfg, seed=77)
+    lens, steps = [37, 128, 300], 4
+    eng = engine_for(m, max_seqs=len(lens))
+    rng = np.random.default_rng(7)
+    prompts = [rng.integers(0, cfg["vocab"], n).astype(np.int32) for n in lens]
+    first = [eng.prefill(p, seq=b)[0] for b, p in enumerate(prompts)]
+    got = eng.decode_batch(np.array(first, np.int32), np.array(lens, np.int32), steps)
+    oracle.lib().or_set_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
+    orc = oracle.Oracle(m)
+    for b, p in enumerate(prompts):
+        kc, vc = m.new_cache()
+        want = orc.generate_layer_major(p, steps + 1, cache=(kc, vc))
+        assert first[b] == want[0], f"seq {b}: prefill token"
+        assert_bits_equal(np.asarray(got[b], np.int32), want[1:], f"seq {b}: batched ids")
+        n = lens[b] + steps
+        for layer in range(cfg["n_layers"]):
+            for g in range(cfg["n_kv_heads"]):
+                k, v = eng.kv_read(b, layer, g, 0, n)
+                assert_bits_equal(k, kc[layer, g, :n], f"K seq {b} layer {layer} head {g}")
+                assert_bits_equal(v, vc[layer, g, :n], f"V seq {b} layer {layer} head {g}")
+    eng.close()
+
+
 def test_decode_timeline_steps_are_decode_steps(small_model):
     """tl_decode_timeline runs ordinary greedy steps from a graph captured
     with clock stamps: decoding on afterwards gives the tokens plain decode
