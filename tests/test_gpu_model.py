@@ -412,9 +412,11 @@ def test_decode_batch_sizes_tinyllama_heads(B):
 
 def test_prefill_then_batched_decode():
     """Three prompts of 37, 128 and 300 tokens prefilled one sequence at a
-    time (tl_prefill), then continued together by tl_decode_batch from each
-    prompt's predicted token: the ids are the oracle's greedy generation over
-    each prompt and the K/V rows of prompt and generated tokens the oracle's."""
+    time (tl_prefill), continued together by tl_decode_batch from each
+    prompt's predicted token, and the second sequence then alone by tl_decode
+    (batch-1 graph replay from the batch's last token): the ids are the
+    oracle's greedy generation over each prompt and the K/V rows of prompt and
+    generated tokens the oracle's."""
     import os
     cfg = dict(oracle.TINYLLAMA_CFG, n_layers=2, vocab=1024)
     m = oracle.synthetic_model(cfg, seed=77)
@@ -424,14 +426,20 @@ def test_prefill_then_batched_decode():
     prompts = [rng.integers(0, cfg["vocab"], n).astype(np.int32) for n in lens]
     first = [eng.prefill(p, seq=b)[0] for b, p in enumerate(prompts)]
     got = eng.decode_batch(np.array(first, np.int32), np.array(lens, np.int32), steps)
+    more = 5
+    alone, stop = eng.decode(more, seq=1)
+    assert stop == "max_tokens"
     oracle.lib().or_set_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
     orc = oracle.Oracle(m)
     for b, p in enumerate(prompts):
         kc, vc = m.new_cache()
-        want = orc.generate_layer_major(p, steps + 1, cache=(kc, vc))
+        extra = more if b == 1 else 0
+        want = orc.generate_layer_major(p, steps + 1 + extra, cache=(kc, vc))
         assert first[b] == want[0], f"seq {b}: prefill token"
-        assert_bits_equal(np.asarray(got[b], np.int32), want[1:], f"seq {b}: batched ids")
-        n = lens[b] + steps
+        assert_bits_equal(np.asarray(got[b], np.int32), want[1:steps + 1], f"seq {b}: batched ids")
+        if extra:
+            assert_bits_equal(np.asarray(alone, np.int32), want[steps + 1:], f"seq {b}: batch-1 ids after the batch")
+        n = lens[b] + steps + extra
         for layer in range(cfg["n_layers"]):
             for g in range(cfg["n_kv_heads"]):
                 k, v = eng.kv_read(b, layer, g, 0, n)
