@@ -659,7 +659,8 @@ def test_generate_tinyllama_shape_matches_oracle():
 @pytest.mark.parametrize("shape,pos0,rows,sharp", [
     ("tinyllama", 0, 1, False), ("tinyllama", 0, 77, False), ("tinyllama", 130, 64, False),
     ("tinyllama", 1900, 100, False), ("small", 5, 33, False), ("small", 0, 256, False),
-    ("small", 96, 160, False), ("tinyllama", 0, 512, True), ("small", 96, 160, True)])
+    ("small", 96, 160, False), ("tinyllama", 0, 512, True), ("small", 96, 160, True),
+    ("tinyllama", 1000, 200, True)])
 def test_attention_rows_match_oracle(shape, pos0, rows, sharp):
     """tl_attention over rows at positions pos0 .. pos0 + rows - 1 of one
     sequence (the prefill path: INT8 MFMA tiles of 32 rows, partial last
